@@ -1,0 +1,181 @@
+/*
+ * qlin.h -- C ABI of the MI355X (gfx950) quantized-linear library, libqlin.so.
+ *
+ * The library replaces the quantized GEMM/GEMV path of the Qwen3.5 prompt-enhancer
+ * engine: the INT8 kernels of kernels/gemm.py and the W4 group-dequant kernels of
+ * kernels/w4.py (reference paths).  Every entry point:
+ *
+ *   - takes plain device pointers, sizes and element strides (no framework types);
+ *   - validates its arguments before launching anything and returns a status code
+ *     (QLIN_OK == 0, negative on error; the message is in qlin_last_error());
+ *   - launches asynchronously on `stream` (a hipStream_t, NULL = default stream),
+ *     never synchronizes and never allocates memory;
+ *   - writes only into caller-allocated outputs.  Split-K partial sums go through the
+ *     caller-supplied `workspace` (at least qlin_workspace_bytes() bytes, zero-filled
+ *     once before first use; the library leaves its counters at zero after every
+ *     call).  Calls that share a workspace must not overlap in time.
+ *
+ * Layouts are the engine's (weights.py:297-309, quant_formats.py:6-9):
+ *   W8  : int8  b[K][N] (N contiguous), scale[N]
+ *   W4  : uint8 b[K/2][N]; byte (j, n) holds k = 2j in bits 0-3 and k = 2j+1 in
+ *         bits 4-7; scale[K/G][N]; optional uint8 zero[K/G][N] (one real zero per
+ *         group, not packed); the weight value is (nibble - z), z = 8 when absent.
+ *   engine activations: int8 a_q[M][K] (row stride K) with fp32 a_s[M][K/64].
+ * All matrices are row-major; `ld*` arguments are row strides in elements.
+ */
+#ifndef QLIN_H
+#define QLIN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QLIN_ABI_VERSION 1
+
+/* status codes */
+#define QLIN_OK 0
+#define QLIN_ERR_INVALID (-1)     /* null pointer, negative or inconsistent size   */
+#define QLIN_ERR_UNSUPPORTED (-2) /* valid, but shape/group/alignment/dtype unsupported */
+#define QLIN_ERR_HIP (-3)         /* HIP runtime error while launching              */
+#define QLIN_ERR_WORKSPACE (-4)   /* workspace missing or too small                 */
+
+/* element type codes (scales, activations, outputs) */
+#define QLIN_F16 1
+#define QLIN_BF16 2
+#define QLIN_F32 3
+
+/* ABI version (QLIN_ABI_VERSION). */
+int qlin_version(void);
+
+/* Message describing the last error returned on the calling thread ("" if none). */
+const char* qlin_last_error(void);
+
+/* Workspace size (bytes) every entry point below accepts. */
+size_t qlin_workspace_bytes(void);
+
+/* ---------------------------------------------------------------------------
+ * Engine-signature entry points (int8 activations + per-64 fp32 scales, bf16 out)
+ * ------------------------------------------------------------------------- */
+
+/* out[M,N] = bf16( sum_kb a_s[m,kb] * (a_q . b)[m,n,kb] * b_s[n] (+ residual) ).
+ * Replaces gemm_i8 (kernels/gemm.py:60-92, kernel gemm.py:20-57).
+ * b int8 [K,N]; b_s [N] of type bs_dtype; out/residual bf16 with row strides
+ * ldo/ldr; residual may alias out (each element is read once before it is
+ * written); residual NULL = none. */
+int qlin_gemm_i8(const int8_t* a_q, const float* a_s, int M, int K,
+                 const int8_t* b, const void* b_s, int bs_dtype, int N,
+                 void* out, int64_t ldo, const void* residual, int64_t ldr,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* W4 twin of qlin_gemm_i8: replaces gemm_w4 (kernels/w4.py:139-166, kernel
+ * w4.py:107-136).  b uint8 [K/2,N]; b_s [K/group, N]; b_z uint8 [K/group, N] or NULL
+ * (z = 8).  group: 32, 64 or a multiple of 64 (quant_formats.py:42-49). */
+int qlin_gemm_w4(const int8_t* a_q, const float* a_s, int M, int K,
+                 const uint8_t* b, const void* b_s, int bs_dtype, const uint8_t* b_z,
+                 int group, int N,
+                 void* out, int64_t ldo, const void* residual, int64_t ldr,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Three W8 projections sharing (a_q, a_s); out[:, 0:n1], [n1:n1+n2], [n1+n2:n1+n2+n3]
+ * with row stride ldo (bf16).  A NULL weight must come with n == 0.
+ * Replaces proj3 (kernels/gemm.py:290-312, kernel gemm.py:234-287). */
+int qlin_proj3_i8(const int8_t* a_q, const float* a_s, int M, int K,
+                  const int8_t* w1, const void* s1, int n1,
+                  const int8_t* w2, const void* s2, int n2,
+                  const int8_t* w3, const void* s3, int n3, int bs_dtype,
+                  void* out, int64_t ldo,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* W4 twin of qlin_proj3_i8 with per-projection zeros (NULL = 8).
+ * Replaces proj3_w4 (kernels/w4.py:220-251, kernel w4.py:169-217). */
+int qlin_proj3_w4(const int8_t* a_q, const float* a_s, int M, int K,
+                  const uint8_t* w1, const void* s1, const uint8_t* z1, int n1,
+                  const uint8_t* w2, const void* s2, const uint8_t* z2, int n2,
+                  const uint8_t* w3, const void* s3, const uint8_t* z3, int n3,
+                  int bs_dtype, int group,
+                  void* out, int64_t ldo,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[M,N] (bf16, row stride N) = silu(gate) * up, gate/up W8.
+ * Replaces mlp_gate_up (kernels/gemm.py:140-151, kernel gemm.py:95-137). */
+int qlin_mlp_gate_up_i8(const int8_t* a_q, const float* a_s, int M, int K,
+                        const int8_t* wg, const void* sg, const int8_t* wu, const void* su,
+                        int bs_dtype, int N, void* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* W4 form of qlin_mlp_gate_up_i8.  No reference counterpart (the reference's
+ * mlp_gate_up is W8 only); exported so the fused W4 quant epilogue can be checked
+ * against the unfused composition, as .dev/test_fused.py does for W8. */
+int qlin_mlp_gate_up_w4(const int8_t* a_q, const float* a_s, int M, int K,
+                        const uint8_t* wg, const void* sg, const uint8_t* zg,
+                        const uint8_t* wu, const void* su, const uint8_t* zu,
+                        int bs_dtype, int group, int N, void* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* h = bf16(silu(gate) * up); per 64 columns sc = max(amax/127, 1e-8),
+ * out_q = round_half_away(h / sc) clamped to +-127 (int8 [M,N], row stride N),
+ * out_s = sc (fp32 [M, N/64]).  N % 64 == 0.
+ * Replaces mlp_gate_up_quant (kernels/gemm.py:214-231, kernel gemm.py:154-211). */
+int qlin_mlp_gate_up_quant_i8(const int8_t* a_q, const float* a_s, int M, int K,
+                              const int8_t* wg, const void* sg,
+                              const int8_t* wu, const void* su, int bs_dtype, int N,
+                              int8_t* out_q, float* out_s,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* W4 twin.  Replaces mlp_gate_up_quant_w4 (kernels/w4.py:300-323, kernel
+ * w4.py:254-297). */
+int qlin_mlp_gate_up_quant_w4(const int8_t* a_q, const float* a_s, int M, int K,
+                              const uint8_t* wg, const void* sg, const uint8_t* zg,
+                              const uint8_t* wu, const void* su, const uint8_t* zu,
+                              int bs_dtype, int group, int N,
+                              int8_t* out_q, float* out_s,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * A16 weight-only core (fp16 activations; the form the engine's linears take when
+ * activations stay in floating point).  The reference computes this on its CPU path
+ * as "dequantize through quant_formats.py (quant_formats.py:6-9), then an fp32
+ * matmul"; these entry points are its GPU counterpart.
+ * ------------------------------------------------------------------------- */
+
+/* out[M,N] = x[M,K] . (w[K,N] * scale[N]) (+ residual).
+ * x: x_dtype (QLIN_F16), row stride ldx; out/residual: out_dtype (F16 or BF16). */
+int qlin_linear_w8(const void* x, int x_dtype, int M, int K, int64_t ldx,
+                   const int8_t* w, const void* scale, int s_dtype, int N,
+                   void* out, int out_dtype, int64_t ldo,
+                   const void* residual, int64_t ldr,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[M,N] = x . ((nibble - z) * scale[k/group, n]) (+ residual); zero NULL = 8. */
+int qlin_linear_w4(const void* x, int x_dtype, int M, int K, int64_t ldx,
+                   const uint8_t* w, const void* scale, int s_dtype,
+                   const uint8_t* zero, int group, int N,
+                   void* out, int out_dtype, int64_t ldo,
+                   const void* residual, int64_t ldr,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Layout entry points (bit-exactness checks of the unpack / dequant)
+ * ------------------------------------------------------------------------- */
+
+/* nib[K,N] = nibble of packed[K/2,N] in natural K order (kernels/w4.py:51-61). */
+int qlin_w4_unpack(const uint8_t* packed, int K, int N, uint8_t* nib, void* stream);
+
+/* out[K,N] fp32 = (nibble - z) * scale[k/group, n] (quant_formats.py:6-8,
+ * kernels/w4.py:103-104). */
+int qlin_w4_dequant_f32(const uint8_t* packed, const void* scale, int s_dtype,
+                        const uint8_t* zero, int group, int K, int N, float* out,
+                        void* stream);
+
+/* out[K,N] fp32 = w[k,n] * scale[n] (quant_formats.py:9). */
+int qlin_w8_dequant_f32(const int8_t* w, const void* scale, int s_dtype, int K, int N,
+                        float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLIN_H */

@@ -1,0 +1,454 @@
+// extern "C" entry points of libqlin.so (declared in include/qlin.h).
+//
+// Every entry point validates its arguments (shape, group, dtype, alignment) and
+// returns a status before anything is launched; the launch plan (column tile width,
+// waves per workgroup, split-K) is chosen here from K and N.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/qlin.h"
+#include "qlin_dev.h"
+#include "qlin_internal.h"
+
+using namespace qlin;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(const char* fn, hipError_t e) {
+  if (e == hipSuccess) return QLIN_OK;
+  return fail(QLIN_ERR_HIP, "%s: HIP error %d (%s)", fn, (int)e, hipGetErrorString(e));
+}
+
+// Workspace: [counters | partial sums].  Counters must be zero between calls.
+constexpr size_t kWorkspaceBytes = size_t(64) << 20;
+constexpr size_t kCounterBytes = size_t(1) << 20;
+constexpr int kTargetWorkgroups = 256;  // one per CU for the split-K heuristic
+constexpr int kWideTiles = 512;         // column tiles at which no K split is needed
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+bool dtype_scale_ok(int dt) { return dt == QLIN_F16 || dt == QLIN_BF16 || dt == QLIN_F32; }
+bool dtype_out_ok(int dt) { return dt == QLIN_F16 || dt == QLIN_BF16; }
+bool group_ok(int g) { return g == 32 || (g > 0 && g % 64 == 0); }
+
+struct Problem {
+  int act, wk, epi;
+  bool hz;
+  int M, K, group;
+  int nsets;  // weight sets per output tile (1, or 2 for gate/up)
+  int ncols;  // total output columns
+};
+
+// Fills L (kernel variant, grid, LDS) and a.kchunk / a.splits / a.ntiles / seg tiles.
+int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
+                    hipStream_t stream) {
+  SkLaunch L;
+  L.act = P.act;
+  L.wk = P.wk;
+  L.hz = P.hz ? 1 : 0;
+  L.epi = P.epi;
+  L.cols = (P.epi == EPI_STORE) ? 16 : 8;
+  const int TN = 16 * L.cols;
+
+  // column tiles per segment
+  int ntiles = 0;
+  for (int s = 0; s < a.nseg; ++s) {
+    a.seg[s].tile0 = ntiles;
+    if (P.epi == EPI_STORE) ntiles += (a.seg[s].n + TN - 1) / TN;
+  }
+  if (P.epi != EPI_STORE) {
+    ntiles = (a.seg[0].n + TN - 1) / TN;
+    a.seg[0].tile0 = a.seg[1].tile0 = 0;
+  }
+  a.ntiles = ntiles;
+
+  // K granularity of one wave's range
+  int kalign = (P.act == ACT_I8) ? 64 : 32;
+  if (P.wk == WK_W4 && P.group > kalign) kalign = P.group;
+  const int nunits = P.K / kalign;
+  const int rtiles = (P.M + 15) / 16;
+
+  int waves, splits;
+  if (P.M > 16 || ntiles >= kWideTiles) {
+    // enough column tiles (or row tiles) to fill the chip: the waves of one
+    // workgroup share K and no cross-workgroup split is needed
+    waves = nunits < 4 ? nunits : 4;
+    splits = 1;
+  } else {
+    // narrow N: split K over single-wave workgroups to reach ~kTargetWorkgroups
+    waves = 1;
+    splits = (kTargetWorkgroups + ntiles - 1) / ntiles;
+    if (splits > nunits) splits = nunits;
+  }
+  // partial sums must fit the workspace; without a workspace there is no cross-workgroup split
+  const size_t part_cap = (workspace && ws_bytes > kCounterBytes) ? ws_bytes - kCounterBytes : 0;
+  auto fits = [&](int s) {
+    const size_t need = (size_t)s * P.nsets * (size_t)P.M * (size_t)P.ncols * sizeof(float);
+    const size_t cnt_need = (size_t)rtiles * ntiles * sizeof(unsigned);
+    return need <= part_cap && cnt_need <= kCounterBytes;
+  };
+  while (splits > 1 && !fits(splits)) splits = (splits + 1) / 2;
+  const int units_per_wave = (nunits + splits * waves - 1) / (splits * waves);
+  splits = (nunits + units_per_wave * waves - 1) / (units_per_wave * waves);
+  a.kchunk = units_per_wave * kalign;
+  a.splits = splits;
+  if (splits > 1) {
+    a.cnt = (unsigned*)workspace;
+    a.part = (float*)((char*)workspace + kCounterBytes);
+  } else {
+    a.cnt = nullptr;
+    a.part = nullptr;
+  }
+  L.waves = waves;
+  L.grid = dim3((unsigned)(ntiles * splits), (unsigned)rtiles, 1);
+  L.lds = (waves > 1) ? (size_t)P.nsets * L.cols * 1024 : 0;
+  if ((long long)ntiles * splits > 0x7FFFFFFFLL || rtiles > 65535)
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: grid too large (M=%d, N=%d)", fn, P.M, P.ncols);
+  return hip_status(fn, launch_skinny(L, a, stream));
+}
+
+int check_common(const char* fn, int M, int K, int N) {
+  if (M < 0 || K <= 0 || N < 0) return fail(QLIN_ERR_INVALID, "%s: bad sizes M=%d K=%d N=%d", fn, M, K, N);
+  return QLIN_OK;
+}
+
+int check_weight(const char* fn, const void* w, const void* s, const uint8_t* z, int n, int wk) {
+  if (n == 0) return QLIN_OK;
+  if (!w || !s) return fail(QLIN_ERR_INVALID, "%s: null weight or scale", fn);
+  if (n % 16 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: N=%d is not a multiple of 16", fn, n);
+  if (!aligned(w, 16) || !aligned(s, 16) || (z && !aligned(z, 16)))
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: weight/scale/zero pointers must be 16-byte aligned", fn);
+  (void)wk;
+  return QLIN_OK;
+}
+
+int check_engine_act(const char* fn, const int8_t* a_q, const float* a_s, int M, int K) {
+  if (M > 0 && (!a_q || !a_s)) return fail(QLIN_ERR_INVALID, "%s: null activations", fn);
+  if (K % 64 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 64", fn, K);
+  if (!aligned(a_q, 8) || !aligned(a_s, 4))
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: activations must be 8-byte aligned", fn);
+  return QLIN_OK;
+}
+
+int check_out16(const char* fn, const void* p, int64_t ld, int N, const char* what) {
+  if (!p) return fail(QLIN_ERR_INVALID, "%s: null %s", fn, what);
+  if (ld < N) return fail(QLIN_ERR_INVALID, "%s: %s row stride %lld < N=%d", fn, what, (long long)ld, N);
+  if (!aligned(p, 16) || ld % 8 != 0)
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: %s must be 16-byte aligned with a row stride multiple of 8", fn,
+                what);
+  return QLIN_OK;
+}
+
+int check_group(const char* fn, int group, int K) {
+  if (!group_ok(group)) return fail(QLIN_ERR_UNSUPPORTED, "%s: weight group %d (need 32 or a multiple of 64)", fn, group);
+  if (K % group != 0) return fail(QLIN_ERR_INVALID, "%s: K=%d not a multiple of the group %d", fn, K, group);
+  return QLIN_OK;
+}
+
+#define QL_TRY(expr)              \
+  do {                            \
+    const int rc_ = (expr);       \
+    if (rc_ != QLIN_OK) return rc_; \
+  } while (0)
+
+Seg make_seg(const void* w, const void* s, const uint8_t* z, int n, int col0) {
+  Seg g;
+  g.w = (const uint8_t*)w;
+  g.s = s;
+  g.z = z;
+  g.n = n;
+  g.col0 = col0;
+  g.tile0 = 0;
+  return g;
+}
+
+SkArgs base_args() {
+  SkArgs a;
+  memset(&a, 0, sizeof(a));
+  return a;
+}
+
+// Common body of gemm_i8 / gemm_w4.
+int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int M, int K, const void* b,
+                const void* b_s, int bs_dtype, const uint8_t* b_z, int group, int N, void* out, int64_t ldo,
+                const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream) {
+  QL_TRY(check_common(fn, M, K, N));
+  if (M == 0 || N == 0) return QLIN_OK;
+  QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
+  if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
+  QL_TRY(check_weight(fn, b, b_s, b_z, N, wk));
+  QL_TRY(check_out16(fn, out, ldo, N, "out"));
+  if (residual) QL_TRY(check_out16(fn, residual, ldr, N, "residual"));
+  SkArgs a = base_args();
+  a.x = a_q;
+  a.xs = a_s;
+  a.M = M;
+  a.K = K;
+  a.seg[0] = make_seg(b, b_s, b_z, N, 0);
+  a.nseg = 1;
+  a.ncols = N;
+  a.group = (wk == WK_W4) ? group : 64;
+  a.sdt = bs_dtype;
+  a.out = out;
+  a.ldo = ldo;
+  a.odt = QLIN_BF16;
+  a.res = residual;
+  a.ldr = ldr;
+  Problem P{ACT_I8, wk, EPI_STORE, b_z != nullptr, M, K, a.group, 1, N};
+  return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
+}
+
+int engine_proj3(const char* fn, int wk, const int8_t* a_q, const float* a_s, int M, int K, const void* w1,
+                 const void* s1, const uint8_t* z1, int n1, const void* w2, const void* s2, const uint8_t* z2,
+                 int n2, const void* w3, const void* s3, const uint8_t* z3, int n3, int bs_dtype, int group,
+                 void* out, int64_t ldo, void* ws, size_t wsb, void* stream) {
+  const int NT = n1 + n2 + n3;
+  QL_TRY(check_common(fn, M, K, NT));
+  if (n1 < 0 || n2 < 0 || n3 < 0) return fail(QLIN_ERR_INVALID, "%s: negative N", fn);
+  if (M == 0 || NT == 0) return QLIN_OK;
+  QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
+  if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
+  QL_TRY(check_weight(fn, w1, s1, z1, n1, wk));
+  QL_TRY(check_weight(fn, w2, s2, z2, n2, wk));
+  QL_TRY(check_weight(fn, w3, s3, z3, n3, wk));
+  QL_TRY(check_out16(fn, out, ldo, NT, "out"));
+  const bool hz = (z1 || z2 || z3);
+  if (hz && ((n1 && !z1) || (n2 && !z2) || (n3 && !z3)))
+    return fail(QLIN_ERR_INVALID, "%s: zeros must be given for every projection or for none", fn);
+  SkArgs a = base_args();
+  a.x = a_q;
+  a.xs = a_s;
+  a.M = M;
+  a.K = K;
+  int ns = 0, col = 0;
+  const void* ws_[3] = {w1, w2, w3};
+  const void* ss_[3] = {s1, s2, s3};
+  const uint8_t* zs_[3] = {z1, z2, z3};
+  const int ns_[3] = {n1, n2, n3};
+  for (int i = 0; i < 3; ++i) {
+    if (ns_[i] == 0) continue;
+    a.seg[ns++] = make_seg(ws_[i], ss_[i], zs_[i], ns_[i], col);
+    col += ns_[i];
+  }
+  a.nseg = ns;
+  a.ncols = NT;
+  a.group = (wk == WK_W4) ? group : 64;
+  a.sdt = bs_dtype;
+  a.out = out;
+  a.ldo = ldo;
+  a.odt = QLIN_BF16;
+  Problem P{ACT_I8, wk, EPI_STORE, hz, M, K, a.group, 1, NT};
+  return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
+}
+
+int engine_gate_up(const char* fn, int wk, int epi, const int8_t* a_q, const float* a_s, int M, int K,
+                   const void* wg, const void* sg, const uint8_t* zg, const void* wu, const void* su,
+                   const uint8_t* zu, int bs_dtype, int group, int N, void* out, int8_t* out_q, float* out_s,
+                   void* ws, size_t wsb, void* stream) {
+  QL_TRY(check_common(fn, M, K, N));
+  if (M == 0 || N == 0) return QLIN_OK;
+  QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
+  if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
+  QL_TRY(check_weight(fn, wg, sg, zg, N, wk));
+  QL_TRY(check_weight(fn, wu, su, zu, N, wk));
+  if ((zg == nullptr) != (zu == nullptr))
+    return fail(QLIN_ERR_INVALID, "%s: zeros must be given for both gate and up or for neither", fn);
+  if (epi == EPI_GATEUP) {
+    QL_TRY(check_out16(fn, out, N, N, "out"));
+  } else {
+    if (N % 64 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: N=%d is not a multiple of 64", fn, N);
+    if (!out_q || !out_s) return fail(QLIN_ERR_INVALID, "%s: null out_q/out_s", fn);
+    if (!aligned(out_q, 16) || !aligned(out_s, 4))
+      return fail(QLIN_ERR_UNSUPPORTED, "%s: out_q must be 16-byte aligned", fn);
+  }
+  SkArgs a = base_args();
+  a.x = a_q;
+  a.xs = a_s;
+  a.M = M;
+  a.K = K;
+  a.seg[0] = make_seg(wg, sg, zg, N, 0);
+  a.seg[1] = make_seg(wu, su, zu, N, 0);
+  a.nseg = 2;
+  a.ncols = N;
+  a.group = (wk == WK_W4) ? group : 64;
+  a.sdt = bs_dtype;
+  a.out = out;
+  a.ldo = N;
+  a.odt = QLIN_BF16;
+  a.oq = out_q;
+  a.os = out_s;
+  Problem P{ACT_I8, wk, epi, zg != nullptr, M, K, a.group, 2, N};
+  return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
+}
+
+int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K, int64_t ldx, const void* w,
+               const void* scale, int s_dtype, const uint8_t* zero, int group, int N, void* out, int out_dtype,
+               int64_t ldo, const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream) {
+  QL_TRY(check_common(fn, M, K, N));
+  if (M == 0 || N == 0) return QLIN_OK;
+  if (!x) return fail(QLIN_ERR_INVALID, "%s: null x", fn);
+  if (x_dtype != QLIN_F16) return fail(QLIN_ERR_UNSUPPORTED, "%s: activation dtype %d (fp16 only)", fn, x_dtype);
+  if (!dtype_scale_ok(s_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, s_dtype);
+  if (!dtype_out_ok(out_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: output dtype %d", fn, out_dtype);
+  if (K % 32 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 32", fn, K);
+  if (ldx < K) return fail(QLIN_ERR_INVALID, "%s: x row stride %lld < K", fn, (long long)ldx);
+  if (!aligned(x, 16) || ldx % 8 != 0)
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: x must be 16-byte aligned with a row stride multiple of 8", fn);
+  if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
+  QL_TRY(check_weight(fn, w, scale, zero, N, wk));
+  QL_TRY(check_out16(fn, out, ldo, N, "out"));
+  if (residual) QL_TRY(check_out16(fn, residual, ldr, N, "residual"));
+  SkArgs a = base_args();
+  a.x = x;
+  a.ldx = ldx;
+  a.M = M;
+  a.K = K;
+  a.seg[0] = make_seg(w, scale, zero, N, 0);
+  a.nseg = 1;
+  a.ncols = N;
+  a.group = (wk == WK_W4) ? group : 32;
+  a.sdt = s_dtype;
+  a.out = out;
+  a.ldo = ldo;
+  a.odt = out_dtype;
+  a.res = residual;
+  a.ldr = ldr;
+  Problem P{ACT_F16, wk, EPI_STORE, zero != nullptr, M, K, a.group, 1, N};
+  return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qlin_version(void) { return QLIN_ABI_VERSION; }
+
+const char* qlin_last_error(void) { return g_err; }
+
+size_t qlin_workspace_bytes(void) { return kWorkspaceBytes; }
+
+int qlin_gemm_i8(const int8_t* a_q, const float* a_s, int M, int K, const int8_t* b, const void* b_s, int bs_dtype,
+                 int N, void* out, int64_t ldo, const void* residual, int64_t ldr, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_gemm("qlin_gemm_i8", WK_W8, a_q, a_s, M, K, b, b_s, bs_dtype, nullptr, 64, N, out, ldo, residual,
+                     ldr, workspace, workspace_bytes, stream);
+}
+
+int qlin_gemm_w4(const int8_t* a_q, const float* a_s, int M, int K, const uint8_t* b, const void* b_s,
+                 int bs_dtype, const uint8_t* b_z, int group, int N, void* out, int64_t ldo, const void* residual,
+                 int64_t ldr, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_gemm("qlin_gemm_w4", WK_W4, a_q, a_s, M, K, b, b_s, bs_dtype, b_z, group, N, out, ldo, residual,
+                     ldr, workspace, workspace_bytes, stream);
+}
+
+int qlin_proj3_i8(const int8_t* a_q, const float* a_s, int M, int K, const int8_t* w1, const void* s1, int n1,
+                  const int8_t* w2, const void* s2, int n2, const int8_t* w3, const void* s3, int n3, int bs_dtype,
+                  void* out, int64_t ldo, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_proj3("qlin_proj3_i8", WK_W8, a_q, a_s, M, K, w1, s1, nullptr, n1, w2, s2, nullptr, n2, w3, s3,
+                      nullptr, n3, bs_dtype, 64, out, ldo, workspace, workspace_bytes, stream);
+}
+
+int qlin_proj3_w4(const int8_t* a_q, const float* a_s, int M, int K, const uint8_t* w1, const void* s1,
+                  const uint8_t* z1, int n1, const uint8_t* w2, const void* s2, const uint8_t* z2, int n2,
+                  const uint8_t* w3, const void* s3, const uint8_t* z3, int n3, int bs_dtype, int group, void* out,
+                  int64_t ldo, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_proj3("qlin_proj3_w4", WK_W4, a_q, a_s, M, K, w1, s1, z1, n1, w2, s2, z2, n2, w3, s3, z3, n3,
+                      bs_dtype, group, out, ldo, workspace, workspace_bytes, stream);
+}
+
+int qlin_mlp_gate_up_i8(const int8_t* a_q, const float* a_s, int M, int K, const int8_t* wg, const void* sg,
+                        const int8_t* wu, const void* su, int bs_dtype, int N, void* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_gate_up("qlin_mlp_gate_up_i8", WK_W8, EPI_GATEUP, a_q, a_s, M, K, wg, sg, nullptr, wu, su, nullptr,
+                        bs_dtype, 64, N, out, nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+int qlin_mlp_gate_up_w4(const int8_t* a_q, const float* a_s, int M, int K, const uint8_t* wg, const void* sg,
+                        const uint8_t* zg, const uint8_t* wu, const void* su, const uint8_t* zu, int bs_dtype,
+                        int group, int N, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_gate_up("qlin_mlp_gate_up_w4", WK_W4, EPI_GATEUP, a_q, a_s, M, K, wg, sg, zg, wu, su, zu, bs_dtype,
+                        group, N, out, nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+int qlin_mlp_gate_up_quant_i8(const int8_t* a_q, const float* a_s, int M, int K, const int8_t* wg, const void* sg,
+                              const int8_t* wu, const void* su, int bs_dtype, int N, int8_t* out_q, float* out_s,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_gate_up("qlin_mlp_gate_up_quant_i8", WK_W8, EPI_GATEUP_Q, a_q, a_s, M, K, wg, sg, nullptr, wu, su,
+                        nullptr, bs_dtype, 64, N, nullptr, out_q, out_s, workspace, workspace_bytes, stream);
+}
+
+int qlin_mlp_gate_up_quant_w4(const int8_t* a_q, const float* a_s, int M, int K, const uint8_t* wg, const void* sg,
+                              const uint8_t* zg, const uint8_t* wu, const void* su, const uint8_t* zu,
+                              int bs_dtype, int group, int N, int8_t* out_q, float* out_s, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_gate_up("qlin_mlp_gate_up_quant_w4", WK_W4, EPI_GATEUP_Q, a_q, a_s, M, K, wg, sg, zg, wu, su, zu,
+                        bs_dtype, group, N, nullptr, out_q, out_s, workspace, workspace_bytes, stream);
+}
+
+int qlin_linear_w8(const void* x, int x_dtype, int M, int K, int64_t ldx, const int8_t* w, const void* scale,
+                   int s_dtype, int N, void* out, int out_dtype, int64_t ldo, const void* residual, int64_t ldr,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return a16_linear("qlin_linear_w8", WK_W8, x, x_dtype, M, K, ldx, w, scale, s_dtype, nullptr, 32, N, out,
+                    out_dtype, ldo, residual, ldr, workspace, workspace_bytes, stream);
+}
+
+int qlin_linear_w4(const void* x, int x_dtype, int M, int K, int64_t ldx, const uint8_t* w, const void* scale,
+                   int s_dtype, const uint8_t* zero, int group, int N, void* out, int out_dtype, int64_t ldo,
+                   const void* residual, int64_t ldr, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  return a16_linear("qlin_linear_w4", WK_W4, x, x_dtype, M, K, ldx, w, scale, s_dtype, zero, group, N, out,
+                    out_dtype, ldo, residual, ldr, workspace, workspace_bytes, stream);
+}
+
+int qlin_w4_unpack(const uint8_t* packed, int K, int N, uint8_t* nib, void* stream) {
+  g_err[0] = 0;
+  if (K < 0 || N < 0 || K % 2) return fail(QLIN_ERR_INVALID, "qlin_w4_unpack: bad sizes K=%d N=%d", K, N);
+  if ((long long)K * N == 0) return QLIN_OK;
+  if (!packed || !nib) return fail(QLIN_ERR_INVALID, "qlin_w4_unpack: null pointer");
+  return hip_status("qlin_w4_unpack", launch_w4_unpack(packed, K, N, nib, (hipStream_t)stream));
+}
+
+int qlin_w4_dequant_f32(const uint8_t* packed, const void* scale, int s_dtype, const uint8_t* zero, int group, int K,
+                        int N, float* out, void* stream) {
+  g_err[0] = 0;
+  if (K < 0 || N < 0 || K % 2) return fail(QLIN_ERR_INVALID, "qlin_w4_dequant_f32: bad sizes K=%d N=%d", K, N);
+  if (group <= 0 || K % group) return fail(QLIN_ERR_INVALID, "qlin_w4_dequant_f32: bad group %d", group);
+  if (!dtype_scale_ok(s_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "qlin_w4_dequant_f32: scale dtype %d", s_dtype);
+  if ((long long)K * N == 0) return QLIN_OK;
+  if (!packed || !scale || !out) return fail(QLIN_ERR_INVALID, "qlin_w4_dequant_f32: null pointer");
+  return hip_status("qlin_w4_dequant_f32",
+                    launch_w4_dequant(packed, scale, s_dtype, zero, group, K, N, out, (hipStream_t)stream));
+}
+
+int qlin_w8_dequant_f32(const int8_t* w, const void* scale, int s_dtype, int K, int N, float* out, void* stream) {
+  g_err[0] = 0;
+  if (K < 0 || N < 0) return fail(QLIN_ERR_INVALID, "qlin_w8_dequant_f32: bad sizes K=%d N=%d", K, N);
+  if (!dtype_scale_ok(s_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "qlin_w8_dequant_f32: scale dtype %d", s_dtype);
+  if ((long long)K * N == 0) return QLIN_OK;
+  if (!w || !scale || !out) return fail(QLIN_ERR_INVALID, "qlin_w8_dequant_f32: null pointer");
+  return hip_status("qlin_w8_dequant_f32", launch_w8_dequant(w, scale, s_dtype, K, N, out, (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,160 @@
+// Device-side helpers for the gfx950 quantized-linear kernels.
+//
+// The engine's weight layouts are N-contiguous (int8 [K,N], packed nibbles [K/2,N]),
+// so a 128-bit load gives one lane 16 adjacent output columns of one K row.  CDNA
+// MFMA wants the opposite in each lane: several consecutive K values of ONE output
+// column.  The helpers below rebuild MFMA operands in registers with v_perm_b32 byte
+// permutes (no LDS round trip):
+//
+//   * f16 operands: a pair of K values of one column becomes one f16x2 through the
+//     exponent-bias trick: 0x6400 | u is the fp16 value 1024 + u for 0 <= u < 1024,
+//     so one permute plus one packed fp16 add/fma yields exact small integers.
+//   * i8 operands: 4x4 byte transposes (8 permutes per 4 output dwords).
+//
+// All arithmetic here is exact: every integer weight value in [-128, 127] and every
+// nibble difference is representable in fp16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+namespace qlin {
+
+enum ActKind { ACT_F16 = 0, ACT_I8 = 1 };
+enum WKind { WK_W8 = 0, WK_W4 = 1 };
+enum EpiKind { EPI_STORE = 0, EPI_GATEUP = 1, EPI_GATEUP_Q = 2 };
+enum DType { DT_F16 = 1, DT_BF16 = 2, DT_F32 = 3 };
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+template <typename T, typename F>
+__device__ __forceinline__ T bitcast(F f) {
+  return __builtin_bit_cast(T, f);
+}
+
+// ---------------------------------------------------------------------------
+// fp16 operands
+// ---------------------------------------------------------------------------
+
+// Two int8 weights of the same column from two K rows -> exact f16x2.
+// d0/d1: dwords of rows k and k+1 holding the column's byte at position `b`
+// (b must fold to a constant after unrolling so the permute selector is an immediate).
+// perm gives [d0.b, 0, d1.b, 0]; xor 0x64806480 sets the 0x64 exponent byte and
+// flips the sign bit (u = b + 128), so each half is 1024 + 128 + b; subtracting
+// 1152 leaves b exactly.
+__device__ __forceinline__ uint32_t w8_pair_f16(uint32_t d0, uint32_t d1, int b) {
+  const uint32_t sel = 0x0c000c00u | ((4u + (uint32_t)b) << 16) | (uint32_t)b;
+  const uint32_t p = perm(d1, d0, sel) ^ 0x64806480u;
+  const f16x2 h = bitcast<f16x2>(p) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+  return bitcast<uint32_t>(h);
+}
+
+// The two nibbles (k even = low nibble, k odd = high nibble) of one packed byte ->
+// exact f16x2 (nibble_lo - z, nibble_hi - z).  perm duplicates the byte under two
+// 0x64 exponent bytes; the mask keeps the low nibble in half 0 (1024 + lo) and the
+// high nibble in place in half 1 (1024 + 16*hi); one packed fma with
+// (1, 1/16) and bias = (-1024 - z, -64 - z) finishes both exactly.
+__device__ __forceinline__ uint32_t w4_pair_f16(uint32_t d, int b, f16x2 bias) {
+  const uint32_t sel = (uint32_t)b | (4u << 8) | ((uint32_t)b << 16) | (4u << 24);
+  const uint32_t p = perm(0x64646464u, d, sel) & 0xFFF0FF0Fu;
+  const f16x2 h = bitcast<f16x2>(p);
+  const f16x2 m = f16x2{(_Float16)1.0f, (_Float16)0.0625f};
+  return bitcast<uint32_t>(__builtin_elementwise_fma(h, m, bias));
+}
+
+__device__ __forceinline__ f16x2 w4_bias(uint32_t z) {
+  return f16x2{(_Float16)(-1024.0f - (float)z), (_Float16)(-64.0f - (float)z)};
+}
+
+// ---------------------------------------------------------------------------
+// int8 operands
+// ---------------------------------------------------------------------------
+
+// 4x4 byte transpose: out[u].byte[r] = in[r].byte[u].
+__device__ __forceinline__ void tr4(const uint32_t in0, const uint32_t in1, const uint32_t in2,
+                                    const uint32_t in3, uint32_t out[4]) {
+  const uint32_t t0 = perm(in1, in0, 0x05010400u);  // in0.b0 in1.b0 in0.b1 in1.b1
+  const uint32_t t1 = perm(in1, in0, 0x07030602u);  // in0.b2 in1.b2 in0.b3 in1.b3
+  const uint32_t t2 = perm(in3, in2, 0x05010400u);
+  const uint32_t t3 = perm(in3, in2, 0x07030602u);
+  out[0] = perm(t2, t0, 0x05040100u);
+  out[1] = perm(t2, t0, 0x07060302u);
+  out[2] = perm(t3, t1, 0x05040100u);
+  out[3] = perm(t3, t1, 0x07060302u);
+}
+
+// Packed nibbles -> int8 holding 16 * (nibble - 8): xor 0x88 maps nibble n to the
+// 4-bit two's complement of n - 8; moved to the top of the byte it reads as an int8
+// equal to 16 * (n - 8).  lo: even-k nibbles, hi: odd-k nibbles.
+__device__ __forceinline__ void w4_split_i8x16(uint32_t d, uint32_t& lo, uint32_t& hi) {
+  const uint32_t x = d ^ 0x88888888u;
+  hi = x & 0xF0F0F0F0u;
+  lo = (x << 4) & 0xF0F0F0F0u;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers (16x16 output; lane l holds D[4*(l/16)+r][l%16], r = 0..3)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ f32x4 mfma_f16(const f16x8 a, const f16x8 b, const f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ i32x4 mfma_i8(const uint64_t a, const uint64_t b, const i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Element conversions
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return bitcast<float>((uint32_t)b << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN -> quiet NaN), as torch's cast.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  const uint32_t u = bitcast<uint32_t>(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)0x7FC0;
+  return (uint16_t)((u + (((u >> 16) & 1u) + 0x7FFFu)) >> 16);
+}
+
+__device__ __forceinline__ float load_scale(const void* p, int dt, long long i) {
+  if (dt == DT_F32) return ((const float*)p)[i];
+  if (dt == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+  return (float)((const _Float16*)p)[i];
+}
+
+__device__ __forceinline__ float load_act16(const void* p, int dt, long long i) {
+  if (dt == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+  return (float)((const _Float16*)p)[i];
+}
+
+__device__ __forceinline__ uint16_t to_out16(float v, int dt) {
+  if (dt == DT_BF16) return f32_to_bf16(v);
+  return bitcast<uint16_t>((_Float16)v);
+}
+
+// x * sigmoid(x) (kernels/common.py:32-34).
+__device__ __forceinline__ float silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
+
+// Round half away from zero with the add in fp32, truncate, clamp to [-127, 127]
+// (kernels/common.py:24-29).
+__device__ __forceinline__ int round_i8(float v) {
+  const float t = v + (v >= 0.0f ? 0.5f : -0.5f);
+  int r = (int)t;
+  r = r < -127 ? -127 : r;
+  r = r > 127 ? 127 : r;
+  return r;
+}
+
+}  // namespace qlin

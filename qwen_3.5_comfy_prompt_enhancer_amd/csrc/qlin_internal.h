@@ -1,0 +1,59 @@
+// Host/device shared definitions of libqlin (not part of the public ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qlin {
+
+// One weight matrix covering a contiguous range of output columns.
+struct Seg {
+  const uint8_t* w;  // int8 [K][n] or packed uint8 [K/2][n]
+  const void* s;     // W8: scale[n]; W4: scale[K/group][n]
+  const uint8_t* z;  // W4 zeros [K/group][n] or nullptr
+  int n;             // columns of this matrix
+  int col0;          // first output column it writes
+  int tile0;         // first column tile that belongs to it
+};
+
+// Arguments of the skinny (row-tile of <= 16 rows) MFMA kernel.
+struct SkArgs {
+  const void* x;       // ACT_F16: fp16 [M][ldx]; ACT_I8: int8 [M][K]
+  const float* xs;     // ACT_I8: fp32 [M][K/64]
+  long long ldx;
+  int M, K;
+  Seg seg[3];          // EPI_STORE: up to 3 column segments; gate/up: seg[0]=gate, seg[1]=up
+  int nseg;
+  int ntiles;          // column tiles
+  int ncols;           // total output columns
+  int group;           // W4 weight group
+  int sdt;             // scale element type (DT_*)
+  void* out;           // EPI_STORE / EPI_GATEUP output (16-bit elements)
+  long long ldo;
+  int odt;             // output element type (DT_F16 / DT_BF16)
+  const void* res;     // residual (odt) or nullptr
+  long long ldr;
+  int8_t* oq;          // EPI_GATEUP_Q int8 [M][ncols]
+  float* os;           // EPI_GATEUP_Q fp32 [M][ncols/64]
+  float* part;         // split-K partials [splits][nsets][M][ncols]
+  unsigned* cnt;       // split-K arrival counters [row tiles][ntiles], zero between calls
+  int kchunk;          // K range of one wave
+  int splits;          // workgroups per column tile along K
+};
+
+struct SkLaunch {
+  int act, wk, hz, epi, cols;
+  int waves;       // waves per workgroup
+  dim3 grid;
+  size_t lds;      // dynamic LDS bytes
+};
+
+hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
+
+hipError_t launch_w4_unpack(const uint8_t* p, int K, int N, uint8_t* out, hipStream_t st);
+hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uint8_t* z,
+                             int group, int K, int N, float* out, hipStream_t st);
+hipError_t launch_w8_dequant(const int8_t* w, const void* s, int sdt, int K, int N, float* out,
+                             hipStream_t st);
+
+}  // namespace qlin

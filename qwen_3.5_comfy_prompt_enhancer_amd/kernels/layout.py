@@ -1,0 +1,58 @@
+"""GPU unpack / dequant of the engine weight layouts (bit-exactness checks).
+
+These expose the exact values the GEMM kernels consume:
+
+* `w4_unpack(packed)` -> uint8 nibbles [K, N] in natural K order (kernels/w4.py:51-61);
+* `w4_dequant_f32(packed, scale, zero=None)` -> fp32 `(nibble - z) * scale[k // G, n]`
+  (quant_formats.py:6-8, kernels/w4.py:103-104);
+* `w8_dequant_f32(w, scale)` -> fp32 `w * scale[None, :]` (quant_formats.py:9).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import common as C
+
+__all__ = ["w4_unpack", "w4_dequant_f32", "w8_dequant_f32"]
+
+
+def w4_unpack(packed: torch.Tensor) -> torch.Tensor:
+    if packed.dtype != torch.uint8 or packed.dim() != 2:
+        raise ValueError("packed must be uint8 [K/2, N]")
+    C.require_contig("packed", packed)
+    C.require_cuda(packed)
+    K, N = packed.shape[0] * 2, packed.shape[1]
+    out = torch.empty((K, N), dtype=torch.uint8, device=packed.device)
+    C.call("qlin_w4_unpack", C.ptr(packed), K, N, C.ptr(out), C.stream_of(packed))
+    return out
+
+
+def w4_dequant_f32(packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor | None = None):
+    if packed.dtype != torch.uint8 or packed.dim() != 2:
+        raise ValueError("packed must be uint8 [K/2, N]")
+    K, N = packed.shape[0] * 2, packed.shape[1]
+    if scale.dim() != 2 or scale.shape[1] != N or K % scale.shape[0] != 0:
+        raise ValueError("scale must be [K/group, N]")
+    group = K // scale.shape[0]
+    if zero is not None and (zero.dtype != torch.uint8 or zero.shape != scale.shape):
+        raise ValueError("zero must be uint8 shaped like scale")
+    for name, t in (("packed", packed), ("scale", scale), ("zero", zero)):
+        C.require_contig(name, t)
+    C.require_cuda(packed, scale, zero)
+    out = torch.empty((K, N), dtype=torch.float32, device=packed.device)
+    C.call("qlin_w4_dequant_f32", C.ptr(packed), C.ptr(scale), C.dtype_code(scale), C.ptr(zero),
+           group, K, N, C.ptr(out), C.stream_of(packed))
+    return out
+
+
+def w8_dequant_f32(w: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    if w.dtype != torch.int8 or w.dim() != 2 or scale.dim() != 1 or scale.shape[0] != w.shape[1]:
+        raise ValueError("w must be int8 [K, N] and scale [N]")
+    C.require_contig("w", w)
+    C.require_contig("scale", scale)
+    C.require_cuda(w, scale)
+    K, N = w.shape
+    out = torch.empty((K, N), dtype=torch.float32, device=w.device)
+    C.call("qlin_w8_dequant_f32", C.ptr(w), C.ptr(scale), C.dtype_code(scale), K, N, C.ptr(out),
+           C.stream_of(w))
+    return out

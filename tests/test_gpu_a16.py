@@ -1,0 +1,204 @@
+"""GPU parity of the layout kernels and the A16 (fp16-activation) linears against the
+CPU oracle, on the workload shapes (decode rows M <= 4 and mid-range M).
+
+Bar: unpack / dequant bit-exact; GEMM max|y - y_ref| / max|y_ref| <= 2e-3 against
+the oracle's fp32 result (y_ref = dequantize, then fp32 matmul).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import helpers as H
+from oracle import ref_cpu as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _k():
+    from qwen35_amd.kernels import layout, linear
+    return layout, linear
+
+
+# ---------------------------------------------------------------- layout, bit-exact
+
+@pytest.mark.parametrize("K,N", [(256, 16), (2048, 512), (4096, 1040)])
+def test_w4_unpack_bit_exact(K, N):
+    layout, _ = _k()
+    packed, _, _ = H.w4(K, N, seed=11)
+    nib = layout.w4_unpack(packed.cuda()).cpu().numpy()
+    assert np.array_equal(nib, R.unpack_w4(packed.numpy()))
+
+
+def test_w4_unpack_all_bytes():
+    layout, _ = _k()
+    packed = torch.arange(256, dtype=torch.int32).to(torch.uint8).reshape(1, 256).repeat(2, 1)
+    nib = layout.w4_unpack(packed.cuda()).cpu().numpy()
+    assert np.array_equal(nib, R.unpack_w4(packed.numpy()))
+
+
+@pytest.mark.parametrize("group,zeros,sdt", [(128, "none", torch.float16), (32, "random", torch.float16),
+                                             (64, "random", torch.bfloat16), (128, "eight", torch.float32)])
+def test_w4_dequant_bit_exact(group, zeros, sdt):
+    layout, _ = _k()
+    K, N = 1024, 256
+    packed, s, z = H.w4(K, N, seed=12, group=group, zeros=zeros)
+    s = s.to(sdt)
+    d = layout.w4_dequant_f32(packed.cuda(), s.cuda(), None if z is None else z.cuda()).cpu().numpy()
+    ref = R.dequant_w4_f32(packed.numpy(), H.np_(s), None if z is None else z.numpy())
+    assert np.array_equal(d, ref)
+
+
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+def test_w8_dequant_bit_exact(sdt):
+    layout, _ = _k()
+    w, s = H.w8(512, 256, seed=13)
+    s = s.to(sdt)
+    d = layout.w8_dequant_f32(w.cuda(), s.cuda()).cpu().numpy()
+    assert np.array_equal(d, R.dequant_w8_f32(w.numpy(), H.np_(s)))
+
+
+# ---------------------------------------------------------------- A16 linears
+
+def _run_w8(x, w, s, out_dtype=torch.float16, residual=None):
+    _, linear = _k()
+    M, N = x.shape[0], w.shape[1]
+    out = torch.empty((M, N), dtype=out_dtype, device="cuda")
+    linear.linear_w8(x.cuda(), w.cuda(), s.cuda(), out,
+                     residual=None if residual is None else residual.cuda())
+    torch.cuda.synchronize()
+    return out
+
+
+def _run_w4(x, packed, s, z, out_dtype=torch.float16, residual=None):
+    _, linear = _k()
+    M, N = x.shape[0], packed.shape[1]
+    out = torch.empty((M, N), dtype=out_dtype, device="cuda")
+    linear.linear_w4(x.cuda(), packed.cuda(), s.cuda(), out,
+                     w_zero=None if z is None else z.cuda(),
+                     residual=None if residual is None else residual.cuda())
+    torch.cuda.synchronize()
+    return out
+
+
+def test_linear_w8_plumbing_case():
+    """M=1, K=2048, N=6144 int8 per-channel, fp16 out (the single-linear CPU case)."""
+    x = H.act_f16(1, 2048, seed=0)
+    w, s = H.w8(2048, 6144, seed=0)
+    y = _run_w8(x, w, s)
+    ref = H.linear_w8_ref_cols(x, w, s, np.arange(6144))
+    assert R.max_rel_err(H.to_f32(y), ref) <= TOL
+    assert R.rel_l2(H.to_f32(y), ref) < 1e-3
+
+
+DECODE_SHAPES = [(2048, 2048), (2048, 512), (2048, 6144), (6144, 2048), (2048, 4096), (4096, 2048)]
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("K,N", DECODE_SHAPES)
+def test_linear_w8_decode_shapes(M, K, N):
+    x = H.act_f16(M, K, seed=100 + M)
+    w, s = H.w8(K, N, seed=K + N)
+    y = _run_w8(x, w, s)
+    ref = H.linear_w8_ref_cols(x, w, s, np.arange(N))
+    assert R.max_rel_err(H.to_f32(y), ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_linear_w8_vocab_head(M):
+    K, N = 2048, 248320
+    x = H.act_f16(M, K, seed=7)
+    w, s = H.w8(K, N, seed=8)
+    y = _run_w8(x, w, s)
+    cols = H.sample_cols(N, 8192)
+    ref = H.linear_w8_ref_cols(x, w, s, cols)
+    assert R.max_rel_err(H.to_f32(y)[:, cols], ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("K,N", DECODE_SHAPES)
+def test_linear_w4_decode_shapes(M, K, N):
+    x = H.act_f16(M, K, seed=200 + M)
+    packed, s, z = H.w4(K, N, seed=K * 3 + N)
+    y = _run_w4(x, packed, s, z)
+    ref = H.linear_w4_ref_cols(x, packed, s, z, np.arange(N))
+    assert R.max_rel_err(H.to_f32(y), ref) <= TOL
+
+
+def test_linear_w4_explicit_zero_eight_is_identical():
+    x = H.act_f16(4, 2048, seed=21)
+    packed, s, _ = H.w4(2048, 2048, seed=22)
+    z8 = torch.full((2048 // 128, 2048), 8, dtype=torch.uint8)
+    y0 = _run_w4(x, packed, s, None)
+    y1 = _run_w4(x, packed, s, z8)
+    assert torch.equal(y0, y1)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+@pytest.mark.parametrize("zeros", ["none", "random"])
+def test_linear_w4_groups_and_zeros(group, zeros):
+    M, K, N = 3, 1024, 768
+    x = H.act_f16(M, K, seed=31)
+    packed, s, z = H.w4(K, N, seed=32, group=group, zeros=zeros)
+    y = _run_w4(x, packed, s, z)
+    ref = H.linear_w4_ref_cols(x, packed, s, z, np.arange(N))
+    assert R.max_rel_err(H.to_f32(y), ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_linear_w4_vocab_head(M):
+    K, N = 2048, 248320
+    x = H.act_f16(M, K, seed=41)
+    packed, s, z = H.w4(K, N, seed=42)
+    y = _run_w4(x, packed, s, z)
+    cols = H.sample_cols(N, 8192)
+    ref = H.linear_w4_ref_cols(x, packed, s, z, cols)
+    assert R.max_rel_err(H.to_f32(y)[:, cols], ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [5, 16, 17, 40])
+def test_linear_mid_range_rows(M):
+    K, N = 2048, 1024
+    x = H.act_f16(M, K, seed=50 + M)
+    w, s = H.w8(K, N, seed=51)
+    y = _run_w8(x, w, s)
+    assert R.max_rel_err(H.to_f32(y), H.linear_w8_ref_cols(x, w, s, np.arange(N))) <= TOL
+    packed, s4, z = H.w4(K, N, seed=52, zeros="random")
+    y4 = _run_w4(x, packed, s4, z)
+    assert R.max_rel_err(H.to_f32(y4), H.linear_w4_ref_cols(x, packed, s4, z, np.arange(N))) <= TOL
+
+
+def test_linear_residual_and_bf16_out():
+    M, K, N = 4, 2048, 2048
+    x = H.act_f16(M, K, seed=61)
+    w, s = H.w8(K, N, seed=62)
+    res = torch.randn((M, N), generator=H.gen(63)).to(torch.bfloat16)
+    y = _run_w8(x, w, s, out_dtype=torch.bfloat16, residual=res)
+    ref = H.linear_w8_ref_cols(x, w, s, np.arange(N), residual=res)
+    assert R.max_rel_err(H.to_f32(y), ref) <= TOL
+
+
+def test_rows_independent_of_batch():
+    """Row m of an M=4 call is bit-identical to the same row run alone (every
+    split choice depends on K and N only)."""
+    K, N = 2048, 6144
+    x = H.act_f16(4, K, seed=71)
+    w, s = H.w8(K, N, seed=72)
+    packed, s4, _ = H.w4(K, N, seed=73)
+    y = _run_w8(x, w, s)
+    y4 = _run_w4(x, packed, s4, None)
+    for m in range(4):
+        assert torch.equal(_run_w8(x[m:m + 1], w, s)[0], y[m])
+        assert torch.equal(_run_w4(x[m:m + 1], packed, s4, None)[0], y4[m])
+
+
+def test_repeat_calls_are_deterministic():
+    """Split-K partials are summed in a fixed order, so repeated calls agree bit for bit."""
+    K, N = 6144, 2048
+    x = H.act_f16(2, K, seed=81)
+    w, s = H.w8(K, N, seed=82)
+    ys = [_run_w8(x, w, s) for _ in range(3)]
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[1], ys[2])

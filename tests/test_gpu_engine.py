@@ -1,0 +1,223 @@
+"""GPU parity of the engine-signature entry points (gemm_i8 / gemm_w4 / proj3(_w4) /
+mlp_gate_up / mlp_gate_up_quant(_w4)) against the CPU oracle, at the shapes the
+reference's own kernel tests use (.dev/test_kernels.py:31-80, .dev/test_fused.py:22-46)
+and at the engine's decode shapes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import helpers as H
+from oracle import ref_cpu as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _g():
+    from qwen35_amd.kernels import gemm, w4
+    return gemm, w4
+
+
+def _bf16(t):
+    return H.np_(t.cpu())
+
+
+def _w4_engine(K, N, seed, group=128, zeros="none"):
+    """Engine W4: packed nibbles + bf16 group scales (weights.py:297-305)."""
+    packed, s, z = H.w4(K, N, seed, group=group, zeros=zeros)
+    return packed, s.to(torch.bfloat16), z
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 3584, 1024), (37, 3584, 1024), (37, 2048, 1024),
+                                   (1, 248320, 1024), (4, 6144, 2048), (8, 2048, 6144)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_gemm_i8(M, N, K, with_res):
+    gemm, _ = _g()
+    a, as_ = H.engine_act(M, K, seed=M + K)
+    b, bs = H.engine_w8(K, N, seed=N)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    res = torch.randn((M, N), generator=H.gen(5)).to(torch.bfloat16) if with_res else None
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out,
+                 residual=None if res is None else res.cuda(), block_k=64)
+    cols = H.sample_cols(N, 8192)
+    ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy()[:, cols], bs.numpy()[cols],
+                        residual=None if res is None else _bf16(res)[:, cols])
+    y = H.to_f32(out)[:, cols]
+    assert R.max_rel_err(y, ref) <= TOL
+    assert R.rel_l2(y, ref) < 3e-3
+
+
+def test_gemm_i8_in_place_residual():
+    """`out is residual` (engine.py:238-240): each element read once before written."""
+    gemm, _ = _g()
+    M, K, N = 4, 2048, 2048
+    a, as_ = H.engine_act(M, K, seed=1)
+    b, bs = H.engine_w8(K, N, seed=2)
+    hid = torch.randn((M, N), generator=H.gen(3)).to(torch.bfloat16)
+    ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy(), bs.numpy(), residual=_bf16(hid))
+    h = hid.cuda()
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), h, residual=h)
+    assert R.max_rel_err(H.to_f32(h), ref) <= TOL
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("zeros", ["none", "random"])
+@pytest.mark.parametrize("M", [1, 4, 37])
+def test_gemm_w4(group, zeros, M):
+    gemm, _ = _g()
+    K, N = 2048, 2048
+    a, as_ = H.engine_act(M, K, seed=M)
+    b, bs, bz = _w4_engine(K, N, seed=group, group=group, zeros=zeros)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    res = torch.randn((M, N), generator=H.gen(9)).to(torch.bfloat16)
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out, residual=res.cuda(),
+                 b_z=None if bz is None else bz.cuda())
+    ref = R.gemm_w4_ref(a.numpy(), as_.numpy(), b.numpy(), _bf16(bs),
+                        None if bz is None else bz.numpy(), residual=_bf16(res))
+    assert R.max_rel_err(H.to_f32(out), ref) <= TOL
+
+
+def test_gemm_w4_explicit_zero_eight_is_identical():
+    _, w4 = _g()
+    M, K, N = 4, 2048, 1024
+    a, as_ = H.engine_act(M, K, seed=3)
+    b, bs, _ = _w4_engine(K, N, seed=4)
+    z8 = torch.full((K // 128, N), 8, dtype=torch.uint8, device="cuda")
+    o0 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    o1 = torch.empty_like(o0)
+    w4.gemm_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), o0)
+    w4.gemm_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), o1, b_z=z8)
+    assert torch.equal(o0, o1)
+
+
+@pytest.mark.parametrize("M", [1, 4, 37])
+def test_proj3_w8(M):
+    """lin_qkv + lin_z shape (6144 + 2048) and q/k/v (4096 + 512 + 512)."""
+    gemm, _ = _g()
+    K = 2048
+    a, as_ = H.engine_act(M, K, seed=11)
+    w1, s1 = H.engine_w8(K, 6144, seed=12)
+    w2, s2 = H.engine_w8(K, 2048, seed=13)
+    out = torch.full((M, 8192 + 64), 7.0, dtype=torch.bfloat16, device="cuda")
+    gemm.proj3(a.cuda(), as_.cuda(), w1.cuda(), s1.cuda(), w2.cuda(), s2.cuda(), None, None, out)
+    ref = R.proj3_ref(a.numpy(), as_.numpy(), w1.numpy(), s1.numpy(), w2.numpy(), s2.numpy(), None, None)
+    y = H.to_f32(out)
+    assert R.max_rel_err(y[:, :6144], ref[:, :6144]) <= TOL
+    assert R.max_rel_err(y[:, 6144:8192], ref[:, 6144:]) <= TOL
+    assert np.all(y[:, 8192:] == 7.0)       # columns beyond NT untouched
+    q, sq = H.engine_w8(K, 4096, seed=14)
+    k, sk = H.engine_w8(K, 512, seed=15)
+    v, sv = H.engine_w8(K, 512, seed=16)
+    out2 = torch.empty((M, 5120), dtype=torch.bfloat16, device="cuda")
+    gemm.proj3(a.cuda(), as_.cuda(), q.cuda(), sq.cuda(), k.cuda(), sk.cuda(), v.cuda(), sv.cuda(), out2)
+    ref2 = R.proj3_ref(a.numpy(), as_.numpy(), q.numpy(), sq.numpy(), k.numpy(), sk.numpy(), v.numpy(), sv.numpy())
+    assert R.max_rel_err(H.to_f32(out2), ref2) <= TOL
+
+
+@pytest.mark.parametrize("zeros", ["none", "random"])
+@pytest.mark.parametrize("M", [1, 4, 37])
+def test_proj3_w4(zeros, M):
+    gemm, _ = _g()
+    K = 2048
+    a, as_ = H.engine_act(M, K, seed=21)
+    ws = [_w4_engine(K, n, seed=22 + i, zeros=zeros) for i, n in enumerate((4096, 512, 512))]
+    out = torch.empty((M, 5120), dtype=torch.bfloat16, device="cuda")
+    cu = lambda t: None if t is None else t.cuda()
+    gemm.proj3(a.cuda(), as_.cuda(), cu(ws[0][0]), cu(ws[0][1]), cu(ws[1][0]), cu(ws[1][1]),
+               cu(ws[2][0]), cu(ws[2][1]), out, z1=cu(ws[0][2]), z2=cu(ws[1][2]), z3=cu(ws[2][2]))
+    npz = lambda t: None if t is None else t.numpy()
+    ref = R.proj3_ref(a.numpy(), as_.numpy(), ws[0][0].numpy(), _bf16(ws[0][1]), ws[1][0].numpy(),
+                      _bf16(ws[1][1]), ws[2][0].numpy(), _bf16(ws[2][1]),
+                      npz(ws[0][2]), npz(ws[1][2]), npz(ws[2][2]))
+    assert R.max_rel_err(H.to_f32(out), ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 16, 37])
+def test_mlp_gate_up(M):
+    gemm, _ = _g()
+    K, N = 1024, 3584
+    a, as_ = H.engine_act(M, K, seed=31)
+    wg, sg = H.engine_w8(K, N, seed=32)
+    wu, su = H.engine_w8(K, N, seed=33)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    gemm.mlp_gate_up(a.cuda(), as_.cuda(), wg.cuda(), sg.cuda(), wu.cuda(), su.cuda(), out)
+    ref = R.mlp_gate_up_ref(a.numpy(), as_.numpy(), wg.numpy(), sg.numpy(), wu.numpy(), su.numpy())
+    assert R.max_rel_err(H.to_f32(out), ref) <= TOL
+
+
+def _fused_vs_unfused(M, w4_=False, zeros="none", group=128):
+    """.dev/test_fused.py:22-46: the fused int8 output must equal quant_row applied to
+    the unfused bf16 h -- here bit for bit, since both kernels share the
+    accumulation and the oracle's quant_groups is the reference's quantizer."""
+    gemm, w4 = _g()
+    K, N = 2048, 6144
+    a, as_ = H.engine_act(M, K, seed=41 + M)
+    if w4_:
+        wg, sg, zg = _w4_engine(K, N, seed=42, group=group, zeros=zeros)
+        wu, su, zu = _w4_engine(K, N, seed=43, group=group, zeros=zeros)
+    else:
+        (wg, sg), (wu, su) = H.engine_w8(K, N, seed=42), H.engine_w8(K, N, seed=43)
+        zg = zu = None
+    cu = lambda t: None if t is None else t.cuda()
+    h = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    q1 = torch.empty((M, N), dtype=torch.int8, device="cuda")
+    s1 = torch.empty((M, N // 64), dtype=torch.float32, device="cuda")
+    if w4_:
+        w4.mlp_gate_up_w4(cu(a), cu(as_), cu(wg), cu(sg), cu(wu), cu(su), h, zg=cu(zg), zu=cu(zu))
+    else:
+        gemm.mlp_gate_up(cu(a), cu(as_), cu(wg), cu(sg), cu(wu), cu(su), h)
+    gemm.mlp_gate_up_quant(cu(a), cu(as_), cu(wg), cu(sg), cu(wu), cu(su), q1, s1, zg=cu(zg), zu=cu(zu))
+    q0, s0 = R.quant_groups(H.to_f32(h))
+    assert np.array_equal(q1.cpu().numpy(), q0)
+    assert np.array_equal(s1.cpu().numpy(), s0)
+    # and against the oracle's fused path: dequantized values within tolerance,
+    # int8 codes equal except where bf16 rounding of h differs
+    npz = lambda t: None if t is None else (H.np_(t) if t.dtype == torch.bfloat16 else t.numpy())
+    qr, sr = R.mlp_gate_up_quant_ref(a.numpy(), as_.numpy(), npz(wg), npz(sg), npz(wu), npz(su),
+                                     npz(zg), npz(zu))
+    deq = q1.cpu().numpy().astype(np.float32) * np.repeat(s1.cpu().numpy(), 64, 1)
+    deq_r = qr.astype(np.float32) * np.repeat(sr, 64, 1)
+    assert R.max_rel_err(deq, deq_r) <= 1e-2
+    assert (q1.cpu().numpy() == qr).mean() > 0.99
+
+
+@pytest.mark.parametrize("M", [1, 16, 37])
+def test_mlp_gate_up_quant_w8(M):
+    _fused_vs_unfused(M)
+
+
+@pytest.mark.parametrize("M,zeros,group", [(1, "none", 128), (4, "random", 128), (16, "none", 32),
+                                           (37, "random", 64)])
+def test_mlp_gate_up_quant_w4(M, zeros, group):
+    _fused_vs_unfused(M, w4_=True, zeros=zeros, group=group)
+
+
+def test_engine_rows_independent_of_batch():
+    gemm, _ = _g()
+    K, N = 2048, 6144
+    a, as_ = H.engine_act(4, K, seed=51)
+    b, bs = H.engine_w8(K, N, seed=52)
+    out = torch.empty((4, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)
+    for m in range(4):
+        o1 = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+        gemm.gemm_i8(a[m:m + 1].cuda(), as_[m:m + 1].cuda(), b.cuda(), bs.cuda(), o1)
+        assert torch.equal(o1[0], out[m])
+
+
+def test_bad_arguments_raise_before_launch():
+    gemm, _ = _g()
+    a, as_ = H.engine_act(2, 96, seed=1)          # K not a multiple of 64
+    b, bs = H.engine_w8(96, 64, seed=2)
+    out = torch.empty((2, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        gemm.gemm_i8(a.cuda(), as_[:, :1].contiguous().cuda(), b.cuda(), bs.cuda(), out)
+    a, as_ = H.engine_act(2, 128, seed=1)
+    b, bs = H.engine_w8(128, 40, seed=2)          # N not a multiple of 16
+    out = torch.empty((2, 40), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)

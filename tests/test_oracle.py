@@ -1,0 +1,306 @@
+"""Pins the CPU oracle (oracle/ref_cpu.py) with checks that do not restate its formulas:
+brute force over all byte values, known answers, round trips, closed forms, an fp64
+recomputation in the reference kernel's own (blocked integer) form, and library
+routines (torch's bf16 cast, silu and round).  A few tests plant a plausible mistake
+in a copy of an oracle function and show that the pinning check catches it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref_cpu as R
+
+RNG = np.random.default_rng(1234)
+
+
+# ---------------------------------------------------------------- W4 nibble layout
+
+def _unpack_kat_ok(unpack) -> bool:
+    """Known answers for the nibble order: byte 0x8F holds k even = 15, k odd = 8."""
+    out = unpack(np.array([[0x8F, 0x07, 0xFF, 0x00]], dtype=np.uint8))
+    return (out[:, 0].tolist() == [15, 8] and out[:, 1].tolist() == [7, 0]
+            and out[:, 2].tolist() == [15, 15] and out[:, 3].tolist() == [0, 0])
+
+
+def test_unpack_all_bytes_brute_force():
+    b = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    nib = R.unpack_w4(b)
+    for v in range(256):
+        hi, lo = divmod(v, 16)
+        assert nib[0, v] == lo and nib[1, v] == hi
+
+
+def test_unpack_known_answers_and_signed_values():
+    assert _unpack_kat_ok(R.unpack_w4)
+    # symmetric grid z = 8 (kernels/w4.py:37): 0x8F -> (+7, 0), 0x07 -> (-1, -8)
+    s = R.w4_int(np.array([[0x8F, 0x07]], dtype=np.uint8))
+    assert s[:, 0].tolist() == [7, 0]
+    assert s[:, 1].tolist() == [-1, -8]
+
+
+def test_unpack_planted_mistake_is_caught():
+    def swapped(p):  # high nibble taken as the even k
+        out = R.unpack_w4(p)
+        return out.reshape(-1, 2, *out.shape[1:])[:, ::-1].reshape(out.shape)
+    assert not _unpack_kat_ok(swapped)
+
+
+def test_pack_unpack_round_trips():
+    nib = RNG.integers(0, 16, size=(64, 48), dtype=np.uint8)
+    assert np.array_equal(R.unpack_w4(R.pack_pairs(nib)), nib)
+    packed = RNG.integers(0, 256, size=(32, 48), dtype=np.uint8)
+    assert np.array_equal(R.pack_pairs(R.unpack_w4(packed)), packed)
+
+
+def test_w4_int_with_zeros_closed_forms():
+    packed = RNG.integers(0, 256, size=(64, 32), dtype=np.uint8)   # K = 128
+    nib = R.unpack_w4(packed)
+    G = 32
+    # z == nibble of the group's first row -> that row decodes to 0
+    z = nib[::G].copy()
+    v = R.w4_int(packed, z, G)
+    assert np.all(v[::G] == 0)
+    # z constant 8 == absent zeros
+    assert np.array_equal(R.w4_int(packed, np.full((4, 32), 8, np.uint8), G), R.w4_int(packed))
+
+
+# ---------------------------------------------------------------- dequant
+
+def test_dequant_w4_group_indexing_closed_form():
+    K, N, G = 256, 16, 64
+    nib = np.full((K, N), 9, dtype=np.uint8)              # value +1 everywhere
+    packed = R.pack_pairs(nib)
+    s = np.stack([np.full(N, 2.0 ** -g, np.float16) for g in range(K // G)])
+    d = R.dequant_w4_f32(packed, s)
+    for k in range(K):
+        assert np.all(d[k] == np.float32(2.0 ** -(k // G)))
+
+
+def test_dequant_w4_exact_vs_fp64():
+    K, N, G = 256, 64, 128
+    packed = RNG.integers(0, 256, size=(K // 2, N), dtype=np.uint8)
+    s = (np.abs(RNG.normal(0, 0.02, size=(K // G, N))) / 7).astype(np.float16)
+    z = RNG.integers(0, 16, size=(K // G, N), dtype=np.uint8)
+    d32 = R.dequant_w4_f32(packed, s, z)
+    nib = R.unpack_w4(packed).astype(np.float64)
+    d64 = (nib - np.repeat(z, G, 0)) * np.repeat(s.astype(np.float64), G, 0)
+    assert np.array_equal(d32.astype(np.float64), d64)       # exact in fp32
+    one = R.dequant_w4_f32(packed, np.ones_like(s), z)        # s = 1 -> integers
+    assert np.array_equal(one, (nib - np.repeat(z, G, 0)).astype(np.float32))
+
+
+def test_dequant_bf16_scales():
+    K, N = 64, 16
+    packed = RNG.integers(0, 256, size=(K // 2, N), dtype=np.uint8)
+    s32 = np.abs(RNG.normal(0, 0.02, size=(1, N))).astype(np.float32)
+    bits = torch.from_numpy(s32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    d = R.dequant_w4_f32(packed, bits)
+    s_back = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert np.array_equal(d, (R.unpack_w4(packed).astype(np.float32) - 8) * s_back)
+
+
+def test_dequant_w8_closed_form():
+    w = RNG.integers(-127, 128, size=(32, 16), dtype=np.int8)
+    s = RNG.random(16).astype(np.float32)
+    d = R.dequant_w8_f32(w, s)
+    # fp32 scales: one correctly rounded product per element
+    assert np.array_equal(d, (w.astype(np.float64) * s.astype(np.float64)).astype(np.float32))
+    # fp16 scales (11-bit significand) times int8 is exact in fp32
+    s16 = s.astype(np.float16)
+    d16 = R.dequant_w8_f32(w, s16)
+    assert np.array_equal(d16.astype(np.float64), w.astype(np.float64) * s16.astype(np.float64))
+
+
+# ---------------------------------------------------------------- GEMM
+
+def test_linear_w8_one_hot_selects_row():
+    K, N = 128, 32
+    w = RNG.integers(-127, 128, size=(K, N), dtype=np.int8)
+    s = (np.abs(RNG.normal(0, 0.02, N)) / 127).astype(np.float16)
+    for k in (0, 5, K - 1):
+        x = np.zeros((1, K), np.float16)
+        x[0, k] = 1
+        y = R.linear_w8_ref(x, w, s)
+        assert np.array_equal(y[0], w[k].astype(np.float32) * s.astype(np.float32))
+
+
+def test_linear_w8_vs_fp64_and_transpose_guard():
+    M, K, N = 3, 512, 96
+    x = RNG.normal(size=(M, K)).astype(np.float16)
+    w = RNG.integers(-127, 128, size=(K, N), dtype=np.int8)
+    s = (np.abs(RNG.normal(0, 0.02, N)) / 127).astype(np.float16)
+    y = R.linear_w8_ref(x, w, s)
+    y64 = (x.astype(np.float64) @ w.astype(np.float64)) * s.astype(np.float64)
+    assert R.max_rel_err(y, y64) < 1e-6
+    # a transposed operand (the config's logical [N, K] weight used unflipped) is far off
+    wt = np.ascontiguousarray(w[:N, :N].T)
+    assert R.max_rel_err(R.linear_w8_ref(x[:, :N], wt, s), y64[:, :N]) > 0.1
+
+
+def test_linear_w8_common_scale_factors_out():
+    M, K, N = 2, 256, 64
+    x = RNG.normal(size=(M, K)).astype(np.float16)
+    w = RNG.integers(-127, 128, size=(K, N), dtype=np.int8)
+    c = np.float16(0.0078125)
+    y = R.linear_w8_ref(x, w, np.full(N, c, np.float16))
+    y_int = x.astype(np.float64) @ w.astype(np.float64)
+    assert R.max_rel_err(y, y_int * float(c)) < 1e-6
+
+
+def _gemm_i8_blocked_fp64(a_q, a_s, b, b_s):
+    """The reference kernel's form (kernels/gemm.py:40-52): exact integer dot per
+    64-block, scaled per block, per-column scale at the end -- in fp64."""
+    M, K = a_q.shape
+    acc = np.zeros((M, b.shape[1]))
+    for kb in range(K // 64):
+        sl = slice(64 * kb, 64 * kb + 64)
+        i32 = a_q[:, sl].astype(np.int64) @ b[sl].astype(np.int64)
+        acc += i32 * a_s[:, kb:kb + 1].astype(np.float64)
+    return acc * b_s.astype(np.float64)[None, :]
+
+
+def test_gemm_i8_vs_blocked_integer_form():
+    M, K, N = 5, 512, 128
+    a_q = RNG.integers(-127, 127, size=(M, K), dtype=np.int8)
+    a_s = (RNG.random((M, K // 64)) * 0.02).astype(np.float32)
+    b = RNG.integers(-127, 127, size=(K, N), dtype=np.int8)
+    b_s = (RNG.random(N) * 0.002).astype(np.float32)
+    y = R.gemm_i8_ref(a_q, a_s, b, b_s)
+    assert R.max_rel_err(y, _gemm_i8_blocked_fp64(a_q, a_s, b, b_s)) < 1e-6
+
+
+def test_gemm_i8_planted_scale_index_mistake_is_caught():
+    M, K, N = 2, 256, 32
+    a_q = RNG.integers(-127, 127, size=(M, K), dtype=np.int8)
+    a_s = (RNG.random((M, K // 64)) * 0.02 + 0.001).astype(np.float32)
+    b = RNG.integers(-127, 127, size=(K, N), dtype=np.int8)
+    b_s = (RNG.random(N) * 0.002 + 1e-4).astype(np.float32)
+    ref = _gemm_i8_blocked_fp64(a_q, a_s, b, b_s)
+    # scale per 64 columns of K taken with np.tile instead of repeat
+    bad = (a_q.astype(np.float32) * np.tile(a_s, (1, 64))) @ R.dequant_w8_f32(b, b_s)
+    assert R.max_rel_err(bad, ref) > 1e-2
+
+
+def _gemm_w4_blocked_fp64(a_q, a_s, b, b_s, b_z=None):
+    """kernels/w4.py:64-104 form: per sub-block of min(G, 64) K values, exact integer
+    dot, times (a_s * w_s)."""
+    M, K = a_q.shape
+    N = b.shape[1]
+    G = K // b_s.shape[0]
+    sub = min(G, 64)
+    q = R.w4_int(b, b_z, G).astype(np.int64)
+    s = R.scale_to_f32(b_s).astype(np.float64)
+    acc = np.zeros((M, N))
+    for k0 in range(0, K, sub):
+        i32 = a_q[:, k0:k0 + sub].astype(np.int64) @ q[k0:k0 + sub]
+        acc += i32 * (a_s[:, k0 // 64][:, None].astype(np.float64) * s[k0 // G][None, :])
+    return acc
+
+
+@pytest.mark.parametrize("G", [32, 64, 128])
+def test_gemm_w4_vs_blocked_integer_form(G):
+    M, K, N = 4, 256, 64
+    a_q = RNG.integers(-127, 127, size=(M, K), dtype=np.int8)
+    a_s = (RNG.random((M, K // 64)) * 0.02).astype(np.float32)
+    b = RNG.integers(0, 256, size=(K // 2, N), dtype=np.uint8)
+    b_s = (np.abs(RNG.normal(0, 0.02, size=(K // G, N))) / 7).astype(np.float16)
+    z = RNG.integers(0, 16, size=(K // G, N), dtype=np.uint8)
+    for zz in (None, z):
+        y = R.gemm_w4_ref(a_q, a_s, b, b_s, b_z=zz)
+        assert R.max_rel_err(y, _gemm_w4_blocked_fp64(a_q, a_s, b, b_s, zz)) < 1e-6
+
+
+def test_proj3_is_column_concatenation():
+    M, K = 3, 128
+    a_q = RNG.integers(-127, 127, size=(M, K), dtype=np.int8)
+    a_s = (RNG.random((M, K // 64)) * 0.02).astype(np.float32)
+    ws = [RNG.integers(-127, 127, size=(K, n), dtype=np.int8) for n in (64, 32, 16)]
+    ss = [(RNG.random(w.shape[1]) * 0.002).astype(np.float32) for w in ws]
+    y = R.proj3_ref(a_q, a_s, ws[0], ss[0], ws[1], ss[1], ws[2], ss[2])
+    assert y.shape == (M, 112)
+    assert np.array_equal(y[:, 64:96], R.gemm_i8_ref(a_q, a_s, ws[1], ss[1]))
+    y2 = R.proj3_ref(a_q, a_s, ws[0], ss[0], ws[1], ss[1], None, None)
+    assert np.array_equal(y2, y[:, :96])
+
+
+# ---------------------------------------------------------------- epilogue pieces
+
+def test_silu_matches_torch():
+    x = RNG.normal(0, 4, size=1000).astype(np.float32)
+    ref = torch.nn.functional.silu(torch.from_numpy(x)).numpy()
+    assert np.allclose(R.silu(x), ref, rtol=2e-6, atol=1e-7)
+
+
+def test_round_i8_known_answers():
+    v = np.array([0.5, -0.5, 1.5, 2.5, -2.5, 0.4, -0.4, 126.5, 127.49, 128.0, 1000.0, -1000.0,
+                  0.49999997], dtype=np.float32)
+    want = [1, -1, 2, 3, -3, 0, 0, 127, 127, 127, 127, -127, 1]
+    assert R.round_i8(v).tolist() == want
+
+
+def test_round_i8_planted_half_even_is_caught():
+    v = np.array([0.5, 2.5, -2.5], dtype=np.float32)
+    assert np.rint(v).astype(np.int8).tolist() != R.round_i8(v).tolist()
+
+
+def test_bf16_cast_matches_torch():
+    x = np.concatenate([RNG.normal(size=4096).astype(np.float32),
+                        np.array([np.inf, -np.inf, 0.0, -0.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8,
+                                  3.4e38, 1e-40], np.float32)])
+    t = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(R.f32_to_bf16_bits(x), t)
+    nan = R.f32_to_bf16_bits(np.array([np.nan], np.float32))
+    assert np.isnan(R.bf16_bits_to_f32(nan))[0]
+
+
+def test_quant_groups_invariants():
+    h = RNG.normal(size=(4, 256)).astype(np.float32)
+    h[1, 64:128] = 0.0
+    q, s = R.quant_groups(h)
+    assert q.dtype == np.int8 and s.shape == (4, 4)
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    assert s[1, 1] == np.float32(1e-8) and np.all(q[1, 64:128] == 0)
+    g = np.abs(q.astype(np.int32)).reshape(4, 4, 64).max(axis=2)
+    assert np.all(g[s > 1e-8] == 127)
+    err = np.abs(q.astype(np.float32) * np.repeat(s, 64, 1) - h)
+    assert np.all(err <= 0.5 * np.repeat(s, 64, 1) * (1 + 1e-5))
+
+
+def test_gate_up_quant_is_the_unfused_composition():
+    M, K, N = 3, 128, 128
+    a_q = RNG.integers(-127, 127, size=(M, K), dtype=np.int8)
+    a_s = (RNG.random((M, K // 64)) * 0.02).astype(np.float32)
+    wg = RNG.integers(-127, 127, size=(K, N), dtype=np.int8)
+    wu = RNG.integers(-127, 127, size=(K, N), dtype=np.int8)
+    sg = (RNG.random(N) * 0.002).astype(np.float32)
+    su = (RNG.random(N) * 0.002).astype(np.float32)
+    h = R.mlp_gate_up_ref(a_q, a_s, wg, sg, wu, su)
+    g = R.gemm_i8_ref(a_q, a_s, wg, sg)
+    u = R.gemm_i8_ref(a_q, a_s, wu, su)
+    ref = torch.nn.functional.silu(torch.from_numpy(g)).numpy() * u
+    assert np.allclose(h, ref, rtol=1e-5, atol=1e-7)
+    q, s = R.mlp_gate_up_quant_ref(a_q, a_s, wg, sg, wu, su)
+    q2, s2 = R.quant_groups(R.round_bf16(h))
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+# ---------------------------------------------------------------- load-time producers
+
+def test_requant_w4_sym_recovers_exact_grid():
+    K, N, G = 64, 16, 32
+    q = RNG.integers(1, 16, size=(K, N)).astype(np.uint8)   # |q - 8| <= 7 (amax / 7 grid)
+    q[0], q[G] = 15, 1                        # each group reaches |q - 8| = 7
+    s = np.full((K // G, N), 2.0 ** -7, np.float32)
+    w = (q.astype(np.float32) - 8) * np.repeat(s, G, 0)
+    packed, sbits = R.requant_w4_sym(w, G)
+    assert np.array_equal(packed, R.pack_pairs(q))
+    assert np.array_equal(R.bf16_bits_to_f32(sbits), s)
+
+
+def test_requant_rounding_matches_torch_round():
+    w = np.array([[0.5], [1.5], [2.5], [-2.5], [127.0]], dtype=np.float32) * np.float32(1 / 127)
+    q, sc = R.requant_w8_row(w)
+    ref = torch.clamp(torch.round(torch.from_numpy(w) / torch.from_numpy(sc)[None, :]), -127, 127)
+    assert np.array_equal(q.astype(np.float32), ref.numpy())
