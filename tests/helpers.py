@@ -98,3 +98,32 @@ def linear_w4_ref_cols(x, packed, s, z, cols, residual=None):
 
 def to_f32(t) -> np.ndarray:
     return t.detach().float().cpu().numpy()
+
+
+def half_ulp(ref, dtype) -> np.ndarray:
+    """Half a unit in the last place of `ref` in the 16-bit output type."""
+    mant = {torch.float16: 10, torch.bfloat16: 7}[dtype]
+    a = np.abs(np.asarray(ref, dtype=np.float64))
+    _, e = np.frexp(a)                      # a = m * 2**e, m in [0.5, 1)
+    ulp = np.ldexp(1.0, e - 1 - mant)
+    if dtype == torch.float16:
+        ulp = np.maximum(ulp, 2.0 ** -24)  # subnormal spacing
+    return 0.5 * ulp
+
+
+def assert_out_close(y: torch.Tensor, ref, tol: float = 2e-3) -> None:
+    """The kernel's result must be within `tol * max|ref|` of the fp32 oracle before
+    it is rounded to the 16-bit output type; the rounding adds at most half an ulp.
+    (A bf16 output alone carries up to 2**-8 relative rounding, so a plain 2e-3
+    normalized bound could not hold for it.)"""
+    y32 = y.detach().float().cpu().numpy().astype(np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    allowed = tol * np.abs(ref).max() + half_ulp(ref, y.dtype)
+    err = np.abs(y32 - ref)
+    bad = err > allowed
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - allowed), err.shape)
+        raise AssertionError(
+            f"{int(bad.sum())} elements out of tolerance; worst at {i}: y={y32[i]} ref={ref[i]} "
+            f"allowed={allowed[i]:.3e}; max_rel_err={R.max_rel_err(y32, ref):.3e} "
+            f"rel_l2={R.rel_l2(y32, ref):.3e}")
