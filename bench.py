@@ -1,0 +1,453 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode-w8]
+
+Default workload (`decode-w8`): INT8 per-channel, fp16-activation decode GEMVs over
+every linear shape of one 2B-class hybrid layer -- q/o (2048,2048), k/v (2048,512),
+gate/up (2048,6144), down (6144,2048), linear-attention in/out (2048,4096) and
+(4096,2048) -- plus the vocabulary head (2048,248320), at M = 1, 2 and 4 rows.
+One step runs all of them once per M.  The layer weights exist in `--layers`
+distinct copies (default 8, about 0.5 GB, like consecutive layers of a model), so
+every launch streams its weights from HBM rather than the 256 MB last-level cache.
+
+The layer launches of one M are replayed as one HIP graph; the vocabulary-head
+launch stays eager with HIP events around it on its launch stream, which gives the
+dominant kernel's live per-launch time for the roofline object.
+
+Other workloads (`--workload`): decode-w4 (same shapes, W4 group 128), prefill
+(M in 128/512/2048, TFLOP/s), chain-w4 (9B-class 32-layer W4 decode chain), single
+(one 2048x6144 int8 linear, M=1).
+
+Prints ONE JSON line (rank 0).  Synthetic data; weights are random in the engine
+layouts.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG_DIR = ROOT / "qwen_3.5_comfy_prompt_enhancer_amd"
+ALIAS = "qwen35_amd"
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, TFLOP/s
+
+METRIC = "W8/W4 decode GEMV HBM GB/s (% peak) at M=1-4; prefill GEMM TFLOPS"
+
+LAYER_SHAPES = [  # (name, K, N) of one 2B-class hybrid layer
+    ("q", 2048, 2048), ("k", 2048, 512), ("v", 2048, 512), ("o", 2048, 2048),
+    ("gate", 2048, 6144), ("up", 2048, 6144), ("down", 6144, 2048),
+    ("lin_in", 2048, 4096), ("lin_out", 4096, 2048),
+]
+HEAD = ("lm_head", 2048, 248320)
+CHAIN_SHAPES = [  # 9B-class layer
+    ("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
+    ("gate", 4096, 12288), ("up", 4096, 12288), ("down", 12288, 4096),
+]
+CHAIN_HEAD = ("lm_head", 4096, 248320)
+PREFILL_SHAPES = [("gate", 2048, 6144), ("down", 6144, 2048), ("q", 2048, 2048)]
+
+
+def _load_package():
+    if ALIAS in sys.modules:
+        return sys.modules[ALIAS]
+    spec = importlib.util.spec_from_file_location(
+        ALIAS, PKG_DIR / "__init__.py", submodule_search_locations=[str(PKG_DIR)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[ALIAS] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ algorithmic bytes
+
+def bytes_w8(M, K, N):
+    """int8 weights + fp16 per-column scales + fp16 activations in + fp16 out."""
+    return K * N + 2 * N + 2 * M * K + 2 * M * N
+
+
+def bytes_w4(M, K, N, G=128):
+    """packed nibbles + fp16 group scales + fp16 activations in + fp16 out."""
+    return K * N // 2 + 2 * (K // G) * N + 2 * M * K + 2 * M * N
+
+
+# ------------------------------------------------------------------ weights
+
+class Weights:
+    def __init__(self, kind, K, N, dev, gen, group=128):
+        import torch
+        self.kind, self.K, self.N = kind, K, N
+        if kind == "w8":
+            self.w = torch.randint(-127, 128, (K, N), generator=gen, dtype=torch.int8).to(dev)
+            self.s = ((torch.randn(N, generator=gen) * 0.02).abs() / 127).to(torch.float16).to(dev)
+        else:
+            self.w = torch.randint(0, 256, (K // 2, N), generator=gen, dtype=torch.uint8).to(dev)
+            self.s = ((torch.randn((K // group, N), generator=gen) * 0.02).abs() / 7).to(torch.float16).to(dev)
+
+    def run(self, lin, x, out):
+        if self.kind == "w8":
+            lin.linear_w8(x, self.w, self.s, out)
+        else:
+            lin.linear_w4(x, self.w, self.s, out)
+
+    def nbytes(self, M):
+        return bytes_w8(M, self.K, self.N) if self.kind == "w8" else bytes_w4(M, self.K, self.N)
+
+
+# ------------------------------------------------------------------ decode sweep
+
+def decode_sweep(args, kind, shapes, head, ms, layers):
+    """Returns (total_bytes_per_step, step_fn, head_events, head_bytes_by_m)."""
+    import torch
+    dev = torch.device("cuda", 0)
+    lin = importlib.import_module(f"{ALIAS}.kernels.linear")
+    gen = torch.Generator().manual_seed(1234)
+    lw = [[Weights(kind, K, N, dev, gen) for (_, K, N) in shapes] for _ in range(layers)]
+    hw = Weights(kind, head[1], head[2], dev, gen)
+    kmax = max(max(K for _, K, _ in shapes), head[1])
+    xs = {M: torch.randn((M, kmax), generator=gen).to(torch.float16).to(dev) for M in ms}
+    outs = {M: [torch.empty((M, N), dtype=torch.float16, device=dev) for (_, _, N) in shapes] for M in ms}
+    hout = {M: torch.empty((M, head[2]), dtype=torch.float16, device=dev) for M in ms}
+
+    def xin(M, K):
+        return xs[M][:, :K]
+
+    def run_layers(M):
+        for l in range(layers):
+            for i, (_, K, _) in enumerate(shapes):
+                lw[l][i].run(lin, xin(M, K), outs[M][i])
+
+    # eager warm-up (allocates the workspace outside capture), then capture per M
+    for M in ms:
+        run_layers(M)
+        hw.run(lin, xin(M, head[1]), hout[M])
+    torch.cuda.synchronize()
+    graphs = {}
+    if not args.no_graph:
+        for M in ms:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                run_layers(M)
+            graphs[M] = g
+        torch.cuda.synchronize()
+
+    head_ev = {M: [] for M in ms}
+    record = {"on": False}
+
+    def step():
+        for M in ms:
+            if graphs:
+                graphs[M].replay()
+            else:
+                run_layers(M)
+            if record["on"]:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                hw.run(lin, xin(M, head[1]), hout[M])
+                e1.record()
+                head_ev[M].append((e0, e1))
+            else:
+                hw.run(lin, xin(M, head[1]), hout[M])
+
+    total = sum(layers * sum(w.nbytes(M) for w in lw[0]) + hw.nbytes(M) for M in ms)
+    head_bytes = {M: hw.nbytes(M) for M in ms}
+    return total, step, head_ev, head_bytes, record, (lw, hw, xs, outs, hout, lin)
+
+
+def time_steps(step, steps, warmup, record=None):
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    if record is not None:
+        record["on"] = True
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    if record is not None:
+        record["on"] = False
+    return (t1 - t0) / steps
+
+
+def detail_table(ctx, kind, shapes, head, ms, reps=40):
+    """Per-shape GPU time (stderr only): a HIP graph of `reps` launches of one shape,
+    rotating over the layer copies, timed with events around its replay."""
+    import torch
+    lw, hw, xs, outs, hout, lin = ctx
+    layers = max(1, len(lw))
+    rows = []
+    for M in ms:
+        for i, (name, K, N) in enumerate(list(shapes) + [head]):
+            is_head = i == len(shapes)
+            n = 4 if is_head else reps
+
+            def body():
+                for r in range(n):
+                    w = hw if is_head else lw[r % layers][i]
+                    w.run(lin, xs[M][:, :K], hout[M] if is_head else outs[M][i])
+            body()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                body()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(3):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (3 * n)
+            b = (hw if is_head else lw[0][i]).nbytes(M)
+            rows.append((M, name, K, N, us, b / us / 1e3))
+    log(f"{'M':>2} {'shape':>8} {'K':>6} {'N':>7} {'us':>9} {'GB/s':>8} {'%peak':>6}")
+    for M, name, K, N, us, gbs in rows:
+        log(f"{M:>2} {name:>8} {K:>6} {N:>7} {us:9.2f} {gbs:8.0f} {100 * gbs / HBM_PEAK_GBS:6.1f}")
+
+
+# ------------------------------------------------------------------ prefill
+
+def prefill_bench(args):
+    import torch
+    dev = torch.device("cuda", 0)
+    lin = importlib.import_module(f"{ALIAS}.kernels.linear")
+    gen = torch.Generator().manual_seed(99)
+    ms = [128, 512, 2048]
+    items = []
+    for kind in ("w8", "w4"):
+        for (name, K, N) in PREFILL_SHAPES:
+            w = Weights(kind, K, N, dev, gen)
+            for M in ms:
+                x = torch.randn((M, K), generator=gen).to(torch.float16).to(dev)
+                o = torch.empty((M, N), dtype=torch.float16, device=dev)
+                items.append((kind, name, M, K, N, w, x, o))
+
+    def step():
+        for (_, _, _, _, _, w, x, o) in items:
+            w.run(lin, x, o)
+
+    flops = sum(2 * M * K * N for (_, _, M, K, N, _, _, _) in items)
+    t = time_steps(step, args.steps, args.warmup)
+    if args.detail:
+        for (kind, name, M, K, N, w, x, o) in items:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                w.run(lin, x, o)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 100
+            log(f"{kind} {name:>5} M={M:5d} K={K} N={N}: {us:9.1f} us {2 * M * K * N / us / 1e6:8.1f} TFLOP/s")
+    return flops, t
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(kind, shapes, head, budget_s=15.0):
+    """The oracle's CPU path (dequantize to fp32, then an fp32 matmul) on a bounded
+    sample of the decode workload: M = 1, every layer shape once, and 1/8 of the
+    vocabulary-head columns; GB/s over the same algorithmic bytes as the GPU."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    if str(ROOT) not in sys.path:
+        sys.path.insert(0, str(ROOT))
+    from oracle import ref_cpu as R
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    rng = np.random.default_rng(5)
+    sample = list(shapes) + [(head[0] + "/8", head[1], head[2] // 8)]
+    tot_b = tot_t = t_deq = 0.0
+    with threadpool_limits(limits=cores):
+        deadline = time.perf_counter() + budget_s
+        reps = 0
+        while True:
+            for (_, K, N) in sample:
+                x = rng.standard_normal((1, K)).astype(np.float16)
+                if kind == "w8":
+                    w = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
+                    s = (np.abs(rng.normal(0, 0.02, N)) / 127).astype(np.float16)
+                    t0 = time.perf_counter()
+                    wd = R.dequant_w8_f32(w, s)
+                    t1 = time.perf_counter()
+                    R.linear_ref(x, wd)
+                    t2 = time.perf_counter()
+                    b = bytes_w8(1, K, N)
+                else:
+                    w = rng.integers(0, 256, size=(K // 2, N), dtype=np.uint8)
+                    s = (np.abs(rng.normal(0, 0.02, (K // 128, N))) / 7).astype(np.float16)
+                    t0 = time.perf_counter()
+                    wd = R.dequant_w4_f32(w, s)
+                    t1 = time.perf_counter()
+                    R.linear_ref(x, wd)
+                    t2 = time.perf_counter()
+                    b = bytes_w4(1, K, N)
+                tot_b += b
+                tot_t += t2 - t0
+                t_deq += t1 - t0
+            reps += 1
+            if time.perf_counter() > deadline:
+                break
+    return {
+        "value": round(tot_b / tot_t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"M=1 decode of every layer shape plus 1/8 of the vocab-head columns, {kind}, "
+                   f"{reps} pass(es); numpy oracle: dequantize to fp32 (single thread, "
+                   f"{100 * t_deq / tot_t:.0f}% of the time) then fp32 matmul (BLAS, {cores} threads)"),
+    }
+
+
+# ------------------------------------------------------------------ counter runs
+
+def head_pmc(args):
+    """For `rocprofv3 --pmc` runs: a few launches of the vocabulary-head GEMVs (W8
+    and W4 g128, M=1) and, as the known-size calibration for the byte counters, a
+    1 GiB device-to-device copy (torch's copy kernel: 1 GiB read, 1 GiB written)."""
+    import torch
+    dev = torch.device("cuda", 0)
+    lin = importlib.import_module(f"{ALIAS}.kernels.linear")
+    gen = torch.Generator().manual_seed(7)
+    _, K, N = HEAD
+    x = torch.randn((1, K), generator=gen).to(torch.float16).to(dev)
+    out = torch.empty((1, N), dtype=torch.float16, device=dev)
+    for kind in ("w8", "w4"):
+        w = Weights(kind, K, N, dev, gen)
+        for _ in range(args.steps):
+            w.run(lin, x, out)
+        del w
+    a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "head-pmc", "w8_bytes_per_launch": bytes_w8(1, K, N),
+                      "w4_bytes_per_launch": bytes_w4(1, K, N), "copy_bytes": 1 << 30}), flush=True)
+    return 0
+
+
+# ------------------------------------------------------------------ main
+
+def read_traffic(kernel_tag):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc
+    summary (profiles/vocab_head_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE, each scaled
+    by the reading of a known-size copy), or None."""
+    p = ROOT / "profiles" / "vocab_head_hbm_traffic.md"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith(f"traffic_bytes_per_launch[{kernel_tag}]"):
+            try:
+                return int(line.split("=")[1].split()[0])
+            except (IndexError, ValueError):
+                return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="decode-w8",
+                    choices=["decode-w8", "decode-w4", "prefill", "chain-w4", "single", "head-pmc"])
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--detail", action="store_true", help="per-shape table on stderr")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU (the path has no multi-GPU part); "
+              "run it with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    _load_package()
+    from qwen35_amd.kernels import common
+    common.lib()
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU", file=sys.stderr)
+        return 1
+
+    wl = args.workload
+    if wl == "head-pmc":
+        return head_pmc(args)
+    ms = [1, 2, 4]
+    roof = None
+    if wl in ("decode-w8", "decode-w4", "chain-w4", "single"):
+        kind = "w4" if wl in ("decode-w4", "chain-w4") else "w8"
+        if wl == "chain-w4":
+            shapes, head, layers, ms = CHAIN_SHAPES, CHAIN_HEAD, 32, [1, 4]
+        elif wl == "single":
+            shapes, head, layers, ms = [], ("gate", 2048, 6144), 0, [1]
+        else:
+            shapes, head, layers = LAYER_SHAPES, HEAD, args.layers
+        total, step, head_ev, head_bytes, record, ctx = decode_sweep(args, kind, shapes, head, ms, layers)
+        t = time_steps(step, args.steps, args.warmup, record)
+        value = total / t / 1e9
+        # dominant kernel: the vocabulary-head GEMV, every launch of the timed steps
+        # (M = 1, 2, 4), timed live with HIP events on its launch stream
+        durs = [(M, e0.elapsed_time(e1) * 1e-3) for M in ms for (e0, e1) in head_ev[M]]
+        dur = sum(d for _, d in durs) / len(durs)
+        hb = sum(head_bytes[M] for M, _ in durs) / len(durs)
+        achieved = hb / dur / 1e9
+        tag = f"{kind}-{head[1]}x{head[2]}"
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(tag),
+                "kernel": f"skinny_kernel {kind} vocab head {head[1]}x{head[2]}, M={'/'.join(map(str, ms))}",
+                "bytes_per_launch": int(hb), "avg_launch_us": round(dur * 1e6, 2)}
+        if args.detail:
+            detail_table(ctx, kind, shapes, head, ms)
+        per_m = {M: sum(e0.elapsed_time(e1) for e0, e1 in head_ev[M]) / len(head_ev[M]) for M in ms}
+        log("vocab head per-launch us by M: " + ", ".join(f"M={M}: {v * 1e3:.1f}" for M, v in per_m.items()))
+        unit = "GB/s"
+        config = {"workload": {"decode-w8": "int8 decode GEMV sweep, 2B-class layer shapes + vocab head",
+                               "decode-w4": "W4 g128 decode GEMV sweep, 2B-class layer shapes + vocab head",
+                               "chain-w4": "9B-class W4 g128 decode chain: 32 layers + vocab head",
+                               "single": "single int8 linear 2048x6144"}[wl],
+                  "rows_M": ms, "layer_copies": layers,
+                  "shapes_KN": [[K, N] for (_, K, N) in shapes] + [[head[1], head[2]]],
+                  "bytes_per_step": total,
+                  "launch": "hipgraph per M for layer shapes, eager vocab head" if not args.no_graph else "eager"}
+        dtype = "f16 x int8" if kind == "w8" else "f16 x int4"
+    else:
+        flops, t = prefill_bench(args)
+        value = flops / t / 1e12
+        unit = "TFLOP/s"
+        config = {"workload": "prefill GEMM, int8 and W4 g128, M in 128/512/2048",
+                  "shapes_KN": [[K, N] for (_, K, N) in PREFILL_SHAPES], "flops_per_step": flops}
+        dtype = "f16 x int8/int4"
+
+    cpu = None
+    if not args.no_cpu_baseline and wl in ("decode-w8", "decode-w4"):
+        cpu = cpu_baseline("w8" if wl == "decode-w8" else "w4", LAYER_SHAPES, HEAD, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": unit, "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic (seeded random weights in the engine layouts)", "config": config,
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

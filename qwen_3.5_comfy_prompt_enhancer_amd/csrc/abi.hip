@@ -5,6 +5,7 @@
 // waves per workgroup, split-K) is chosen here from K and N.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "../../include/qlin.h"
@@ -33,8 +34,12 @@ int hip_status(const char* fn, hipError_t e) {
 // Workspace: [counters | partial sums].  Counters must be zero between calls.
 constexpr size_t kWorkspaceBytes = size_t(64) << 20;
 constexpr size_t kCounterBytes = size_t(1) << 20;
-constexpr int kTargetWorkgroups = 256;  // one per CU for the split-K heuristic
-constexpr int kWideTiles = 512;         // column tiles at which no K split is needed
+constexpr int kWideTiles = 512;          // 256-column tiles at which no K split is needed
+// narrow launches: most waves to spread K over, and least K per wave (measured)
+constexpr long long kTargetWavesW8 = 256;
+constexpr long long kTargetWavesW4 = 1024;
+constexpr int kMinWaveKW8 = 256;
+constexpr int kMinWaveKW4 = 128;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 bool dtype_scale_ok(int dt) { return dt == QLIN_F16 || dt == QLIN_BF16 || dt == QLIN_F32; }
@@ -50,6 +55,22 @@ struct Problem {
 };
 
 // Fills L (kernel variant, grid, LDS) and a.kchunk / a.splits / a.ntiles / seg tiles.
+// Launch-plan override for tuning sweeps: QLIN_SKINNY_PLAN="cols,waves,units" (0 keeps
+// the default for that field; units = K granules of one wave).  Unset in normal use.
+void plan_override(bool store_epi, int& cols, int& waves, int& upw) {
+  const char* e = getenv("QLIN_SKINNY_PLAN");
+  if (!e || !*e) return;
+  int c = 0, w = 0, u = 0;
+  if (sscanf(e, "%d,%d,%d", &c, &w, &u) != 3) return;
+  if (c == 8 || c == 16) cols = c;
+  if (!store_epi) cols = 8;  // gate/up kernels exist with 8-column tiles only
+  if (w >= 1 && w <= 4) waves = w;
+  if (u >= 1) upw = u;
+}
+
+// Chooses the kernel variant, column tile, waves per workgroup and split-K, then launches.
+// Every choice depends on K, N (and whether M > 16), never on M itself, so an output row
+// is computed the same way for every M <= 16.
 int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
                     hipStream_t stream) {
   SkLaunch L;
@@ -57,38 +78,58 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   L.wk = P.wk;
   L.hz = P.hz ? 1 : 0;
   L.epi = P.epi;
-  L.cols = (P.epi == EPI_STORE) ? 16 : 8;
-  const int TN = 16 * L.cols;
 
-  // column tiles per segment
-  int ntiles = 0;
-  for (int s = 0; s < a.nseg; ++s) {
-    a.seg[s].tile0 = ntiles;
-    if (P.epi == EPI_STORE) ntiles += (a.seg[s].n + TN - 1) / TN;
-  }
-  if (P.epi != EPI_STORE) {
-    ntiles = (a.seg[0].n + TN - 1) / TN;
-    a.seg[0].tile0 = a.seg[1].tile0 = 0;
-  }
-  a.ntiles = ntiles;
-
-  // K granularity of one wave's range
+  auto count_tiles = [&](int tn) {
+    int nt = 0;
+    if (P.epi == EPI_STORE) {
+      for (int s = 0; s < a.nseg; ++s) nt += (a.seg[s].n + tn - 1) / tn;
+    } else {
+      nt = (a.seg[0].n + tn - 1) / tn;
+    }
+    return nt;
+  };
+  // K granule of one wave's range: the MFMA step, the activation group (int8) and
+  // whole W4 weight groups
   int kalign = (P.act == ACT_I8) ? 64 : 32;
   if (P.wk == WK_W4 && P.group > kalign) kalign = P.group;
   const int nunits = P.K / kalign;
   const int rtiles = (P.M + 15) / 16;
+  const bool wide = P.M > 16 || count_tiles(256) >= kWideTiles;
 
-  int waves, splits;
-  if (P.M > 16 || ntiles >= kWideTiles) {
-    // enough column tiles (or row tiles) to fill the chip: the waves of one
-    // workgroup share K and no cross-workgroup split is needed
-    waves = nunits < 4 ? nunits : 4;
-    splits = 1;
+  // Measured on MI355X: wide W8 launches stream best as single-wave workgroups over
+  // 128-column tiles, wide W4 over 256-column tiles; narrow launches as 4-wave
+  // workgroups over 128-column tiles.
+  int cols = (wide && P.wk == WK_W4 && P.epi == EPI_STORE && P.M <= 16) ? 16 : 8;
+  int waves = (wide && P.M <= 16) ? 1 : 4, upw = 0;
+  plan_override(P.epi == EPI_STORE, cols, waves, upw);
+  const int TN = 16 * cols;
+  const int ntiles = count_tiles(TN);
+  int ntile_acc = 0;
+  for (int s = 0; s < a.nseg; ++s) {
+    a.seg[s].tile0 = (P.epi == EPI_STORE) ? ntile_acc : 0;
+    if (P.epi == EPI_STORE) ntile_acc += (a.seg[s].n + TN - 1) / TN;
+  }
+  a.ntiles = ntiles;
+
+  int splits;
+  if (wide) {
+    if (waves > nunits) waves = nunits;
+    if (upw == 0) upw = (nunits + waves - 1) / waves;
+    splits = (nunits + upw * waves - 1) / (upw * waves);
+    if (P.M > 16) splits = 1, upw = (nunits + waves - 1) / waves;
   } else {
-    // narrow N: split K over single-wave workgroups to reach ~kTargetWorkgroups
-    waves = 1;
-    splits = (kTargetWorkgroups + ntiles - 1) / ntiles;
-    if (splits > nunits) splits = nunits;
+    // narrow N: spread K over up to kTargetWaves waves, each at least kMinWaveK deep
+    const long long target = (P.wk == WK_W4) ? kTargetWavesW4 : kTargetWavesW8;
+    const int min_k = (P.wk == WK_W4) ? kMinWaveKW4 : kMinWaveKW8;
+    const int min_upw = (min_k + kalign - 1) / kalign;
+    if (upw == 0) {
+      upw = (int)(((long long)ntiles * nunits + target - 1) / target);
+      if (upw < min_upw) upw = min_upw;
+    }
+    if (upw > nunits) upw = nunits;
+    const int chunks = (nunits + upw - 1) / upw;  // waves per tile
+    if (waves > chunks) waves = chunks;
+    splits = (chunks + waves - 1) / waves;
   }
   // partial sums must fit the workspace; without a workspace there is no cross-workgroup split
   const size_t part_cap = (workspace && ws_bytes > kCounterBytes) ? ws_bytes - kCounterBytes : 0;
@@ -97,10 +138,15 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
     const size_t cnt_need = (size_t)rtiles * ntiles * sizeof(unsigned);
     return need <= part_cap && cnt_need <= kCounterBytes;
   };
-  while (splits > 1 && !fits(splits)) splits = (splits + 1) / 2;
-  const int units_per_wave = (nunits + splits * waves - 1) / (splits * waves);
-  splits = (nunits + units_per_wave * waves - 1) / (units_per_wave * waves);
-  a.kchunk = units_per_wave * kalign;
+  while (splits > 1 && !fits(splits)) {
+    upw *= 2;
+    splits = (nunits + upw * waves - 1) / (upw * waves);
+  }
+  if (splits <= 1) {
+    splits = 1;
+    upw = (nunits + waves - 1) / waves;
+  }
+  a.kchunk = upw * kalign;
   a.splits = splits;
   if (splits > 1) {
     a.cnt = (unsigned*)workspace;
@@ -109,9 +155,10 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
     a.cnt = nullptr;
     a.part = nullptr;
   }
+  L.cols = cols;
   L.waves = waves;
   L.grid = dim3((unsigned)(ntiles * splits), (unsigned)rtiles, 1);
-  L.lds = (waves > 1) ? (size_t)P.nsets * L.cols * 1024 : 0;
+  L.lds = (waves > 1 || splits > 1) ? (size_t)P.nsets * cols * 1024 : 0;
   if ((long long)ntiles * splits > 0x7FFFFFFFLL || rtiles > 65535)
     return fail(QLIN_ERR_UNSUPPORTED, "%s: grid too large (M=%d, N=%d)", fn, P.M, P.ncols);
   return hip_status(fn, launch_skinny(L, a, stream));

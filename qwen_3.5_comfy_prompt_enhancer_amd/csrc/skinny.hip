@@ -23,9 +23,13 @@
 //     kernels/w4.py:103-104).
 //   * The K dimension is split over the `waves` of a workgroup (reduced in LDS in a
 //     fixed order) and over `splits` workgroups (fp32 partials in the caller's
-//     workspace; the last workgroup to arrive at a per-tile counter sums them in
-//     split order and resets the counter).  Split choices depend on K and N only,
-//     so each output row is computed identically for every M <= 16.
+//     workspace, written and read as agent-scope atomics; the last workgroup to
+//     arrive at a per-tile counter sums them in split order and resets the counter).
+//     Split choices depend on K and N only, so each output row is computed
+//     identically for every M <= 16.
+//   * Every load of a 32-wide K step is issued D steps ahead from a register ring.
+#include <type_traits>
+
 #include "qlin_dev.h"
 #include "qlin_internal.h"
 
@@ -55,29 +59,40 @@ __device__ __forceinline__ Row<COLS> ld_row(const uint8_t* p, bool valid) {
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t d, int b) { return (d >> (8 * b)) & 0xFFu; }
 
-// COLS consecutive scale values starting at element `idx` (16-byte aligned) -> fp32.
+// Raw dwords of COLS consecutive scale values (COLS/4 vectors for fp32, COLS/8 for
+// 16-bit types); the conversion is deferred to cvt_scales so the load latency is not
+// waited on where it is issued.
 template <int COLS>
-__device__ __forceinline__ void ld_scales(const void* p, int dt, long long idx, float out[COLS]) {
+__device__ __forceinline__ void ld_scales_raw(const void* p, int dt, long long idx, u32x4 raw[COLS / 4]) {
   if (dt == DT_F32) {
-    const float* q = (const float*)p + idx;
+    const u32x4* q = (const u32x4*)((const float*)p + idx);
 #pragma unroll
-    for (int c = 0; c < COLS; c += 4) {
-      const f32x4 v = *(const f32x4*)(q + c);
-      out[c] = v.x;
-      out[c + 1] = v.y;
-      out[c + 2] = v.z;
-      out[c + 3] = v.w;
+    for (int c = 0; c < COLS / 4; ++c) raw[c] = q[c];
+  } else {
+    const u32x4* q = (const u32x4*)((const uint16_t*)p + idx);
+#pragma unroll
+    for (int c = 0; c < COLS / 8; ++c) raw[c] = q[c];
+  }
+}
+
+template <int COLS>
+__device__ __forceinline__ void cvt_scales(const u32x4 raw[COLS / 4], int dt, float out[COLS]) {
+  if (dt == DT_F32) {
+#pragma unroll
+    for (int c = 0; c < COLS / 4; ++c) {
+      out[4 * c] = bitcast<float>(raw[c].x);
+      out[4 * c + 1] = bitcast<float>(raw[c].y);
+      out[4 * c + 2] = bitcast<float>(raw[c].z);
+      out[4 * c + 3] = bitcast<float>(raw[c].w);
     }
   } else {
-    const uint16_t* q = (const uint16_t*)p + idx;
 #pragma unroll
-    for (int c = 0; c < COLS; c += 8) {
-      const u32x4 v = *(const u32x4*)(q + c);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (int c = 0; c < COLS / 8; ++c) {
+      const uint32_t w[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-        out[c + e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+        out[8 * c + e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
       }
     }
   }
@@ -127,7 +142,9 @@ __device__ __forceinline__ void st_i8(int8_t* p, const int q[COLS]) {
   }
 }
 
-template <int ACT, int WK, bool HZ, int EPI, int COLS>
+// SPLIT: whether workgroups split K (partials + arrival counters).  Wide launches
+// (enough column or row tiles to fill the chip) use SPLIT = false.
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT>
 __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
   constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;  // weight sets feeding one output tile
   constexpr int TN = 16 * COLS;
@@ -140,8 +157,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
   const int lane = threadIdx.x & 63;
   const int j = lane & 15;
   const int g = lane >> 4;
-  const int tile = blockIdx.x / a.splits;
-  const int split = blockIdx.x - tile * a.splits;
+  const int tile = SPLIT ? blockIdx.x / a.splits : blockIdx.x;
+  const int split = SPLIT ? blockIdx.x - tile * a.splits : 0;
   const int rt = blockIdx.y;
   const int M = a.M;
   const int K = a.K;
@@ -181,9 +198,78 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
 #pragma unroll
     for (int t = 0; t < COLS; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if constexpr (ACT == ACT_F16) {
+  // ---------------- software-pipelined K loop ----------------
+  // Every load of one 32-wide K step (weights, activations, the step's group scales,
+  // zeros and activation scales) goes into slot d of a D-deep register ring and is
+  // issued D steps ahead, unconditionally (the step index is clamped to the wave's
+  // last step), so the loop body is straight-line and D steps of HBM latency overlap.
+  // Lanes past N or M read clamped in-bounds addresses; their MFMA columns / rows
+  // are never stored.
+  constexpr int D = (NS == 2) ? 2 : 4;
+  constexpr bool F16 = ACT == ACT_F16;
+  constexpr bool W4 = WK == WK_W4;
+  using XV = typename std::conditional<F16, u32x4, u32x2>::type;
+  struct Step {
+    Row<COLS> w[NS][NR];
+    XV xv;                            // fp16: 8 halves; int8: 8 bytes
+    u32x4 sraw[W4 ? NS : 1][COLS / 4];  // W4: raw scales of the step's group
+    Row<COLS> z[(W4 && HZ) ? NS : 1];   // W4: zeros of the step's group
+    float as_[F16 ? 1 : 4];           // int8: activation scales, rows 4g..4g+3
+  };
+  const long long xrow = (long long)(avalid ? arow : 0);
+  const _Float16* xpf = (const _Float16*)a.x + xrow * a.ldx + 8 * g;
+  const int8_t* xpi = (const int8_t*)a.x + xrow * K + 8 * g;
+  const int NG = K / 64;
+  long long asrow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int orow = rt * 16 + 4 * g + r;
+    asrow[r] = (long long)(orow < M ? orow : 0) * NG;
+  }
+  auto load_step = [&](Step& st, int k) {
+    if constexpr (F16) {
+      st.xv = *(const u32x4*)(xpf + k);
+    } else {
+      st.xv = *(const u32x2*)(xpi + k);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.as_[r] = a.xs[asrow[r] + k / 64];
+    }
+    const long long r0 = W4 ? (long long)(k / 2 + 4 * g) : (long long)(k + 8 * g);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint8_t* base = wp[s] + r0 * n + ccl;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) st.w[s][r] = ld_row<COLS>(base + (long long)r * n, true);
+      if constexpr (W4) {
+        const long long gi = (long long)(k / G) * n + ccl;
+        ld_scales_raw<COLS>(sp[s], a.sdt, gi, st.sraw[s]);
+        if constexpr (HZ) st.z[s] = ld_row<COLS>(zp[s] + gi, true);
+      }
+    }
+  };
+  const int nsteps = ke > kb ? (ke - kb) >> 5 : 0;
+  Step buf[D];
+  auto run_pipeline = [&](auto&& compute) {
+    if (nsteps <= 0) return;
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_step(buf[d], kb + 32 * (d < nsteps ? d : nsteps - 1));
+    const int nfull = nsteps - nsteps % D;
+    for (int base = 0; base < nfull; base += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int i = base + d;
+        compute(buf[d], kb + 32 * i);
+        const int nx = i + D < nsteps ? i + D : nsteps - 1;
+        load_step(buf[d], kb + 32 * nx);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (nfull + d < nsteps) compute(buf[d], kb + 32 * (nfull + d));
+  };
+
+  if constexpr (F16) {
     // ---------------- fp16 activations, fp16 MFMA ----------------
-    const _Float16* xp = (const _Float16*)a.x + (long long)(avalid ? arow : 0) * a.ldx + 8 * g;
     f32x4 tot[NS][COLS];
     f16x2 bias[NS][COLS];
 #pragma unroll
@@ -193,52 +279,42 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
         tot[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         bias[s][t] = f16x2{(_Float16)-1032.0f, (_Float16)-72.0f};
       }
-    for (int k = kb; k < ke; k += 32) {
-      f16x8 av = *(const f16x8*)(xp + k);
-      if (!avalid) av = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      if constexpr (WK == WK_W4 && HZ) {
-        if (k % G == 0) {
-          const long long zi = (long long)(k / G) * n + ccl;
+    run_pipeline([&](const Step& st, int k) {
+      if constexpr (W4 && HZ) {
+        if (k % G == 0) {  // group start: per-column (nibble - z) bias
 #pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const Row<COLS> zr = ld_row<COLS>(zp[s] + zi, cvalid);
+          for (int s = 0; s < NS; ++s)
 #pragma unroll
-            for (int t = 0; t < COLS; ++t) bias[s][t] = w4_bias(byte_of(zr.d[t >> 2], t & 3));
-          }
+            for (int t = 0; t < COLS; ++t) bias[s][t] = w4_bias(byte_of(st.z[s].d[t >> 2], t & 3));
         }
       }
+      const f16x8 av = bitcast<f16x8>(st.xv);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const long long r0 = (WK == WK_W8) ? (long long)(k + 8 * g) : (long long)(k / 2 + 4 * g);
-        const uint8_t* base = wp[s] + r0 * n + ccl;
-        Row<COLS> rows[NR];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) rows[r] = ld_row<COLS>(base + (long long)r * n, cvalid);
 #pragma unroll
         for (int t = 0; t < COLS; ++t) {
           const int q = t >> 2, b = t & 3;
           u32x4 bw;
-          if constexpr (WK == WK_W8) {
-            bw.x = w8_pair_f16(rows[0].d[q], rows[1].d[q], b);
-            bw.y = w8_pair_f16(rows[2].d[q], rows[3].d[q], b);
-            bw.z = w8_pair_f16(rows[4].d[q], rows[5].d[q], b);
-            bw.w = w8_pair_f16(rows[6].d[q], rows[7].d[q], b);
+          if constexpr (W4) {
+            bw.x = w4_pair_f16(st.w[s][0].d[q], b, bias[s][t]);
+            bw.y = w4_pair_f16(st.w[s][1].d[q], b, bias[s][t]);
+            bw.z = w4_pair_f16(st.w[s][2].d[q], b, bias[s][t]);
+            bw.w = w4_pair_f16(st.w[s][3].d[q], b, bias[s][t]);
           } else {
-            bw.x = w4_pair_f16(rows[0].d[q], b, bias[s][t]);
-            bw.y = w4_pair_f16(rows[1].d[q], b, bias[s][t]);
-            bw.z = w4_pair_f16(rows[2].d[q], b, bias[s][t]);
-            bw.w = w4_pair_f16(rows[3].d[q], b, bias[s][t]);
+            bw.x = w8_pair_f16(st.w[s][0].d[q], st.w[s][1].d[q], b);
+            bw.y = w8_pair_f16(st.w[s][2].d[q], st.w[s][3].d[q], b);
+            bw.z = w8_pair_f16(st.w[s][4].d[q], st.w[s][5].d[q], b);
+            bw.w = w8_pair_f16(st.w[s][6].d[q], st.w[s][7].d[q], b);
           }
           acc[s][t] = mfma_f16(av, bitcast<f16x8>(bw), acc[s][t]);
         }
       }
-      if constexpr (WK == WK_W4) {
-        if ((k + 32) % G == 0) {  // end of a weight group: fold in its scale
-          const long long si_ = (long long)(k / G) * n + ccl;
+      if constexpr (W4) {
+        if ((k + 32) % G == 0) {  // group end: fold in its scale
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
             float sc[COLS];
-            ld_scales<COLS>(sp[s], a.sdt, si_, sc);
+            cvt_scales<COLS>(st.sraw[s], a.sdt, sc);
 #pragma unroll
             for (int t = 0; t < COLS; ++t) {
 #pragma unroll
@@ -248,8 +324,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
           }
         }
       }
-    }
-    if constexpr (WK == WK_W4) {
+    });
+    if constexpr (W4) {
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -257,43 +333,34 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
     }
   } else {
     // ---------------- int8 activations (engine signature), int8 MFMA ----------------
-    const int8_t* xp = (const int8_t*)a.x + (long long)(avalid ? arow : 0) * K + 8 * g;
-    const int NG = K / 64;
-    const int SUB = (WK == WK_W8) ? 64 : (G < 64 ? G : 64);
+    const int SUB = W4 ? (G < 64 ? G : 64) : 64;
     i32x4 iacc[NS][COLS];
     i32x4 sx = i32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int t = 0; t < COLS; ++t) iacc[s][t] = i32x4{0, 0, 0, 0};
-    for (int k = kb; k < ke; k += 32) {
-      uint64_t a8 = *(const uint64_t*)(xp + k);
-      if (!avalid) a8 = 0;
-      uint64_t ap = a8;
-      if constexpr (WK == WK_W4) {
+    run_pipeline([&](const Step& st, int k) {
+      uint64_t ap = (uint64_t)st.xv.x | ((uint64_t)st.xv.y << 32);
+      if constexpr (W4) {
         // k slots: even K values first, then odd (the nibble split order below)
-        const uint32_t lo = (uint32_t)a8, hi = (uint32_t)(a8 >> 32);
-        ap = (uint64_t)perm(hi, lo, 0x06040200u) | ((uint64_t)perm(hi, lo, 0x07050301u) << 32);
+        ap = (uint64_t)perm(st.xv.y, st.xv.x, 0x06040200u) |
+             ((uint64_t)perm(st.xv.y, st.xv.x, 0x07050301u) << 32);
       }
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const long long r0 = (WK == WK_W8) ? (long long)(k + 8 * g) : (long long)(k / 2 + 4 * g);
-        const uint8_t* base = wp[s] + r0 * n + ccl;
-        Row<COLS> rows[NR];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) rows[r] = ld_row<COLS>(base + (long long)r * n, cvalid);
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           uint32_t lo4[4], hi4[4];
-          if constexpr (WK == WK_W8) {
-            tr4(rows[0].d[q], rows[1].d[q], rows[2].d[q], rows[3].d[q], lo4);
-            tr4(rows[4].d[q], rows[5].d[q], rows[6].d[q], rows[7].d[q], hi4);
-          } else {
+          if constexpr (W4) {
             uint32_t L[4], H[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) w4_split_i8x16(rows[r].d[q], L[r], H[r]);
+            for (int r = 0; r < 4; ++r) w4_split_i8x16(st.w[s][r].d[q], L[r], H[r]);
             tr4(L[0], L[1], L[2], L[3], lo4);
             tr4(H[0], H[1], H[2], H[3], hi4);
+          } else {
+            tr4(st.w[s][0].d[q], st.w[s][1].d[q], st.w[s][2].d[q], st.w[s][3].d[q], lo4);
+            tr4(st.w[s][4].d[q], st.w[s][5].d[q], st.w[s][6].d[q], st.w[s][7].d[q], hi4);
           }
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
@@ -302,39 +369,30 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
           }
         }
       }
-      if constexpr (WK == WK_W4 && HZ) sx = mfma_i8(ap, 0x0101010101010101ull, sx);
-      if ((k + 32) % SUB == 0) {
-        const int kblk = k / 64;
-        float as_[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int orow = rt * 16 + 4 * g + r;
-          as_[r] = orow < M ? a.xs[(long long)orow * NG + kblk] : 0.0f;
-        }
-        if constexpr (WK == WK_W8) {
+      if constexpr (W4 && HZ) sx = mfma_i8(ap, 0x0101010101010101ull, sx);
+      if ((k + 32) % SUB == 0) {  // end of an activation block / weight sub-block
+        if constexpr (!W4) {
 #pragma unroll
           for (int s = 0; s < NS; ++s)
 #pragma unroll
             for (int t = 0; t < COLS; ++t) {
 #pragma unroll
-              for (int r = 0; r < 4; ++r) acc[s][t][r] = fmaf((float)iacc[s][t][r], as_[r], acc[s][t][r]);
+              for (int r = 0; r < 4; ++r)
+                acc[s][t][r] = fmaf((float)iacc[s][t][r], st.as_[r], acc[s][t][r]);
               iacc[s][t] = i32x4{0, 0, 0, 0};
             }
         } else {
-          const long long gi = (long long)(k / G) * n + ccl;
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
             float ws[COLS];
-            ld_scales<COLS>(sp[s], a.sdt, gi, ws);
-            Row<COLS> zr;
-            if constexpr (HZ) zr = ld_row<COLS>(zp[s] + gi, cvalid);
+            cvt_scales<COLS>(st.sraw[s], a.sdt, ws);
 #pragma unroll
             for (int t = 0; t < COLS; ++t) {
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 int v = iacc[s][t][r] >> 4;  // exact: the MFMA summed 16 * (nibble - 8)
-                if constexpr (HZ) v += (8 - (int)byte_of(zr.d[t >> 2], t & 3)) * sx[r];
-                acc[s][t][r] = fmaf((float)v, as_[r] * ws[t], acc[s][t][r]);
+                if constexpr (HZ) v += (8 - (int)byte_of(st.z[s].d[t >> 2], t & 3)) * sx[r];
+                acc[s][t][r] = fmaf((float)v, st.as_[r] * ws[t], acc[s][t][r]);
               }
               iacc[s][t] = i32x4{0, 0, 0, 0};
             }
@@ -342,10 +400,21 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
           if constexpr (HZ) sx = i32x4{0, 0, 0, 0};
         }
       }
+    });
+  }
+
+  // Per-column scales of the W8 epilogue, issued now so their latency overlaps the
+  // reductions below.
+  u32x4 csraw[NS][COLS / 4];
+  if constexpr (WK == WK_W8) {
+    if (wave == 0) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) ld_scales_raw<COLS>(sp[s], a.sdt, ccl, csraw[s]);
     }
   }
 
   // ---------------- reduction over the waves of the workgroup (fixed order) ----------------
+  // `red` holds NS*COLS*256 floats: the per-wave partials here, the summed tile below.
   const int Mt = min(16, M - rt * 16);
   const int RG = (Mt + 3) >> 2;  // row groups (of 4 MFMA rows) that hold real rows
   if (nw > 1) {
@@ -364,8 +433,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
       }
     }
     __syncthreads();
-    if (wave != 0) return;
-    if (g < RG) {
+    if (wave == 0 && g < RG) {
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -376,65 +444,83 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
   }
 
   // ---------------- reduction over workgroups (split-K) ----------------
-  if (a.splits > 1) {
+  // Partials travel as agent-scope atomic stores / loads (coherent across XCDs by
+  // themselves, so no whole-L2 writeback or invalidate is needed).  Each workgroup
+  // waits until its partial stores have completed before it increments the tile's
+  // arrival counter; the workgroup that sees the final count reads every partial.
+  if constexpr (SPLIT) {
+    __shared__ int s_last;
     const long long MN = (long long)M * a.ncols;
-    if (g < RG && cvalid) {
+    if (wave == 0) {
+      if (g < RG && cvalid) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int orow = rt * 16 + 4 * g + r;
-          if (orow < M) {
-            float* pp = a.part + ((long long)split * NS + s) * MN + (long long)orow * a.ncols + ocol;
+          for (int r = 0; r < 4; ++r) {
+            const int orow = rt * 16 + 4 * g + r;
+            if (orow < M) {
+              float* pp = a.part + ((long long)split * NS + s) * MN + (long long)orow * a.ncols + ocol;
 #pragma unroll
-            for (int t = 0; t < COLS; t += 4)
-              *(f32x4*)(pp + t) = f32x4{acc[s][t][r], acc[s][t + 1][r], acc[s][t + 2][r], acc[s][t + 3][r]};
-          }
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    unsigned* cp = a.cnt + (long long)rt * a.ntiles + tile;
-    unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0);
-    if (prev != (unsigned)(a.splits - 1)) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (g < RG && cvalid) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int orow = rt * 16 + 4 * g + r;
-          if (orow < M) {
-            const float* pp = a.part + (long long)s * MN + (long long)orow * a.ncols + ocol;
-            float v[COLS];
-#pragma unroll
-            for (int t = 0; t < COLS; ++t) v[t] = pp[t];
-            for (int p = 1; p < a.splits; ++p) {
-              const float* pq = pp + (long long)p * NS * MN;
-#pragma unroll
-              for (int t = 0; t < COLS; t += 4) {
-                const f32x4 w = *(const f32x4*)(pq + t);
-                v[t] += w.x;
-                v[t + 1] += w.y;
-                v[t + 2] += w.z;
-                v[t + 3] += w.w;
-              }
+              for (int t = 0; t < COLS; ++t)
+                __hip_atomic_store(pp + t, acc[s][t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-#pragma unroll
-            for (int t = 0; t < COLS; ++t) acc[s][t][r] = v[t];
           }
-        }
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      unsigned* cp = a.cnt + (long long)rt * a.ntiles + tile;
+      if (lane == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (unsigned)(a.splits - 1);
+        if (last) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
     }
-    if (lane == 0) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (!s_last) return;  // uniform over the workgroup
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // The last workgroup sums the tile's partials in split order, every thread on
+    // its own (set, row, column) elements, into red[s][row][col].
+    const int tcol0 = (tile - sg0.tile0) * TN;  // tile's first column within the matrix
+    const int nel = NS * Mt * TN;
+    for (int e = threadIdx.x; e < nel; e += blockDim.x) {
+      const int s = e / (Mt * TN);
+      const int rem = e - s * (Mt * TN);
+      const int row = rem / TN;
+      const int col = rem - row * TN;
+      float v = 0.0f;
+      if (tcol0 + col < n) {
+        const float* pp = a.part + (long long)s * MN + (long long)(rt * 16 + row) * a.ncols + sg0.col0 + tcol0 + col;
+        const long long stride = (long long)NS * MN;
+        v = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll 8
+        for (int p = 1; p < a.splits; ++p)
+          v += __hip_atomic_load(pp + p * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      red[(s * 16 + row) * TN + col] = v;
+    }
+    __syncthreads();
+    if (wave == 0 && g < RG) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int t = 0; t < COLS; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r;
+            acc[s][t][r] = row < Mt ? red[(s * 16 + row) * TN + j * COLS + t] : 0.0f;
+          }
+    }
   }
+  if (wave != 0) return;
 
   // ---------------- epilogue ----------------
   if (g >= RG) return;
   if constexpr (EPI == EPI_STORE) {
     if (!cvalid) return;
     float cs[COLS];
-    if constexpr (WK == WK_W8) ld_scales<COLS>(sp[0], a.sdt, ccl, cs);
+    if constexpr (WK == WK_W8) cvt_scales<COLS>(csraw[0], a.sdt, cs);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int orow = rt * 16 + 4 * g + r;
@@ -453,8 +539,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
   } else {
     float cg[COLS], cu[COLS];
     if constexpr (WK == WK_W8) {
-      ld_scales<COLS>(sp[0], a.sdt, ccl, cg);
-      ld_scales<COLS>(sp[1], a.sdt, ccl, cu);
+      cvt_scales<COLS>(csraw[0], a.sdt, cg);
+      cvt_scales<COLS>(csraw[1], a.sdt, cu);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -493,7 +579,10 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
 
 template <int ACT, int WK, bool HZ, int EPI, int COLS>
 static hipError_t launch_t(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((skinny_kernel<ACT, WK, HZ, EPI, COLS>), L.grid, dim3(64 * L.waves), L.lds, st, a);
+  if (a.splits > 1)
+    hipLaunchKernelGGL((skinny_kernel<ACT, WK, HZ, EPI, COLS, true>), L.grid, dim3(64 * L.waves), L.lds, st, a);
+  else
+    hipLaunchKernelGGL((skinny_kernel<ACT, WK, HZ, EPI, COLS, false>), L.grid, dim3(64 * L.waves), L.lds, st, a);
   return hipGetLastError();
 }
 
@@ -502,20 +591,21 @@ static hipError_t launch_t(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
     return launch_t<A, W, Z, E, C>(L, a, st);
 
 #define QL_COLS(A, W, Z, E) QL_CASE(A, W, Z, E, 8) QL_CASE(A, W, Z, E, 16)
+#define QL_C8(A, W, Z, E) QL_CASE(A, W, Z, E, 8)
 
 hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
   QL_COLS(ACT_F16, WK_W8, false, EPI_STORE)
   QL_COLS(ACT_F16, WK_W4, false, EPI_STORE)
   QL_COLS(ACT_F16, WK_W4, true, EPI_STORE)
   QL_COLS(ACT_I8, WK_W8, false, EPI_STORE)
-  QL_COLS(ACT_I8, WK_W8, false, EPI_GATEUP)
-  QL_COLS(ACT_I8, WK_W8, false, EPI_GATEUP_Q)
+  QL_C8(ACT_I8, WK_W8, false, EPI_GATEUP)
+  QL_C8(ACT_I8, WK_W8, false, EPI_GATEUP_Q)
   QL_COLS(ACT_I8, WK_W4, false, EPI_STORE)
   QL_COLS(ACT_I8, WK_W4, true, EPI_STORE)
-  QL_COLS(ACT_I8, WK_W4, false, EPI_GATEUP)
-  QL_COLS(ACT_I8, WK_W4, true, EPI_GATEUP)
-  QL_COLS(ACT_I8, WK_W4, false, EPI_GATEUP_Q)
-  QL_COLS(ACT_I8, WK_W4, true, EPI_GATEUP_Q)
+  QL_C8(ACT_I8, WK_W4, false, EPI_GATEUP)
+  QL_C8(ACT_I8, WK_W4, true, EPI_GATEUP)
+  QL_C8(ACT_I8, WK_W4, false, EPI_GATEUP_Q)
+  QL_C8(ACT_I8, WK_W4, true, EPI_GATEUP_Q)
   return hipErrorInvalidValue;
 }
 
