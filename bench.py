@@ -379,8 +379,8 @@ def main() -> int:
 
     import torch
     _load_package()
-    from qwen35_amd.kernels import common
-    common.lib()
+    from qwen35_amd.kernels import qlin
+    qlin.lib()
     if not torch.cuda.is_available():
         print("bench.py: no GPU", file=sys.stderr)
         return 1

@@ -1,171 +1,10 @@
-"""Shared host-side helpers of the MI355X quantized-linear kernels.
+"""Constants shared with the engine (kernels/common.py:5-9 of the reference).
 
-Counterpart of the reference's kernels/common.py (kernels/common.py:1-58).  The
-device helpers that file defines as Triton functions -- `swizzle` (12-21),
-`round_i8` (24-29), `silu` (32-34) -- live in HIP in `csrc/qlin_dev.h`; this module
-keeps `GROUP` (7-9, imported by the engine) and the launch plumbing:
-
-* loading `libqlin.so` with ctypes and declaring its C ABI (include/qlin.h);
-* tensor -> pointer / dtype-code marshalling and the current HIP stream;
-* the per-device split-K workspace (allocated once, zero-filled, reused);
-* status code -> exception (ValueError for bad arguments, RuntimeError otherwise).
-
-There is no fallback: if the library is missing or no GPU is present, the
-entry points raise.
+In a drop-in install the reference's own kernels/common.py (which also carries the
+Triton helpers its norm / attention kernels use) stays in place; it defines the same
+GROUP.  The launch plumbing of the quantized linears lives in `qlin.py`.
 """
-from __future__ import annotations
-
-import ctypes
-import os
-import pathlib
-import threading
-
-import torch
 
 # Activation quantization granularity: one fp32 scale per 64 int8 values along K
 # (kernels/common.py:5-7).
 GROUP = 64
-
-LIB_PATH = pathlib.Path(__file__).resolve().parent / "libqlin.so"
-
-QLIN_OK = 0
-QLIN_ERR_INVALID = -1
-QLIN_ERR_UNSUPPORTED = -2
-QLIN_ERR_HIP = -3
-QLIN_ERR_WORKSPACE = -4
-
-QLIN_F16 = 1
-QLIN_BF16 = 2
-QLIN_F32 = 3
-
-_DT = {torch.float16: QLIN_F16, torch.bfloat16: QLIN_BF16, torch.float32: QLIN_F32}
-
-_lib = None
-_lib_lock = threading.Lock()
-
-_P = ctypes.c_void_p
-_I = ctypes.c_int
-_L = ctypes.c_int64
-_S = ctypes.c_size_t
-
-# argument lists of the C ABI (include/qlin.h); every entry point returns int
-_SIGS = {
-    "qlin_gemm_i8": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _L, _P, _L, _P, _S, _P],
-    "qlin_gemm_w4": [_P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _P, _L, _P, _L, _P, _S, _P],
-    "qlin_proj3_i8": [_P, _P, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _P, _L, _P, _S, _P],
-    "qlin_proj3_w4": [_P, _P, _I, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I,
-                      _P, _L, _P, _S, _P],
-    "qlin_mlp_gate_up_i8": [_P, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _S, _P],
-    "qlin_mlp_gate_up_w4": [_P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _S, _P],
-    "qlin_mlp_gate_up_quant_i8": [_P, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _S, _P],
-    "qlin_mlp_gate_up_quant_w4": [_P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P,
-                                  _P, _S, _P],
-    "qlin_linear_w8": [_P, _I, _I, _I, _L, _P, _P, _I, _I, _P, _I, _L, _P, _L, _P, _S, _P],
-    "qlin_linear_w4": [_P, _I, _I, _I, _L, _P, _P, _I, _P, _I, _I, _P, _I, _L, _P, _L, _P, _S, _P],
-    "qlin_w4_unpack": [_P, _I, _I, _P, _P],
-    "qlin_w4_dequant_f32": [_P, _P, _I, _P, _I, _I, _I, _P, _P],
-    "qlin_w8_dequant_f32": [_P, _P, _I, _I, _I, _P, _P],
-}
-
-EXPORTS = ("qlin_version", "qlin_last_error", "qlin_workspace_bytes", *_SIGS)
-
-
-def lib() -> ctypes.CDLL:
-    """The loaded libqlin.so (raises ImportError if it has not been built)."""
-    global _lib
-    if _lib is not None:
-        return _lib
-    with _lib_lock:
-        if _lib is None:
-            if not LIB_PATH.exists():
-                raise ImportError(
-                    f"{LIB_PATH} not found: build it with "
-                    "`python qwen_3.5_comfy_prompt_enhancer_amd/build.py`")
-            L = ctypes.CDLL(str(LIB_PATH))
-            L.qlin_version.restype = ctypes.c_int
-            L.qlin_version.argtypes = []
-            L.qlin_last_error.restype = ctypes.c_char_p
-            L.qlin_last_error.argtypes = []
-            L.qlin_workspace_bytes.restype = ctypes.c_size_t
-            L.qlin_workspace_bytes.argtypes = []
-            for name, args in _SIGS.items():
-                f = getattr(L, name)
-                f.restype = ctypes.c_int
-                f.argtypes = args
-            _lib = L
-    return _lib
-
-
-def ptr(t) -> int | None:
-    """Device pointer of a tensor (None -> NULL)."""
-    return None if t is None else t.data_ptr()
-
-
-def dtype_code(t: torch.Tensor) -> int:
-    try:
-        return _DT[t.dtype]
-    except KeyError:
-        raise ValueError(f"unsupported dtype {t.dtype}") from None
-
-
-def stream_of(t: torch.Tensor) -> int:
-    """The current HIP stream of `t`'s device, as the hipStream_t the C ABI takes."""
-    return torch.cuda.current_stream(t.device).cuda_stream
-
-
-def check(status: int, name: str) -> None:
-    if status == QLIN_OK:
-        return
-    msg = lib().qlin_last_error().decode(errors="replace") or name
-    if status in (QLIN_ERR_INVALID, QLIN_ERR_UNSUPPORTED):
-        raise ValueError(msg)
-    raise RuntimeError(msg)
-
-
-_ws: dict[int, torch.Tensor] = {}
-_ws_lock = threading.Lock()
-
-
-def workspace(device: torch.device) -> torch.Tensor:
-    """Per-device split-K workspace (zero-filled once; the kernels leave their
-    arrival counters at zero after every call, so it is never cleared again)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    w = _ws.get(idx)
-    if w is None:
-        with _ws_lock:
-            w = _ws.get(idx)
-            if w is None:
-                nbytes = lib().qlin_workspace_bytes()
-                w = torch.zeros(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
-                _ws[idx] = w
-    return w
-
-
-def require_cuda(*ts) -> torch.device:
-    dev = None
-    for t in ts:
-        if t is None:
-            continue
-        if not t.is_cuda:
-            raise ValueError("all tensors must be on the GPU")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError("all tensors must be on the same device")
-    return dev
-
-
-def require_contig(name: str, t) -> None:
-    if t is not None and not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
-
-
-def require_rowmajor(name: str, t) -> None:
-    """2-D with unit column stride (rows may be strided)."""
-    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
-        raise ValueError(f"{name} must be a 2-D row-major matrix")
-
-
-def call(name: str, *args) -> None:
-    """Invoke one C entry point and raise on a non-zero status."""
-    check(getattr(lib(), name)(*args), name)

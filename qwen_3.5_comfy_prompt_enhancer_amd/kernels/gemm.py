@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import torch
 
-from . import common as C
+from . import qlin as C
 from .common import GROUP
 from .w4 import gemm_w4, mlp_gate_up_quant_w4, mlp_gate_up_w4, proj3_w4
 

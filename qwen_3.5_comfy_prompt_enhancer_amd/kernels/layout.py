@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import torch
 
-from . import common as C
+from . import qlin as C
 
 __all__ = ["w4_unpack", "w4_dequant_f32", "w8_dequant_f32"]
 

@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import torch
 
-from . import common as C
+from . import qlin as C
 
 __all__ = ["linear_w8", "linear_w4", "linear"]
 

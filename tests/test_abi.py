@@ -1,0 +1,152 @@
+"""CPU tests of the C-ABI boundary (no GPU needed): libqlin.so loads, exports every
+function include/qlin.h declares, and rejects bad arguments with the documented
+status codes before launching anything; the Python shims validate shapes and dtypes
+and raise ValueError like the reference's wrappers would fail on bad input."""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "qlin.h"
+
+
+def _lib():
+    from qwen35_amd.kernels import qlin
+    return qlin, qlin.lib()
+
+
+def declared_functions():
+    src = HEADER.read_text()
+    return re.findall(r"^\s*(?:int|const char\*|size_t)\s+(qlin_\w+)\s*\(", src, re.M)
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    assert len(names) == 16
+    for n in ("qlin_gemm_i8", "qlin_gemm_w4", "qlin_proj3_i8", "qlin_proj3_w4",
+              "qlin_mlp_gate_up_quant_i8", "qlin_mlp_gate_up_quant_w4", "qlin_linear_w8",
+              "qlin_linear_w4", "qlin_w4_unpack", "qlin_w4_dequant_f32"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    qlin, L = _lib()
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert missing == []
+    assert set(declared_functions()) == set(qlin.EXPORTS)
+
+
+def test_version_and_workspace():
+    _, L = _lib()
+    assert L.qlin_version() == 1
+    assert L.qlin_workspace_bytes() == 64 << 20
+    assert L.qlin_last_error() == b""
+
+
+I64 = ctypes.c_int64
+SZ = ctypes.c_size_t
+FAKE = ctypes.c_void_p(0x10000)      # aligned non-null pointer, never dereferenced
+
+
+def test_null_activations_rejected():
+    qlin, L = _lib()
+    rc = L.qlin_gemm_i8(None, None, 1, 128, FAKE, FAKE, qlin.QLIN_F32, 64, FAKE, I64(64), None, I64(0),
+                        None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_INVALID
+    assert b"null activations" in L.qlin_last_error()
+
+
+def test_bad_k_rejected():
+    qlin, L = _lib()
+    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 96, FAKE, FAKE, qlin.QLIN_F32, 64, FAKE, I64(64), None, I64(0),
+                        None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED
+    assert b"K=96" in L.qlin_last_error()
+
+
+def test_bad_n_and_alignment_rejected():
+    qlin, L = _lib()
+    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 128, FAKE, FAKE, qlin.QLIN_F32, 40, FAKE, I64(40), None, I64(0),
+                        None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"N=40" in L.qlin_last_error()
+    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 128, ctypes.c_void_p(0x10001), FAKE, qlin.QLIN_F32, 64, FAKE,
+                        I64(64), None, I64(0), None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"aligned" in L.qlin_last_error()
+
+
+def test_bad_group_rejected():
+    qlin, L = _lib()
+    rc = L.qlin_gemm_w4(FAKE, FAKE, 1, 256, FAKE, FAKE, qlin.QLIN_BF16, None, 48, 64, FAKE, I64(64), None,
+                        I64(0), None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"group 48" in L.qlin_last_error()
+    rc = L.qlin_linear_w4(FAKE, qlin.QLIN_F16, 1, 192, I64(192), FAKE, FAKE, qlin.QLIN_F16, None, 128, 64,
+                          FAKE, qlin.QLIN_F16, I64(64), None, I64(0), None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_INVALID and b"not a multiple of the group" in L.qlin_last_error()
+
+
+def test_bad_dtypes_rejected():
+    qlin, L = _lib()
+    rc = L.qlin_linear_w8(FAKE, qlin.QLIN_F32, 1, 128, I64(128), FAKE, FAKE, qlin.QLIN_F16, 64, FAKE,
+                          qlin.QLIN_F16, I64(64), None, I64(0), None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"activation dtype" in L.qlin_last_error()
+    rc = L.qlin_linear_w8(FAKE, qlin.QLIN_F16, 1, 128, I64(128), FAKE, FAKE, 9, 64, FAKE,
+                          qlin.QLIN_F16, I64(64), None, I64(0), None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"scale dtype" in L.qlin_last_error()
+
+
+def test_zero_sized_calls_are_no_ops():
+    qlin, L = _lib()
+    assert L.qlin_gemm_i8(None, None, 0, 128, None, None, qlin.QLIN_F32, 64, None, I64(64), None, I64(0),
+                          None, SZ(0), None) == 0
+    assert L.qlin_w4_unpack(None, 0, 16, None, None) == 0
+
+
+def test_proj3_zero_mixing_rejected():
+    qlin, L = _lib()
+    rc = L.qlin_proj3_w4(FAKE, FAKE, 1, 128, FAKE, FAKE, FAKE, 64, FAKE, FAKE, None, 64, None, None, None, 0,
+                         qlin.QLIN_BF16, 128, FAKE, I64(128), None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_INVALID and b"zeros" in L.qlin_last_error()
+
+
+# ---------------------------------------------------------------- Python shim validation
+
+def test_shims_validate_before_launch():
+    from qwen35_amd.kernels import gemm, linear, w4
+    a = torch.zeros((2, 128), dtype=torch.int8)
+    s = torch.zeros((2, 2), dtype=torch.float32)
+    b = torch.zeros((128, 64), dtype=torch.int8)
+    bs = torch.zeros(64, dtype=torch.float32)
+    out = torch.zeros((2, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="a_s must be"):
+        gemm.gemm_i8(a, s[:, :1], b, bs, out)
+    with pytest.raises(ValueError, match="out must be"):
+        gemm.gemm_i8(a, s, b, bs, out.float())
+    with pytest.raises(ValueError, match="GPU"):
+        gemm.gemm_i8(a, s, b, bs, out)                 # CPU tensors
+    p = torch.zeros((64, 64), dtype=torch.uint8)
+    ps = torch.zeros((1, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="zeros"):
+        w4.gemm_w4(a, s, p, ps, out, b_z=torch.zeros((2, 64), dtype=torch.uint8))
+    x = torch.zeros((2, 128), dtype=torch.float32)
+    with pytest.raises(ValueError, match="float16"):
+        linear.linear_w8(x, b, bs.half(), out.half())
+
+
+def test_w4_dispatch_follows_weight_dtype():
+    """uint8 weights route gemm_i8 / proj3 / mlp_gate_up_quant to the W4 path
+    (kernels/gemm.py:15-17): the W4 validator's message proves the route."""
+    from qwen35_amd.kernels import gemm
+    a = torch.zeros((2, 128), dtype=torch.int8)
+    s = torch.zeros((2, 2), dtype=torch.float32)
+    p = torch.zeros((32, 64), dtype=torch.uint8)        # wrong K/2 on purpose
+    ps = torch.zeros((1, 64), dtype=torch.bfloat16)
+    out = torch.zeros((2, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match=r"uint8 \[K/2=64"):
+        gemm.gemm_i8(a, s, p, ps, out)
+    with pytest.raises(ValueError, match=r"uint8 \[K/2=64"):
+        gemm.proj3(a, s, p, ps, None, None, None, None, out)
