@@ -358,6 +358,29 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
   QL_TRY(check_weight(fn, w, scale, zero, N, wk));
   QL_TRY(check_out16(fn, out, ldo, N, "out"));
   if (residual) QL_TRY(check_out16(fn, residual, ldr, N, "residual"));
+  if (M > 16 && K % 64 == 0) {
+    // prefill: LDS-tiled MFMA GEMM (K in tiles of 64; other K take the row-tiled skinny path)
+    TlArgs t;
+    t.x = (const _Float16*)x;
+    t.ldx = ldx;
+    t.w = (const uint8_t*)w;
+    t.s = scale;
+    t.z = zero;
+    t.M = M;
+    t.N = N;
+    t.K = K;
+    t.group = (wk == WK_W4) ? group : 32;
+    t.sdt = s_dtype;
+    t.out = out;
+    t.ldo = ldo;
+    t.odt = out_dtype;
+    t.res = residual;
+    t.ldr = ldr;
+    int depth = 3;
+    const char* e = getenv("QLIN_TILED_DEPTH");  // tuning override (2, 3 or 4)
+    if (e && *e) depth = atoi(e);
+    return hip_status(fn, launch_tiled(t, wk, zero != nullptr, depth, (hipStream_t)stream));
+  }
   SkArgs a = base_args();
   a.x = x;
   a.ldx = ldx;

@@ -50,6 +50,25 @@ struct SkLaunch {
 
 hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
 
+// Arguments of the tiled (M > 16) fp16-activation MFMA kernel.
+struct TlArgs {
+  const _Float16* x;  // fp16 [M][ldx]
+  long long ldx;
+  const uint8_t* w;   // int8 [K][N] or packed uint8 [K/2][N]
+  const void* s;      // W8: scale[N]; W4: scale[K/group][N]
+  const uint8_t* z;   // W4 zeros or nullptr
+  int M, N, K;
+  int group;
+  int sdt;
+  void* out;          // 16-bit [M][ldo]
+  long long ldo;
+  int odt;
+  const void* res;    // 16-bit [M][ldr] or nullptr
+  long long ldr;
+};
+
+hipError_t launch_tiled(const TlArgs& a, int wk, bool hz, int depth, hipStream_t stream);
+
 hipError_t launch_w4_unpack(const uint8_t* p, int K, int N, uint8_t* out, hipStream_t st);
 hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uint8_t* z,
                              int group, int K, int N, float* out, hipStream_t st);

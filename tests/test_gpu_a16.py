@@ -202,3 +202,63 @@ def test_repeat_calls_are_deterministic():
     w, s = H.w8(K, N, seed=82)
     ys = [_run_w8(x, w, s) for _ in range(3)]
     assert torch.equal(ys[0], ys[1]) and torch.equal(ys[1], ys[2])
+
+
+# ---------------------------------------------------------------- prefill (M > 16): tiled MFMA path
+
+@pytest.mark.parametrize("M", [17, 128, 300])
+@pytest.mark.parametrize("K,N", [(2048, 1024), (512, 2064)])
+def test_prefill_w8(M, K, N):
+    x = H.act_f16(M, K, seed=300 + M)
+    w, s = H.w8(K, N, seed=301)
+    res = torch.randn((M, N), generator=H.gen(302)).to(torch.float16)
+    H.assert_out_close(_run_w8(x, w, s), H.linear_w8_ref_cols(x, w, s, np.arange(N)))
+    H.assert_out_close(_run_w8(x, w, s, residual=res),
+                       H.linear_w8_ref_cols(x, w, s, np.arange(N), residual=res))
+
+
+@pytest.mark.parametrize("M", [40, 256])
+@pytest.mark.parametrize("group,zeros,sdt", [(128, "none", torch.float16), (32, "random", torch.float16),
+                                             (64, "random", torch.bfloat16), (128, "eight", torch.float32)])
+def test_prefill_w4(M, group, zeros, sdt):
+    """W4 prefill folds the group scale into the fp16 weight (one fp16 rounding per
+    weight), so it is held to the GEMM tolerance, not bit-exactness."""
+    K, N = 1024, 1024
+    x = H.act_f16(M, K, seed=310 + M)
+    packed, s, z = H.w4(K, N, seed=311, group=group, zeros=zeros)
+    s = s.to(sdt)
+    y = _run_w4(x, packed, s, z, out_dtype=torch.bfloat16)
+    H.assert_out_close(y, H.linear_w4_ref_cols(x, packed, s.float() if sdt == torch.bfloat16 else s, z,
+                                               np.arange(N)))
+
+
+def test_prefill_rows_independent_of_chunking():
+    """Rows computed in one M=300 call equal the same rows computed as an M=100
+    chunk (the tiled family's per-row arithmetic does not depend on M)."""
+    K, N = 2048, 1024
+    x = H.act_f16(300, K, seed=320)
+    w, s = H.w8(K, N, seed=321)
+    y = _run_w8(x, w, s)
+    yc = _run_w8(x[100:200].contiguous(), w, s)
+    assert torch.equal(y[100:200], yc)
+
+
+@pytest.mark.parametrize("K", [512, 576, 640, 2048])
+def test_prefill_ring_depths_agree(K, monkeypatch):
+    """The K-tile order of the tiled kernel does not depend on how many tiles of
+    global loads are in flight, so every ring depth (QLIN_TILED_DEPTH, a tuning
+    override) gives bit-identical outputs that also meet the oracle.  K covers
+    tile counts that are and are not multiples of each depth (8, 9, 10, 32)."""
+    M, N = 200, 1024
+    x = H.act_f16(M, K, seed=330 + K)
+    w, s = H.w8(K, N, seed=331)
+    packed, s4, z = H.w4(K, N, seed=332, group=64, zeros="random")
+    outs = {}
+    for depth in (2, 3, 4):
+        monkeypatch.setenv("QLIN_TILED_DEPTH", str(depth))
+        outs[depth] = (_run_w8(x, w, s), _run_w4(x, packed, s4, z))
+    for depth in (3, 4):
+        assert torch.equal(outs[depth][0], outs[2][0]), f"W8 depth {depth}"
+        assert torch.equal(outs[depth][1], outs[2][1]), f"W4 depth {depth}"
+    H.assert_out_close(outs[3][0], H.linear_w8_ref_cols(x, w, s, np.arange(N)))
+    H.assert_out_close(outs[3][1], H.linear_w4_ref_cols(x, packed, s4, z, np.arange(N)))
