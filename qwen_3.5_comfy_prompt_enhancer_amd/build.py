@@ -37,13 +37,21 @@ CFLAGS = [
 ]
 
 
+# Per-source flags.  prefill.hip keeps its 128 fp32 accumulators per lane in
+# architectural VGPRs (the VGPR form of MFMA): with accumulation registers the
+# compiler rotates the loop-carried accumulators through copies every K tile.
+EXTRA = {
+    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def sources() -> list[pathlib.Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
 def compile_one(src: pathlib.Path) -> pathlib.Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
     noise = "'-packed-fp32-ops' is not a recognized feature"

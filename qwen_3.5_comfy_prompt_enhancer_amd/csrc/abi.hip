@@ -358,7 +358,16 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
   QL_TRY(check_weight(fn, w, scale, zero, N, wk));
   QL_TRY(check_out16(fn, out, ldo, N, "out"));
   if (residual) QL_TRY(check_out16(fn, residual, ldr, N, "residual"));
-  if (M > 16 && K % 64 == 0) {
+  // More than 16 rows: the LDS-tiled MFMA kernel when it has enough tiles to fill the
+  // chip, else row tiles of 16 through the skinny kernel (whose weight re-reads per
+  // row tile come from L2).  QLIN_PREFILL ("skinny", "v1") overrides for tuning.
+  const char* pimpl = getenv("QLIN_PREFILL");
+  const long long tiles128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
+  const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
+  bool tiled = M > 256 && K % 64 == 0 && tiles128 >= 128;
+  if (pimpl && strcmp(pimpl, "skinny") == 0) tiled = false;
+  if (pimpl && (strcmp(pimpl, "v1") == 0 || strcmp(pimpl, "v2") == 0)) tiled = M > 16 && K % 64 == 0;
+  if (tiled) {
     // prefill: LDS-tiled MFMA GEMM (K in tiles of 64; other K take the row-tiled skinny path)
     TlArgs t;
     t.x = (const _Float16*)x;
@@ -376,6 +385,15 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
     t.odt = out_dtype;
     t.res = residual;
     t.ldr = ldr;
+    const char* impl = getenv("QLIN_PREFILL");  // tuning override: "v1" = register-ring kernel
+    // the DMA kernel addresses activations with 32-bit byte offsets
+    const bool fits32 = ((long long)(M - 1) * ldx + K) * 2 < (1LL << 31);
+    if (fits32 && !(impl && strcmp(impl, "v1") == 0)) {
+      int shape = (tiles256 >= 128) ? PF_256x256 : PF_128x128;
+      const char* e = getenv("QLIN_PREFILL_SHAPE");  // tuning override (0, 1 or 2)
+      if (e && *e) shape = atoi(e);
+      return hip_status(fn, launch_prefill(t, wk, zero != nullptr, shape, (hipStream_t)stream));
+    }
     int depth = 3;
     const char* e = getenv("QLIN_TILED_DEPTH");  // tuning override (2, 3 or 4)
     if (e && *e) depth = atoi(e);

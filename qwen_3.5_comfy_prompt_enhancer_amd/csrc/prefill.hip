@@ -1,0 +1,340 @@
+// Prefill GEMM for fp16 activations with more than 16 rows, gfx950.
+//
+// out[M,N] = x[M,K] . dequant(W)[K,N] (+ residual), W in the engine layouts (int8
+// [K,N] with per-column scales, or packed nibbles [K/2,N] with per-group scales and
+// optional zeros).
+//
+//   * Workgroup tile BM x BN = (128 WM) x (64 WN) computed by WM x WN waves, each
+//     owning a 128 x 64 output tile = 8 x 4 blocks of v_mfma_f32_16x16x32_f16 with
+//     fp32 accumulation.  Tall wave tiles make every dequantized weight operand feed
+//     8 MFMAs.  With 8 waves (256 x 256) two waves share each SIMD, so one wave's
+//     dequantization and LDS traffic issue while the other's MFMAs run.
+//   * Global -> LDS copies are 16-byte LDS DMA (global_load_lds_dwordx4): no VGPR
+//     staging.  Activation tiles land as 128-byte rows of 64 halves with the 16-byte
+//     chunk c of row r stored at position c ^ ((r >> 1) & 7), which makes the MFMA
+//     operand reads (ds_read_b128, rows j of 16, K chunks by lane group) free of bank
+//     conflicts for gfx950's read phases (lane blocks 0/3, 1/2, 4/7, 5/6 of 8 lanes
+//     share a cycle).  Weight tiles land as raw bytes, in blocks of 8 rows of 128
+//     bytes padded to 1088 bytes, so the four lane groups of a ds_read_b32 hit four
+//     disjoint bank quarters.
+//   * Weights are dequantized per MFMA operand in registers (v_perm_b32 exponent
+//     trick): lane (g, j) reads 4 adjacent columns of its 8 K rows and builds the B
+//     operands of 4 MFMAs; MFMA column j of instruction t is output column 4j + t.
+//     W8 values are exact integers in fp16 and the column scale multiplies the fp32
+//     result; W4 (nibble - z) is exact and the group scale is folded into the fp16
+//     weight (one fp16 rounding per weight).
+//   * NSTAGE K tiles of 64 in an LDS ring.  Each iteration waits (vmcnt) for the
+//     oldest tile, passes one barrier, issues the DMA of the tile NSTAGE - 1 ahead
+//     into the stage freed by the previous iteration, and computes.  The DMA is
+//     issued from inline assembly so the compiler's wait insertion, which would
+//     otherwise drain every in-flight copy before each LDS read, leaves the ring
+//     alone; the waits are explicit and count this kernel's own copies only.
+//   * The K order of every output element is fixed (tiles 0..K/64-1, two 32-wide
+//     substeps each), so a row's result does not depend on M.
+#include "qlin_dev.h"
+#include "qlin_internal.h"
+
+namespace qlin {
+
+namespace {
+
+constexpr int BK = 64;           // K per stage
+constexpr int WBLK = 1024 + 64;  // LDS bytes of one 8-row weight block (rows of 128 B + pad)
+constexpr int NSTAGE = 3;
+constexpr int GROUP_M = 8;       // tile order: 8 row tiles per group
+
+template <int WK, int WM, int WN>
+struct Geo {
+  static constexpr int BM = 128 * WM;
+  static constexpr int BN = 64 * WN;  // WN even: the weight tile is stored in 128-column halves
+  static constexpr int WAVES = WM * WN;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int A_BYTES = BM * 128;
+  static constexpr int HB_BLOCKS = (WK == WK_W8) ? 8 : 4;  // 64 int8 rows or 32 packed rows per half
+  static constexpr int B_BLOCKS = HB_BLOCKS * (BN / 128);
+  static constexpr int B_BYTES = B_BLOCKS * WBLK;
+  static constexpr int SC_BYTES = (WK == WK_W8) ? 0 : WAVES * 1024;  // W4 scales + zeros
+  static constexpr int STAGE = A_BYTES + B_BYTES + SC_BYTES;
+  static constexpr int A_DMA = (BM / 8) / WAVES;  // 1 KB activation blocks per wave
+  static constexpr int B_DMA = B_BLOCKS / WAVES;  // weight blocks per wave
+  static constexpr int DMA = A_DMA + B_DMA + (WK == WK_W4 ? 1 : 0);  // copies per wave per stage
+  static constexpr int OCC = (WAVES >= 8) ? 2 : 1;                    // waves per SIMD
+  static_assert(WN % 2 == 0 && (BM / 8) % WAVES == 0 && B_BLOCKS % WAVES == 0, "tile geometry");
+  static_assert(WK == WK_W8 || 10 * BN <= SC_BYTES, "W4 scale region");
+};
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4
+// left at its maximum, lgkmcnt 11:8 = 0).
+constexpr int wait_vm_lgkm0(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | 0x70; }
+
+__device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ const void* rfl_ptr(const void* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint64_t lo = rfl((uint32_t)v), hi = rfl((uint32_t)(v >> 32));
+  return (const void*)((hi << 32) | lo);
+}
+
+// 16-byte LDS DMA: lane i copies 16 bytes from sbase + voff to LDS m0 + 16 i.
+__device__ __forceinline__ void dma_s(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+
+// Same with a full 64-bit address per lane.
+__device__ __forceinline__ void dma_v(const void* vaddr, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(vaddr), "{m0}"(m0) : "memory");
+}
+
+__device__ __forceinline__ _Float16 scale_f16(uint32_t bits, int dt) {
+  if (dt == DT_F32) return (_Float16)bitcast<float>(bits);
+  if (dt == DT_BF16) return (_Float16)bf16_to_f32((uint16_t)bits);
+  return bitcast<_Float16>((uint16_t)bits);
+}
+
+}  // namespace
+
+template <int WK, bool HZ, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(Geo<WK, WM, WN>::OCC, Geo<WK, WM, WN>::OCC)))
+void prefill_kernel(const TlArgs a) {
+  using G = Geo<WK, WM, WN>;
+  constexpr int BN = G::BN;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+
+  const int tid = threadIdx.x;
+  const int wave = (int)rfl((uint32_t)tid >> 6), lane = tid & 63;  // wave index in an SGPR
+  const int j = lane & 15, g = lane >> 4;
+  const int wm = wave / WN, wn = wave % WN;
+  const int M = a.M, N = a.N, K = a.K;
+
+  // grouped tile order: consecutive workgroups share weight column tiles in L2
+  const int tiles_m = (M + G::BM - 1) / G::BM, tiles_n = (N + BN - 1) / BN;
+  const int pid = blockIdx.x;
+  const int per_group = GROUP_M * tiles_n;
+  const int first_m = (pid / per_group) * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (pid % per_group) % gsize;
+  const int tn = (pid % per_group) / gsize;
+  const int m0 = tm * G::BM, n0 = tn * BN;
+
+  // activation copies: block q of this wave = rows 8 * blk .. +7; lane -> row
+  // 8 blk + lane / 8, LDS position lane % 8 holding K chunk (position ^ swizzle)
+  uint32_t offA[G::A_DMA];
+#pragma unroll
+  for (int q = 0; q < G::A_DMA; ++q) {
+    const int r = 8 * (wave * G::A_DMA + q) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int row = min(m0 + r, M - 1);  // rows past M read row M-1 and are never stored
+    offA[q] = (uint32_t)(((long long)row * a.ldx + 8 * c) * 2);
+  }
+  // weight copies: block = 8 (packed) rows of 128 bytes of one 128-column half;
+  // lane -> row, 16-byte chunk
+  uint32_t offB[G::B_DMA];
+#pragma unroll
+  for (int q = 0; q < G::B_DMA; ++q) {
+    const int blk = wave * G::B_DMA + q;
+    const int half = blk / G::HB_BLOCKS, b = blk % G::HB_BLOCKS;
+    const int s = lane >> 3;
+    // W4 stores packed row 4h + i of a block at slot 2i + h so the two halves of the
+    // 4 rows a lane group reads sit in different bank halves
+    const int r = 8 * b + ((WK == WK_W8) ? s : 4 * (s & 1) + (s >> 1));
+    int col = n0 + 128 * half + 16 * (lane & 7);
+    col = (col < N) ? col : n0;  // chunks past N (N % 16 == 0) re-read a valid chunk
+    offB[q] = (uint32_t)(r * N + col);
+  }
+  const int ssz = (a.sdt == DT_F32) ? 4 : 2;
+  const int SB = BN * ssz;  // bytes of one scale row of the tile
+
+  auto issue = [&](int kt, int st) {
+    const int k0 = kt * BK;
+    const uint32_t base = lds0 + (uint32_t)(st * G::STAGE);
+    const void* xa = rfl_ptr(a.x + k0);
+#pragma unroll
+    for (int q = 0; q < G::A_DMA; ++q) dma_s(xa, offA[q], rfl(base + (uint32_t)((wave * G::A_DMA + q) * 1024)));
+    const void* wb = rfl_ptr(a.w + (long long)((WK == WK_W8) ? k0 : k0 / 2) * N);
+#pragma unroll
+    for (int q = 0; q < G::B_DMA; ++q)
+      dma_s(wb, offB[q], rfl(base + (uint32_t)(G::A_BYTES + (wave * G::B_DMA + q) * WBLK)));
+    if constexpr (WK == WK_W4) {
+      // scale rows of K substeps 0 and 1 (the same row when the group spans the
+      // tile), then zero rows; remaining lanes re-read a valid address
+      const int gr0 = k0 / a.group, gr1 = (k0 + 32) / a.group;
+      const int o = wave * 1024 + 16 * lane;
+      const void* p = a.s;
+      if (o < 2 * SB) {
+        const int gi = o / SB, inr = o % SB;
+        if (n0 + inr / ssz < N)
+          p = (const uint8_t*)a.s + ((long long)(gi ? gr1 : gr0) * N + n0) * ssz + inr;
+      } else if (HZ && o < 2 * SB + 2 * BN) {
+        const int gz = (o - 2 * SB) / BN, inr = (o - 2 * SB) % BN;
+        if (n0 + inr < N) p = a.z + (long long)(gz ? gr1 : gr0) * N + n0 + inr;
+      }
+      dma_v(p, rfl(base + (uint32_t)(G::A_BYTES + G::B_BYTES + wave * 1024)));
+    }
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[rb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Operands of one 32-wide K substep: 8 activation blocks, the raw weight dwords
+  // (8 int8 rows or 4 packed rows of 4 columns) and, for W4, 4 scales and 4 zeros.
+  struct Ops {
+    f16x8 av[8];
+    uint32_t d[8];
+    uint32_t sv[4];
+    uint32_t zv;
+  };
+  const int cc = wn * 64 + 4 * j;  // first of this lane's 4 columns within the tile
+  const int cb = (wn >> 1) * G::HB_BLOCKS * WBLK + (wn & 1) * 64 + 4 * j;  // its byte in a weight half
+
+  auto load_ops = [&](int st, int ks, Ops& o) {
+    const uint8_t* sA = lds + st * G::STAGE;
+    const uint8_t* sB = sA + G::A_BYTES;
+    const uint8_t* sS = sB + G::B_BYTES;
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb) {
+      const int row = wm * 128 + rb * 16 + j;
+      o.av[rb] = *(const f16x8*)(sA + row * 128 + 16 * ((4 * ks + g) ^ (j >> 1)));
+    }
+    if constexpr (WK == WK_W8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o.d[i] = *(const uint32_t*)(sB + (4 * ks + g) * WBLK + i * 128 + cb);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o.d[i] = *(const uint32_t*)(sB + (2 * ks + (g >> 1)) * WBLK + (2 * i + (g & 1)) * 128 + cb);
+      if (ssz == 4) {
+        const u32x4 v = *(const u32x4*)(sS + ks * SB + cc * 4);
+        o.sv[0] = v.x, o.sv[1] = v.y, o.sv[2] = v.z, o.sv[3] = v.w;
+      } else {
+        const u32x2 v = *(const u32x2*)(sS + ks * SB + cc * 2);
+        o.sv[0] = v.x & 0xFFFFu, o.sv[1] = v.x >> 16, o.sv[2] = v.y & 0xFFFFu, o.sv[3] = v.y >> 16;
+      }
+      o.zv = 0x08080808u;
+      if constexpr (HZ) o.zv = *(const uint32_t*)(sS + 2 * SB + ks * BN + cc);
+    }
+  };
+
+  // column-outer order: the dequantization of column t + 1 overlaps the 8 MFMAs of
+  // column t
+  auto mma = [&](const Ops& o) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      u32x4 h;
+      if constexpr (WK == WK_W8) {
+        h = u32x4{w8_pair_f16(o.d[0], o.d[1], t), w8_pair_f16(o.d[2], o.d[3], t), w8_pair_f16(o.d[4], o.d[5], t),
+                  w8_pair_f16(o.d[6], o.d[7], t)};
+      } else {
+        const f16x2 bias = w4_bias((o.zv >> (8 * t)) & 0xFFu);
+        const _Float16 sc = scale_f16(o.sv[t], a.sdt);
+        const f16x2 s2 = f16x2{sc, sc};
+        h.x = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[0], t, bias)) * s2);
+        h.y = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[1], t, bias)) * s2);
+        h.z = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[2], t, bias)) * s2);
+        h.w = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[3], t, bias)) * s2);
+      }
+      const f16x8 bv = bitcast<f16x8>(h);
+#pragma unroll
+      for (int rb = 0; rb < 8; ++rb) acc[rb][t] = mfma_f16(o.av[rb], bv, acc[rb][t]);
+    }
+  };
+
+  auto compute = [&](int st) {
+    Ops o0, o1;
+    load_ops(st, 0, o0);
+    load_ops(st, 1, o1);  // in flight while substep 0 computes
+    mma(o0);
+    mma(o1);
+    // schedule: every LDS read first (both substeps' operands stay live), the
+    // dequantization of the first weight operand, then each MFMA followed by two
+    // VALU slots so the remaining dequantization hides under the MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, 40, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+    }
+  };
+
+  const int nk = K / BK;
+#pragma unroll
+  for (int u = 0; u < NSTAGE - 1; ++u) issue(min(u, nk - 1), u);
+  for (int kt = 0; kt < nk; ++kt) {
+    // the oldest stage's copies (this wave's) are done; the barrier publishes every
+    // wave's copies and frees the stage computed in the previous iteration
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((NSTAGE - 2) * G::DMA));
+    asm volatile("s_barrier" ::: "memory");
+    // past the last tile the copy re-reads tile nk-1 into a stage never read again
+    issue(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
+    compute(kt % NSTAGE);
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no copy may outlive the workgroup
+
+  // epilogue: lane holds rows 4g..4g+3 of each 16-row block, columns 4j..4j+3 of the
+  // wave's 64 (MFMA t = column 4j + t)
+  const int colb = n0 + wn * 64 + 4 * j;
+  if (colb >= N) return;
+  float cs[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (WK == WK_W8) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) cs[t] = load_scale(a.s, a.sdt, colb + t);
+  }
+#pragma unroll
+  for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + wm * 128 + rb * 16 + 4 * g + r;
+      if (row >= M) continue;
+      float y[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) y[t] = acc[rb][t][r] * cs[t];
+      if (a.res) {
+        const u32x2 rv = *(const u32x2*)((const uint16_t*)a.res + (long long)row * a.ldr + colb);
+        const uint16_t rh[4] = {(uint16_t)rv.x, (uint16_t)(rv.x >> 16), (uint16_t)rv.y, (uint16_t)(rv.y >> 16)};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          y[t] += (a.odt == DT_BF16) ? bf16_to_f32(rh[t]) : (float)bitcast<_Float16>(rh[t]);
+      }
+      u32x2 o;
+      o.x = (uint32_t)to_out16(y[0], a.odt) | ((uint32_t)to_out16(y[1], a.odt) << 16);
+      o.y = (uint32_t)to_out16(y[2], a.odt) | ((uint32_t)to_out16(y[3], a.odt) << 16);
+      *(u32x2*)((uint16_t*)a.out + (long long)row * a.ldo + colb) = o;
+    }
+}
+
+template <int WK, bool HZ, int WM, int WN>
+static hipError_t launch_prefill_t(const TlArgs& a, hipStream_t st) {
+  using G = Geo<WK, WM, WN>;
+  const int tiles = ((a.M + G::BM - 1) / G::BM) * ((a.N + G::BN - 1) / G::BN);
+  const size_t lds = (size_t)NSTAGE * G::STAGE;
+  static bool attr_set = false;  // benign race: every caller sets the same value
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<WK, HZ, WM, WN>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((prefill_kernel<WK, HZ, WM, WN>), dim3(tiles), dim3(G::THREADS), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int WM, int WN>
+static hipError_t launch_prefill_g(const TlArgs& a, int wk, bool hz, hipStream_t st) {
+  if (wk == WK_W8) return launch_prefill_t<WK_W8, false, WM, WN>(a, st);
+  if (hz) return launch_prefill_t<WK_W4, true, WM, WN>(a, st);
+  return launch_prefill_t<WK_W4, false, WM, WN>(a, st);
+}
+
+hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t st) {
+  switch (shape) {
+    case PF_128x128: return launch_prefill_g<1, 2>(a, wk, hz, st);
+    case PF_256x128: return launch_prefill_g<2, 2>(a, wk, hz, st);
+    default: return launch_prefill_g<2, 4>(a, wk, hz, st);
+  }
+}
+
+}  // namespace qlin

@@ -69,6 +69,10 @@ struct TlArgs {
 
 hipError_t launch_tiled(const TlArgs& a, int wk, bool hz, int depth, hipStream_t stream);
 
+// LDS-DMA prefill kernel; `shape` picks the workgroup tile (rows x columns).
+enum PrefillShape { PF_128x128 = 0, PF_256x128 = 1, PF_256x256 = 2 };
+hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t stream);
+
 hipError_t launch_w4_unpack(const uint8_t* p, int K, int N, uint8_t* out, hipStream_t st);
 hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uint8_t* z,
                              int group, int K, int N, float* out, hipStream_t st);

@@ -205,10 +205,22 @@ def test_repeat_calls_are_deterministic():
 
 
 # ---------------------------------------------------------------- prefill (M > 16): tiled MFMA path
+#
+# The library picks the LDS-tiled MFMA kernel for M > 16 only when it has enough
+# tiles to fill the chip; QLIN_PREFILL=v2 forces it (and QLIN_PREFILL_SHAPE its
+# workgroup tile: 0 = 128x128, 1 = 256x128, 2 = 256x256) so these small cases
+# exercise every tile shape, edge tiles in M and N included.
 
-@pytest.mark.parametrize("M", [17, 128, 300])
+def _force_tiled(monkeypatch, shape):
+    monkeypatch.setenv("QLIN_PREFILL", "v2")
+    monkeypatch.setenv("QLIN_PREFILL_SHAPE", str(shape))
+
+
+@pytest.mark.parametrize("shape", [0, 1, 2])
+@pytest.mark.parametrize("M", [17, 300])
 @pytest.mark.parametrize("K,N", [(2048, 1024), (512, 2064)])
-def test_prefill_w8(M, K, N):
+def test_prefill_w8(M, K, N, shape, monkeypatch):
+    _force_tiled(monkeypatch, shape)
     x = H.act_f16(M, K, seed=300 + M)
     w, s = H.w8(K, N, seed=301)
     res = torch.randn((M, N), generator=H.gen(302)).to(torch.float16)
@@ -217,13 +229,15 @@ def test_prefill_w8(M, K, N):
                        H.linear_w8_ref_cols(x, w, s, np.arange(N), residual=res))
 
 
+@pytest.mark.parametrize("shape", [0, 2])
 @pytest.mark.parametrize("M", [40, 256])
 @pytest.mark.parametrize("group,zeros,sdt", [(128, "none", torch.float16), (32, "random", torch.float16),
                                              (64, "random", torch.bfloat16), (128, "eight", torch.float32)])
-def test_prefill_w4(M, group, zeros, sdt):
+def test_prefill_w4(M, group, zeros, sdt, shape, monkeypatch):
     """W4 prefill folds the group scale into the fp16 weight (one fp16 rounding per
     weight), so it is held to the GEMM tolerance, not bit-exactness."""
-    K, N = 1024, 1024
+    _force_tiled(monkeypatch, shape)
+    K, N = 1024, 1280
     x = H.act_f16(M, K, seed=310 + M)
     packed, s, z = H.w4(K, N, seed=311, group=group, zeros=zeros)
     s = s.to(sdt)
@@ -232,9 +246,26 @@ def test_prefill_w4(M, group, zeros, sdt):
                                                np.arange(N)))
 
 
-def test_prefill_rows_independent_of_chunking():
+def test_prefill_tile_shapes_agree(monkeypatch):
+    """Every workgroup tile shape accumulates each output element over the same K
+    order, so the three shapes give bit-identical results (W8 and W4 with zeros)."""
+    M, K, N = 300, 1024, 1280
+    x = H.act_f16(M, K, seed=340)
+    w, s = H.w8(K, N, seed=341)
+    packed, s4, z = H.w4(K, N, seed=342, group=64, zeros="random")
+    outs = []
+    for shape in (0, 1, 2):
+        _force_tiled(monkeypatch, shape)
+        outs.append((_run_w8(x, w, s), _run_w4(x, packed, s4, z)))
+    for o in outs[1:]:
+        assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1])
+
+
+@pytest.mark.parametrize("shape", [0, 2])
+def test_prefill_rows_independent_of_chunking(shape, monkeypatch):
     """Rows computed in one M=300 call equal the same rows computed as an M=100
-    chunk (the tiled family's per-row arithmetic does not depend on M)."""
+    chunk (the tiled kernel's per-row arithmetic does not depend on M)."""
+    _force_tiled(monkeypatch, shape)
     K, N = 2048, 1024
     x = H.act_f16(300, K, seed=320)
     w, s = H.w8(K, N, seed=321)
@@ -243,12 +274,25 @@ def test_prefill_rows_independent_of_chunking():
     assert torch.equal(y[100:200], yc)
 
 
+@pytest.mark.parametrize("M,K,N", [(512, 512, 4096), (1024, 256, 8192)])
+def test_prefill_default_dispatch(M, K, N):
+    """Sizes where the library itself picks the tiled kernel (128x128 and 256x256
+    tiles), checked on sampled columns against the oracle."""
+    x = H.act_f16(M, K, seed=350 + M)
+    w, s = H.w8(K, N, seed=351)
+    packed, s4, z = H.w4(K, N, seed=352, group=128, zeros="random")
+    cols = H.sample_cols(N, 512, seed=353)
+    H.assert_out_close(_run_w8(x, w, s).cpu()[:, cols], H.linear_w8_ref_cols(x, w, s, cols))
+    H.assert_out_close(_run_w4(x, packed, s4, z).cpu()[:, cols], H.linear_w4_ref_cols(x, packed, s4, z, cols))
+
+
 @pytest.mark.parametrize("K", [512, 576, 640, 2048])
 def test_prefill_ring_depths_agree(K, monkeypatch):
-    """The K-tile order of the tiled kernel does not depend on how many tiles of
-    global loads are in flight, so every ring depth (QLIN_TILED_DEPTH, a tuning
-    override) gives bit-identical outputs that also meet the oracle.  K covers
-    tile counts that are and are not multiples of each depth (8, 9, 10, 32)."""
+    """The register-ring tiled kernel (QLIN_PREFILL=v1): its K-tile order does not
+    depend on how many tiles of global loads are in flight, so every ring depth
+    (QLIN_TILED_DEPTH) gives bit-identical outputs that also meet the oracle.  K
+    covers tile counts that are and are not multiples of each depth (8, 9, 10, 32)."""
+    monkeypatch.setenv("QLIN_PREFILL", "v1")
     M, N = 200, 1024
     x = H.act_f16(M, K, seed=330 + K)
     w, s = H.w8(K, N, seed=331)
