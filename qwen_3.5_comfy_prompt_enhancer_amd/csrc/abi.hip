@@ -32,7 +32,7 @@ int hip_status(const char* fn, hipError_t e) {
 }
 
 // Workspace: [counters | partial sums].  Counters must be zero between calls.
-constexpr size_t kWorkspaceBytes = size_t(64) << 20;
+constexpr size_t kWorkspaceBytes = size_t(256) << 20;
 constexpr size_t kCounterBytes = size_t(1) << 20;
 constexpr int kWideTiles = 512;          // 256-column tiles at which no K split is needed
 // narrow launches: most waves to spread K over, and least K per wave (measured)
@@ -341,6 +341,51 @@ int engine_gate_up(const char* fn, int wk, int epi, const int8_t* a_q, const flo
   return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
 }
 
+// Prefill plan: the LDS-tiled kernel with a tile shape and a split-K factor, or the
+// skinny kernel over row tiles, whichever a time model fitted to MI355X
+// measurements (fp16 x int8, W4 about 1.3x slower per tile) prefers:
+//   tiled:  fixed + rounds x (K tiles per workgroup) x t_tile(workgroups per CU)
+//           + split-K partial traffic (about 3.6 us per MB written and read back)
+//   skinny: fixed + cost per (row x MB of int8-sized weights): its 16-row tiles
+//           re-read the weights from L2
+struct PfPlan {
+  bool tiled;
+  int shape;
+  int splits;
+};
+
+PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
+  struct Cand {
+    int shape;
+    int per_cu;        // workgroups one CU can hold
+    double t_tile[2];  // seconds per 64-wide K tile of a workgroup, 1 or 2 per CU
+  };
+  const double w4f = (wk == WK_W4) ? 1.3 : 1.0;
+  const Cand cands[2] = {{PF_128x128_K2, 2, {0.66e-6, 1.35e-6}}, {PF_256x256, 1, {1.96e-6, 1.96e-6}}};
+  const int nk = K / 64;
+  PfPlan best{false, PF_128x128_K2, 1};
+  double best_t = 9.8e-6 + 6.3e-9 * M * ((double)K * N / 1e6);
+  for (const Cand& c : cands) {
+    int bm, bn, waves;
+    prefill_geometry(c.shape, &bm, &bn, &waves);
+    const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    for (int S = 1; S <= 16; S *= 2) {
+      if (nk % S != 0 || nk / S < 2) break;
+      const double part_bytes = (double)tiles * S * waves * 128 * 64 * sizeof(float);
+      if (S > 1 && (part_bytes > (double)part_cap || tiles > (long long)(kCounterBytes / sizeof(unsigned)))) break;
+      const long long wgs = tiles * S;
+      const int occ = (wgs > 256 && c.per_cu > 1) ? 2 : 1;
+      const double rounds = (double)((wgs + 256LL * occ - 1) / (256LL * occ));
+      const double t = 5e-6 + rounds * (nk / S) * c.t_tile[occ - 1] * w4f + (S > 1 ? part_bytes * 3.6e-12 : 0.0);
+      if (t < best_t) {
+        best_t = t;
+        best = PfPlan{true, c.shape, S};
+      }
+    }
+  }
+  return best;
+}
+
 int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K, int64_t ldx, const void* w,
                const void* scale, int s_dtype, const uint8_t* zero, int group, int N, void* out, int out_dtype,
                int64_t ldo, const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream) {
@@ -358,17 +403,18 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
   QL_TRY(check_weight(fn, w, scale, zero, N, wk));
   QL_TRY(check_out16(fn, out, ldo, N, "out"));
   if (residual) QL_TRY(check_out16(fn, residual, ldr, N, "residual"));
-  // More than 16 rows: the LDS-tiled MFMA kernel when it has enough tiles to fill the
-  // chip, else row tiles of 16 through the skinny kernel (whose weight re-reads per
-  // row tile come from L2).  QLIN_PREFILL ("skinny", "v1") overrides for tuning.
+  // More than 16 rows: the LDS-tiled MFMA kernel (tile shape and split-K from a time
+  // model) or row tiles of 16 through the skinny kernel, whichever the model prefers.
+  // QLIN_PREFILL ("skinny", "v1", "v2"), QLIN_PREFILL_SHAPE and QLIN_PREFILL_SPLITS
+  // override the choice for tuning.
   const char* pimpl = getenv("QLIN_PREFILL");
-  const long long tiles128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
-  const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
-  bool tiled = M > 256 && K % 64 == 0 && tiles128 >= 128;
-  if (pimpl && strcmp(pimpl, "skinny") == 0) tiled = false;
-  if (pimpl && (strcmp(pimpl, "v1") == 0 || strcmp(pimpl, "v2") == 0)) tiled = M > 16 && K % 64 == 0;
-  if (tiled) {
-    // prefill: LDS-tiled MFMA GEMM (K in tiles of 64; other K take the row-tiled skinny path)
+  const bool force_skinny = pimpl && strcmp(pimpl, "skinny") == 0;
+  const bool force_v1 = pimpl && strcmp(pimpl, "v1") == 0;
+  const bool force_v2 = pimpl && strcmp(pimpl, "v2") == 0;
+  // the DMA kernel addresses activations with 32-bit byte offsets
+  const bool fits32 = ((long long)(M - 1) * ldx + K) * 2 < (1LL << 31);
+  const size_t part_cap = (ws && wsb > kCounterBytes) ? wsb - kCounterBytes : 0;
+  if (M > 16 && K % 64 == 0 && !force_skinny) {
     TlArgs t;
     t.x = (const _Float16*)x;
     t.ldx = ldx;
@@ -385,19 +431,43 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
     t.odt = out_dtype;
     t.res = residual;
     t.ldr = ldr;
-    const char* impl = getenv("QLIN_PREFILL");  // tuning override: "v1" = register-ring kernel
-    // the DMA kernel addresses activations with 32-bit byte offsets
-    const bool fits32 = ((long long)(M - 1) * ldx + K) * 2 < (1LL << 31);
-    if (fits32 && !(impl && strcmp(impl, "v1") == 0)) {
-      int shape = (tiles256 >= 128) ? PF_256x256 : PF_128x128;
-      const char* e = getenv("QLIN_PREFILL_SHAPE");  // tuning override (0, 1 or 2)
-      if (e && *e) shape = atoi(e);
-      return hip_status(fn, launch_prefill(t, wk, zero != nullptr, shape, (hipStream_t)stream));
+    t.splits = 1;
+    t.part = nullptr;
+    t.cnt = nullptr;
+    if (force_v1) {
+      int depth = 3;
+      const char* e = getenv("QLIN_TILED_DEPTH");  // tuning override (2, 3 or 4)
+      if (e && *e) depth = atoi(e);
+      return hip_status(fn, launch_tiled(t, wk, zero != nullptr, depth, (hipStream_t)stream));
     }
-    int depth = 3;
-    const char* e = getenv("QLIN_TILED_DEPTH");  // tuning override (2, 3 or 4)
-    if (e && *e) depth = atoi(e);
-    return hip_status(fn, launch_tiled(t, wk, zero != nullptr, depth, (hipStream_t)stream));
+    if (fits32) {
+      PfPlan p = plan_prefill(wk, M, K, N, part_cap);
+      if (getenv("QLIN_PREFILL_VERBOSE"))
+        fprintf(stderr, "qlin prefill plan M=%d K=%d N=%d: %s shape=%d splits=%d\n", M, K, N,
+                p.tiled ? "tiled" : "skinny", p.shape, p.splits);
+      const char* e = getenv("QLIN_PREFILL_SHAPE");
+      const char* e2 = getenv("QLIN_PREFILL_SPLITS");
+      if ((e && *e) || (e2 && *e2)) {
+        p.tiled = true;
+        if (e && *e) p.shape = atoi(e);
+        p.splits = (e2 && *e2) ? atoi(e2) : 1;
+        int bm, bn, waves;
+        prefill_geometry(p.shape, &bm, &bn, &waves);
+        const size_t tiles = (size_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        if (p.splits < 1 || (K / 64) % p.splits != 0 ||
+            (p.splits > 1 && (tiles * p.splits * waves * 128 * 64 * sizeof(float) > part_cap ||
+                              tiles > kCounterBytes / sizeof(unsigned))))
+          return fail(QLIN_ERR_UNSUPPORTED, "%s: QLIN_PREFILL_SPLITS=%d unusable here", fn, p.splits);
+      }
+      if (p.tiled || force_v2) {
+        t.splits = p.splits;
+        if (p.splits > 1) {
+          t.cnt = (unsigned*)ws;
+          t.part = (float*)((char*)ws + kCounterBytes);
+        }
+        return hip_status(fn, launch_prefill(t, wk, zero != nullptr, p.shape, (hipStream_t)stream));
+      }
+    }
   }
   SkArgs a = base_args();
   a.x = x;

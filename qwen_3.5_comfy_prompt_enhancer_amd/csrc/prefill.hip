@@ -29,8 +29,15 @@
 //     issued from inline assembly so the compiler's wait insertion, which would
 //     otherwise drain every in-flight copy before each LDS read, leaves the ring
 //     alone; the waits are explicit and count this kernel's own copies only.
-//   * The K order of every output element is fixed (tiles 0..K/64-1, two 32-wide
-//     substeps each), so a row's result does not depend on M.
+//   * Split-K: `splits` workgroups share an output tile, each over a contiguous
+//     range of K tiles.  Each stores its fp32 partial tile (agent-scope atomic
+//     stores, coherent across XCDs), waits for the stores, and bumps the tile's
+//     arrival counter; the last to arrive sums the partials in split order, resets
+//     the counter and runs the epilogue.  The sum order is fixed, so results are
+//     deterministic.
+//   * The K order of every output element is fixed (tiles in order, two 32-wide
+//     substeps each, partials summed in split order), so a row's result depends on
+//     the split count but not on M or on the tile shape.
 #include "qlin_dev.h"
 #include "qlin_internal.h"
 
@@ -40,14 +47,14 @@ namespace {
 
 constexpr int BK = 64;           // K per stage
 constexpr int WBLK = 1024 + 64;  // LDS bytes of one 8-row weight block (rows of 128 B + pad)
-constexpr int NSTAGE = 3;
 constexpr int GROUP_M = 8;       // tile order: 8 row tiles per group
 
-template <int WK, int WM, int WN>
+template <int WK, int WM, int WN, int KG, int NS = 3>
 struct Geo {
+  static constexpr int NSTAGE = NS;  // K tiles in the LDS ring
   static constexpr int BM = 128 * WM;
   static constexpr int BN = 64 * WN;  // WN even: the weight tile is stored in 128-column halves
-  static constexpr int WAVES = WM * WN;
+  static constexpr int WAVES = WM * WN * KG;  // KG wave groups split each K tile's substeps
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int A_BYTES = BM * 128;
   static constexpr int HB_BLOCKS = (WK == WK_W8) ? 8 : 4;  // 64 int8 rows or 32 packed rows per half
@@ -60,6 +67,8 @@ struct Geo {
   static constexpr int DMA = A_DMA + B_DMA + (WK == WK_W4 ? 1 : 0);  // copies per wave per stage
   static constexpr int OCC = (WAVES >= 8) ? 2 : 1;                    // waves per SIMD
   static_assert(WN % 2 == 0 && (BM / 8) % WAVES == 0 && B_BLOCKS % WAVES == 0, "tile geometry");
+  static_assert(KG == 1 || KG == 2, "one or two K groups");
+  static_assert(KG == 1 || NSTAGE * STAGE >= WM * WN * 128 * 64 * 4, "LDS for the K-group reduction");
   static_assert(WK == WK_W8 || 10 * BN <= SC_BYTES, "W4 scale region");
 };
 
@@ -93,10 +102,12 @@ __device__ __forceinline__ _Float16 scale_f16(uint32_t bits, int dt) {
 
 }  // namespace
 
-template <int WK, bool HZ, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(Geo<WK, WM, WN>::OCC, Geo<WK, WM, WN>::OCC)))
+template <int WK, bool HZ, int WM, int WN, int KG, int NS>
+__global__ __launch_bounds__(64 * WM * WN * KG)
+__attribute__((amdgpu_waves_per_eu(Geo<WK, WM, WN, KG, NS>::OCC, Geo<WK, WM, WN, KG, NS>::OCC)))
 void prefill_kernel(const TlArgs a) {
-  using G = Geo<WK, WM, WN>;
+  using G = Geo<WK, WM, WN, KG, NS>;
+  constexpr int NSTAGE = G::NSTAGE;
   constexpr int BN = G::BN;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
@@ -104,12 +115,17 @@ void prefill_kernel(const TlArgs a) {
   const int tid = threadIdx.x;
   const int wave = (int)rfl((uint32_t)tid >> 6), lane = tid & 63;  // wave index in an SGPR
   const int j = lane & 15, g = lane >> 4;
-  const int wm = wave / WN, wn = wave % WN;
+  const int kg = wave / (WM * WN);  // K group: with KG = 2, group kg computes substep kg
+  const int wl = wave % (WM * WN);  // wave within its group
+  const int wm = wl / WN, wn = wl % WN;
   const int M = a.M, N = a.N, K = a.K;
 
   // grouped tile order: consecutive workgroups share weight column tiles in L2
   const int tiles_m = (M + G::BM - 1) / G::BM, tiles_n = (N + BN - 1) / BN;
-  const int pid = blockIdx.x;
+  const int S = a.splits;
+  const int split = blockIdx.x % S;
+  const int tile = blockIdx.x / S;
+  const int pid = tile;
   const int per_group = GROUP_M * tiles_n;
   const int first_m = (pid / per_group) * GROUP_M;
   const int gsize = min(tiles_m - first_m, GROUP_M);
@@ -242,42 +258,172 @@ void prefill_kernel(const TlArgs a) {
     }
   };
 
-  auto compute = [&](int st) {
-    Ops o0, o1;
-    load_ops(st, 0, o0);
-    load_ops(st, 1, o1);  // in flight while substep 0 computes
-    mma(o0);
-    mma(o1);
-    // schedule: every LDS read first (both substeps' operands stay live), the
-    // dequantization of the first weight operand, then each MFMA followed by two
-    // VALU slots so the remaining dequantization hides under the MFMAs
-    __builtin_amdgcn_sched_group_barrier(0x100, 40, 0);  // DS reads
-    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU
+  // Software pipeline, one barrier per K tile, placed between the two substeps:
+  //   load substep-1 operands of tile kt  | MFMAs of tile kt substep 0
+  //   wait: this wave's LDS reads returned, tile kt+1 copied; barrier
+  //   DMA tile kt + NSTAGE into tile kt's stage (every wave has read it)
+  //   load substep-0 operands of tile kt+1 | MFMAs of tile kt substep 1
+  // LDS reads always overlap MFMAs, and a wave waiting at the barrier still has
+  // its substep-0 MFMAs executing.
+  auto schedule = [&]() {
+    // dequantization of the first weight operand, then each MFMA with one LDS read
+    // and two VALU slots
+    __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
+    for (int i = 0; i < 32; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
     }
   };
 
-  const int nk = K / BK;
+  // this workgroup's K tiles: kb .. kb + nk - 1
+  const int nk = K / BK / S;
+  const int kb = split * nk;
 #pragma unroll
-  for (int u = 0; u < NSTAGE - 1; ++u) issue(min(u, nk - 1), u);
-  for (int kt = 0; kt < nk; ++kt) {
-    // the oldest stage's copies (this wave's) are done; the barrier publishes every
-    // wave's copies and frees the stage computed in the previous iteration
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((NSTAGE - 2) * G::DMA));
+  for (int u = 0; u < NSTAGE - 1; ++u) issue(kb + min(u, nk - 1), u);
+  // With one wave per SIMD (registers to spare) the loops below are unrolled by
+  // NSTAGE so that every LDS stage index is a compile-time constant in the main
+  // loop (no per-iteration address arithmetic); a runtime-indexed copy of the body
+  // finishes the last nk % NSTAGE tiles.  Two waves per SIMD keep the rolled loop
+  // (its 256 registers would not hold the unrolled one).
+  constexpr int UNROLL = (G::OCC == 1) ? NSTAGE : 1;
+  if constexpr (KG == 2) {
+    // each wave computes one substep per tile: wait for the tile, barrier (which also
+    // frees the stage computed in the previous iteration), copy ahead, compute
+    auto body = [&](int kt, int st) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((NSTAGE - 2) * G::DMA));
+      asm volatile("s_barrier" ::: "memory");
+      issue(kb + min(kt + NSTAGE - 1, nk - 1), (st + NSTAGE - 1) % NSTAGE);
+      __builtin_amdgcn_sched_barrier(0);
+      Ops o;
+      load_ops(st, kg, o);
+      mma(o);
+      __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // DS reads
+      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+      }
+    };
+    int kt = 0;
+    if constexpr (UNROLL > 1) {
+      for (; kt + NSTAGE <= nk; kt += NSTAGE) {
+#pragma unroll
+        for (int u = 0; u < NSTAGE; ++u) body(kt + u, u);
+      }
+    }
+    for (; kt < nk; ++kt) body(kt, kt % NSTAGE);
+  } else {
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((NSTAGE - 2) * G::DMA));  // first tile copied
     asm volatile("s_barrier" ::: "memory");
-    // past the last tile the copy re-reads tile nk-1 into a stage never read again
-    issue(min(kt + NSTAGE - 1, nk - 1), (kt + NSTAGE - 1) % NSTAGE);
-    compute(kt % NSTAGE);
+    issue(kb + min(NSTAGE - 1, nk - 1), NSTAGE - 1);
+    Ops o0, o1;
+    load_ops(0, 0, o0);
+    auto body = [&](int kt, int st) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_ops(st, 1, o1);
+      mma(o0);
+      schedule();
+      __builtin_amdgcn_sched_barrier(0);
+      // outstanding copies: tiles kt+1 .. kt+NSTAGE-1; wait for kt+1 (and for every
+      // LDS read of stage st), then hand stage st to the copy of tile kt + NSTAGE
+      // (past the last tile it re-reads tile nk-1 into a stage never read again)
+      __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0((NSTAGE - 2) * G::DMA));
+      asm volatile("s_barrier" ::: "memory");
+      issue(kb + min(kt + NSTAGE, nk - 1), st);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 1 < nk) load_ops((st + 1) % NSTAGE, 0, o0);
+      mma(o1);
+      schedule();
+    };
+    int kt = 0;
+    if constexpr (UNROLL > 1) {
+      for (; kt + NSTAGE <= nk; kt += NSTAGE) {
+#pragma unroll
+        for (int u = 0; u < NSTAGE; ++u) body(kt + u, u);
+      }
+    }
+    for (; kt < nk; ++kt) body(kt, kt % NSTAGE);
   }
+  __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));  // no copy may outlive the workgroup
+
+  if constexpr (KG == 2) {
+    // K-group reduction through the (now idle) LDS stages: group 1 writes its
+    // accumulators, group 0 adds them (fixed order: group 0 + group 1)
+    float* red = (float*)lds + (long long)wl * (128 * 64) + lane;
+    asm volatile("s_barrier" ::: "memory");  // every wave's last LDS read has returned
+    if (kg == 1) {
+#pragma unroll
+      for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[((rb * 4 + t) * 4 + r) * 64] = acc[rb][t][r];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[rb][t][r] += red[((rb * 4 + t) * 4 + r) * 64];
+    }
+  }
+
+  if (S > 1) {
+    // partial tile of this wave: element e = (rb * 4 + t) * 4 + r of every lane,
+    // lane-minor so each store instruction writes 256 contiguous bytes
+    __shared__ int s_last;
+    const long long wslot = 128LL * 64;
+    float* mine = a.part + (((long long)tile * S + split) * G::WAVES + wl) * wslot + lane;
+    if (kg == 0) {
+#pragma unroll
+      for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            __hip_atomic_store(mine + ((rb * 4 + t) * 4 + r) * 64, acc[rb][t][r], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev == (unsigned)(S - 1);
+      if (last) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last || kg != 0) return;  // uniform over each wave
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const float* base = a.part + ((long long)tile * S * G::WAVES + wl) * wslot + lane;
+    const long long sstride = (long long)G::WAVES * wslot;
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float* pp = base + ((rb * 4 + t) * 4 + r) * 64;
+          float v = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int sp = 1; sp < S; ++sp)
+            v += __hip_atomic_load(pp + sp * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          acc[rb][t][r] = v;
+        }
+  }
 
   // epilogue: lane holds rows 4g..4g+3 of each 16-row block, columns 4j..4j+3 of the
   // wave's 64 (MFMA t = column 4j + t)
   const int colb = n0 + wn * 64 + 4 * j;
-  if (colb >= N) return;
+  if (kg != 0 || colb >= N) return;
   float cs[4] = {1.f, 1.f, 1.f, 1.f};
   if constexpr (WK == WK_W8) {
 #pragma unroll
@@ -306,34 +452,47 @@ void prefill_kernel(const TlArgs a) {
     }
 }
 
-template <int WK, bool HZ, int WM, int WN>
+template <int WK, bool HZ, int WM, int WN, int KG, int NS>
 static hipError_t launch_prefill_t(const TlArgs& a, hipStream_t st) {
-  using G = Geo<WK, WM, WN>;
-  const int tiles = ((a.M + G::BM - 1) / G::BM) * ((a.N + G::BN - 1) / G::BN);
-  const size_t lds = (size_t)NSTAGE * G::STAGE;
+  using G = Geo<WK, WM, WN, KG, NS>;
+  const int tiles = ((a.M + G::BM - 1) / G::BM) * ((a.N + G::BN - 1) / G::BN) * a.splits;
+  const size_t lds = (size_t)G::NSTAGE * G::STAGE;
   static bool attr_set = false;  // benign race: every caller sets the same value
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<WK, HZ, WM, WN>,
+    const hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<WK, HZ, WM, WN, KG, NS>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((prefill_kernel<WK, HZ, WM, WN>), dim3(tiles), dim3(G::THREADS), lds, st, a);
+  hipLaunchKernelGGL((prefill_kernel<WK, HZ, WM, WN, KG, NS>), dim3(tiles), dim3(G::THREADS), lds, st, a);
   return hipGetLastError();
 }
 
-template <int WM, int WN>
+template <int WM, int WN, int KG, int NS>
 static hipError_t launch_prefill_g(const TlArgs& a, int wk, bool hz, hipStream_t st) {
-  if (wk == WK_W8) return launch_prefill_t<WK_W8, false, WM, WN>(a, st);
-  if (hz) return launch_prefill_t<WK_W4, true, WM, WN>(a, st);
-  return launch_prefill_t<WK_W4, false, WM, WN>(a, st);
+  if (wk == WK_W8) return launch_prefill_t<WK_W8, false, WM, WN, KG, NS>(a, st);
+  if (hz) return launch_prefill_t<WK_W4, true, WM, WN, KG, NS>(a, st);
+  return launch_prefill_t<WK_W4, false, WM, WN, KG, NS>(a, st);
+}
+
+void prefill_geometry(int shape, int* bm, int* bn, int* waves) {
+  using G0 = Geo<WK_W8, 1, 2, 1>;
+  using G1 = Geo<WK_W8, 2, 2, 1>;
+  using G2 = Geo<WK_W8, 2, 4, 1>;
+  using G3 = Geo<WK_W8, 1, 2, 2>;
+  if (shape == PF_128x128) *bm = G0::BM, *bn = G0::BN, *waves = G0::WAVES;
+  else if (shape == PF_256x128) *bm = G1::BM, *bn = G1::BN, *waves = G1::WAVES;
+  else if (shape == PF_128x128_K2 || shape == PF_128x128_K2_DEEP) *bm = G3::BM, *bn = G3::BN, *waves = G3::WAVES;
+  else *bm = G2::BM, *bn = G2::BN, *waves = G2::WAVES;
 }
 
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t st) {
   switch (shape) {
-    case PF_128x128: return launch_prefill_g<1, 2>(a, wk, hz, st);
-    case PF_256x128: return launch_prefill_g<2, 2>(a, wk, hz, st);
-    default: return launch_prefill_g<2, 4>(a, wk, hz, st);
+    case PF_128x128: return launch_prefill_g<1, 2, 1, 3>(a, wk, hz, st);
+    case PF_256x128: return launch_prefill_g<2, 2, 1, 3>(a, wk, hz, st);
+    case PF_128x128_K2: return launch_prefill_g<1, 2, 2, 3>(a, wk, hz, st);
+    case PF_128x128_K2_DEEP: return launch_prefill_g<1, 2, 2, 6>(a, wk, hz, st);
+    default: return launch_prefill_g<2, 4, 1, 3>(a, wk, hz, st);
   }
 }
 

@@ -65,13 +65,20 @@ struct TlArgs {
   int odt;
   const void* res;    // 16-bit [M][ldr] or nullptr
   long long ldr;
+  int splits;         // workgroups per output tile along K (LDS-DMA kernel)
+  float* part;        // split-K partials [tiles][splits][waves][128 * 64], or nullptr
+  unsigned* cnt;      // split-K arrival counters [tiles], zero between calls
 };
 
 hipError_t launch_tiled(const TlArgs& a, int wk, bool hz, int depth, hipStream_t stream);
 
 // LDS-DMA prefill kernel; `shape` picks the workgroup tile (rows x columns).
-enum PrefillShape { PF_128x128 = 0, PF_256x128 = 1, PF_256x256 = 2 };
+// PF_128x128_K2: two wave groups split every K tile's two substeps (4 waves);
+// _DEEP: the same with a 6-tile LDS ring (one workgroup per CU, more copies in flight).
+enum PrefillShape { PF_128x128 = 0, PF_256x128 = 1, PF_256x256 = 2, PF_128x128_K2 = 3, PF_128x128_K2_DEEP = 4 };
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t stream);
+// rows, columns and waves of a prefill workgroup tile
+void prefill_geometry(int shape, int* bm, int* bn, int* waves);
 
 hipError_t launch_w4_unpack(const uint8_t* p, int K, int N, uint8_t* out, hipStream_t st);
 hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uint8_t* z,

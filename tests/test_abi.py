@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_workspace():
     _, L = _lib()
     assert L.qlin_version() == 1
-    assert L.qlin_workspace_bytes() == 64 << 20
+    assert L.qlin_workspace_bytes() == 256 << 20
     assert L.qlin_last_error() == b""
 
 

@@ -208,15 +208,16 @@ def test_repeat_calls_are_deterministic():
 #
 # The library picks the LDS-tiled MFMA kernel for M > 16 only when it has enough
 # tiles to fill the chip; QLIN_PREFILL=v2 forces it (and QLIN_PREFILL_SHAPE its
-# workgroup tile: 0 = 128x128, 1 = 256x128, 2 = 256x256) so these small cases
-# exercise every tile shape, edge tiles in M and N included.
+# workgroup tile: 0 = 128x128, 1 = 256x128, 2 = 256x256, 3 = 128x128 with two wave
+# groups splitting each K tile, 4 = the same with a 6-tile LDS ring) so these small
+# cases exercise every tile shape, edge tiles in M and N included.
 
 def _force_tiled(monkeypatch, shape):
     monkeypatch.setenv("QLIN_PREFILL", "v2")
     monkeypatch.setenv("QLIN_PREFILL_SHAPE", str(shape))
 
 
-@pytest.mark.parametrize("shape", [0, 1, 2])
+@pytest.mark.parametrize("shape", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("M", [17, 300])
 @pytest.mark.parametrize("K,N", [(2048, 1024), (512, 2064)])
 def test_prefill_w8(M, K, N, shape, monkeypatch):
@@ -229,7 +230,7 @@ def test_prefill_w8(M, K, N, shape, monkeypatch):
                        H.linear_w8_ref_cols(x, w, s, np.arange(N), residual=res))
 
 
-@pytest.mark.parametrize("shape", [0, 2])
+@pytest.mark.parametrize("shape", [0, 2, 3, 4])
 @pytest.mark.parametrize("M", [40, 256])
 @pytest.mark.parametrize("group,zeros,sdt", [(128, "none", torch.float16), (32, "random", torch.float16),
                                              (64, "random", torch.bfloat16), (128, "eight", torch.float32)])
@@ -247,8 +248,10 @@ def test_prefill_w4(M, group, zeros, sdt, shape, monkeypatch):
 
 
 def test_prefill_tile_shapes_agree(monkeypatch):
-    """Every workgroup tile shape accumulates each output element over the same K
-    order, so the three shapes give bit-identical results (W8 and W4 with zeros)."""
+    """Every single-group workgroup tile shape accumulates each output element over
+    the same K order, so the three shapes give bit-identical results (W8 and W4 with
+    zeros).  The two-group shape sums its groups' substeps separately (another
+    rounding order) and is checked against the oracle instead."""
     M, K, N = 300, 1024, 1280
     x = H.act_f16(M, K, seed=340)
     w, s = H.w8(K, N, seed=341)
@@ -261,7 +264,29 @@ def test_prefill_tile_shapes_agree(monkeypatch):
         assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1])
 
 
-@pytest.mark.parametrize("shape", [0, 2])
+@pytest.mark.parametrize("shape,splits", [(0, 2), (0, 16), (2, 4), (2, 8), (3, 4), (4, 2)])
+def test_prefill_split_k(shape, splits, monkeypatch):
+    """Split-K: each of `splits` workgroups per tile covers K/splits; the last to
+    arrive sums the fp32 partials in split order.  Checked against the oracle (W8
+    with residual, W4 with zeros and bf16 out) and for bit-identical repeat calls
+    (the arrival order must not matter)."""
+    _force_tiled(monkeypatch, shape)
+    monkeypatch.setenv("QLIN_PREFILL_SPLITS", str(splits))
+    M, K, N = 300, 1024, 1280
+    x = H.act_f16(M, K, seed=360 + splits)
+    w, s = H.w8(K, N, seed=361)
+    res = torch.randn((M, N), generator=H.gen(362)).to(torch.float16)
+    y = _run_w8(x, w, s, residual=res)
+    H.assert_out_close(y, H.linear_w8_ref_cols(x, w, s, np.arange(N), residual=res))
+    for _ in range(2):
+        assert torch.equal(_run_w8(x, w, s, residual=res), y)
+    packed, s4, z = H.w4(K, N, seed=363, group=128, zeros="random")
+    y4 = _run_w4(x, packed, s4, z, out_dtype=torch.bfloat16)
+    H.assert_out_close(y4, H.linear_w4_ref_cols(x, packed, s4, z, np.arange(N)))
+    assert torch.equal(_run_w4(x, packed, s4, z, out_dtype=torch.bfloat16), y4)
+
+
+@pytest.mark.parametrize("shape", [0, 2, 3, 4])
 def test_prefill_rows_independent_of_chunking(shape, monkeypatch):
     """Rows computed in one M=300 call equal the same rows computed as an M=100
     chunk (the tiled kernel's per-row arithmetic does not depend on M)."""
