@@ -405,12 +405,11 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
   if (residual) QL_TRY(check_out16(fn, residual, ldr, N, "residual"));
   // More than 16 rows: the LDS-tiled MFMA kernel (tile shape and split-K from a time
   // model) or row tiles of 16 through the skinny kernel, whichever the model prefers.
-  // QLIN_PREFILL ("skinny", "v1", "v2"), QLIN_PREFILL_SHAPE and QLIN_PREFILL_SPLITS
+  // QLIN_PREFILL ("skinny" or "tiled"), QLIN_PREFILL_SHAPE and QLIN_PREFILL_SPLITS
   // override the choice for tuning.
   const char* pimpl = getenv("QLIN_PREFILL");
   const bool force_skinny = pimpl && strcmp(pimpl, "skinny") == 0;
-  const bool force_v1 = pimpl && strcmp(pimpl, "v1") == 0;
-  const bool force_v2 = pimpl && strcmp(pimpl, "v2") == 0;
+  const bool force_tiled = pimpl && strcmp(pimpl, "tiled") == 0;
   // the DMA kernel addresses activations with 32-bit byte offsets
   const bool fits32 = ((long long)(M - 1) * ldx + K) * 2 < (1LL << 31);
   const size_t part_cap = (ws && wsb > kCounterBytes) ? wsb - kCounterBytes : 0;
@@ -434,12 +433,6 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
     t.splits = 1;
     t.part = nullptr;
     t.cnt = nullptr;
-    if (force_v1) {
-      int depth = 3;
-      const char* e = getenv("QLIN_TILED_DEPTH");  // tuning override (2, 3 or 4)
-      if (e && *e) depth = atoi(e);
-      return hip_status(fn, launch_tiled(t, wk, zero != nullptr, depth, (hipStream_t)stream));
-    }
     if (fits32) {
       PfPlan p = plan_prefill(wk, M, K, N, part_cap);
       if (getenv("QLIN_PREFILL_VERBOSE"))
@@ -459,7 +452,7 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
                               tiles > kCounterBytes / sizeof(unsigned))))
           return fail(QLIN_ERR_UNSUPPORTED, "%s: QLIN_PREFILL_SPLITS=%d unusable here", fn, p.splits);
       }
-      if (p.tiled || force_v2) {
+      if (p.tiled || force_tiled) {
         t.splits = p.splits;
         if (p.splits > 1) {
           t.cnt = (unsigned*)ws;

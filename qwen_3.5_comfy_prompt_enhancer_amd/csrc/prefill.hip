@@ -8,7 +8,10 @@
 //     owning a 128 x 64 output tile = 8 x 4 blocks of v_mfma_f32_16x16x32_f16 with
 //     fp32 accumulation.  Tall wave tiles make every dequantized weight operand feed
 //     8 MFMAs.  With 8 waves (256 x 256) two waves share each SIMD, so one wave's
-//     dequantization and LDS traffic issue while the other's MFMAs run.
+//     dequantization and LDS traffic issue while the other's MFMAs run.  With KG = 2
+//     wave groups, each group computes one of the two 32-wide substeps of every K
+//     tile and the groups' accumulators are added through LDS at the end: twice the
+//     waves for the same tile, for shapes with few tiles.
 //   * Global -> LDS copies are 16-byte LDS DMA (global_load_lds_dwordx4): no VGPR
 //     staging.  Activation tiles land as 128-byte rows of 64 halves with the 16-byte
 //     chunk c of row r stored at position c ^ ((r >> 1) & 7), which makes the MFMA
@@ -23,12 +26,12 @@
 //     W8 values are exact integers in fp16 and the column scale multiplies the fp32
 //     result; W4 (nibble - z) is exact and the group scale is folded into the fp16
 //     weight (one fp16 rounding per weight).
-//   * NSTAGE K tiles of 64 in an LDS ring.  Each iteration waits (vmcnt) for the
-//     oldest tile, passes one barrier, issues the DMA of the tile NSTAGE - 1 ahead
-//     into the stage freed by the previous iteration, and computes.  The DMA is
-//     issued from inline assembly so the compiler's wait insertion, which would
-//     otherwise drain every in-flight copy before each LDS read, leaves the ring
-//     alone; the waits are explicit and count this kernel's own copies only.
+//   * NSTAGE K tiles of 64 in an LDS ring with one barrier per tile.  Before it, a
+//     wave waits (vmcnt) for the copy of the next tile it needs; after it, the stage
+//     every wave has finished reading receives the copy of the tile NSTAGE ahead.
+//     The DMA is issued from inline assembly so the compiler's wait insertion, which
+//     would otherwise drain every in-flight copy before each LDS read, leaves the
+//     ring alone; the waits are explicit and count this kernel's own copies only.
 //   * Split-K: `splits` workgroups share an output tile, each over a contiguous
 //     range of K tiles.  Each stores its fp32 partial tile (agent-scope atomic
 //     stores, coherent across XCDs), waits for the stores, and bumps the tile's
@@ -37,7 +40,7 @@
 //     deterministic.
 //   * The K order of every output element is fixed (tiles in order, two 32-wide
 //     substeps each, partials summed in split order), so a row's result depends on
-//     the split count but not on M or on the tile shape.
+//     the split count and the number of wave groups but not on M or the tile size.
 #include "qlin_dev.h"
 #include "qlin_internal.h"
 
@@ -477,21 +480,17 @@ static hipError_t launch_prefill_g(const TlArgs& a, int wk, bool hz, hipStream_t
 
 void prefill_geometry(int shape, int* bm, int* bn, int* waves) {
   using G0 = Geo<WK_W8, 1, 2, 1>;
-  using G1 = Geo<WK_W8, 2, 2, 1>;
-  using G2 = Geo<WK_W8, 2, 4, 1>;
-  using G3 = Geo<WK_W8, 1, 2, 2>;
+  using G1 = Geo<WK_W8, 2, 4, 1>;
+  using G2 = Geo<WK_W8, 1, 2, 2>;
   if (shape == PF_128x128) *bm = G0::BM, *bn = G0::BN, *waves = G0::WAVES;
-  else if (shape == PF_256x128) *bm = G1::BM, *bn = G1::BN, *waves = G1::WAVES;
-  else if (shape == PF_128x128_K2 || shape == PF_128x128_K2_DEEP) *bm = G3::BM, *bn = G3::BN, *waves = G3::WAVES;
-  else *bm = G2::BM, *bn = G2::BN, *waves = G2::WAVES;
+  else if (shape == PF_128x128_K2) *bm = G2::BM, *bn = G2::BN, *waves = G2::WAVES;
+  else *bm = G1::BM, *bn = G1::BN, *waves = G1::WAVES;
 }
 
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t st) {
   switch (shape) {
     case PF_128x128: return launch_prefill_g<1, 2, 1, 3>(a, wk, hz, st);
-    case PF_256x128: return launch_prefill_g<2, 2, 1, 3>(a, wk, hz, st);
     case PF_128x128_K2: return launch_prefill_g<1, 2, 2, 3>(a, wk, hz, st);
-    case PF_128x128_K2_DEEP: return launch_prefill_g<1, 2, 2, 6>(a, wk, hz, st);
     default: return launch_prefill_g<2, 4, 1, 3>(a, wk, hz, st);
   }
 }

@@ -50,7 +50,7 @@ struct SkLaunch {
 
 hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
 
-// Arguments of the tiled (M > 16) fp16-activation MFMA kernel.
+// Arguments of the LDS-tiled (prefill) fp16-activation MFMA kernel.
 struct TlArgs {
   const _Float16* x;  // fp16 [M][ldx]
   long long ldx;
@@ -70,12 +70,10 @@ struct TlArgs {
   unsigned* cnt;      // split-K arrival counters [tiles], zero between calls
 };
 
-hipError_t launch_tiled(const TlArgs& a, int wk, bool hz, int depth, hipStream_t stream);
-
-// LDS-DMA prefill kernel; `shape` picks the workgroup tile (rows x columns).
-// PF_128x128_K2: two wave groups split every K tile's two substeps (4 waves);
-// _DEEP: the same with a 6-tile LDS ring (one workgroup per CU, more copies in flight).
-enum PrefillShape { PF_128x128 = 0, PF_256x128 = 1, PF_256x256 = 2, PF_128x128_K2 = 3, PF_128x128_K2_DEEP = 4 };
+// LDS-DMA prefill kernel; `shape` picks the workgroup tile (rows x columns):
+// PF_128x128 (2 waves), PF_256x256 (8 waves, two per SIMD) and PF_128x128_K2 (two
+// wave groups split every K tile's substeps: 4 waves).
+enum PrefillShape { PF_128x128 = 0, PF_256x256 = 1, PF_128x128_K2 = 2 };
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t stream);
 // rows, columns and waves of a prefill workgroup tile
 void prefill_geometry(int shape, int* bm, int* bn, int* waves);
