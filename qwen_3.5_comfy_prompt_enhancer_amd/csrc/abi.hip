@@ -35,16 +35,18 @@ int hip_status(const char* fn, hipError_t e) {
 constexpr size_t kWorkspaceBytes = size_t(256) << 20;
 constexpr size_t kCounterBytes = size_t(1) << 20;
 constexpr int kWideTiles = 512;          // 256-column tiles at which no K split is needed
-// narrow launches: most waves to spread K over, and least K per wave (measured)
-constexpr long long kTargetWavesW8 = 256;
+// narrow launches: most waves to spread K over, and least K per wave (measured with
+// 8-wave workgroups: many short waves keep the most weight bytes in flight)
+constexpr long long kTargetWavesW8 = 2048;
 constexpr long long kTargetWavesW4 = 1024;
-constexpr int kMinWaveKW8 = 256;
+constexpr int kMinWaveKW8 = 64;
 constexpr int kMinWaveKW4 = 128;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 bool dtype_scale_ok(int dt) { return dt == QLIN_F16 || dt == QLIN_BF16 || dt == QLIN_F32; }
 bool dtype_out_ok(int dt) { return dt == QLIN_F16 || dt == QLIN_BF16; }
 bool group_ok(int g) { return g == 32 || (g > 0 && g % 64 == 0); }
+
 
 struct Problem {
   int act, wk, epi;
@@ -57,14 +59,14 @@ struct Problem {
 // Fills L (kernel variant, grid, LDS) and a.kchunk / a.splits / a.ntiles / seg tiles.
 // Launch-plan override for tuning sweeps: QLIN_SKINNY_PLAN="cols,waves,units" (0 keeps
 // the default for that field; units = K granules of one wave).  Unset in normal use.
-void plan_override(bool store_epi, int& cols, int& waves, int& upw) {
+void plan_override(const Problem& P, int& cols, int& waves, int& upw) {
   const char* e = getenv("QLIN_SKINNY_PLAN");
   if (!e || !*e) return;
   int c = 0, w = 0, u = 0;
   if (sscanf(e, "%d,%d,%d", &c, &w, &u) != 3) return;
   if (c == 8 || c == 16) cols = c;
-  if (!store_epi) cols = 8;  // gate/up kernels exist with 8-column tiles only
-  if (w >= 1 && w <= 4) waves = w;
+  if (P.epi != EPI_STORE) cols = 8;  // gate/up kernels exist with 8-column tiles only
+  if (w >= 1 && w <= 8) waves = w;  // clamped to the variant's maximum by the caller
   if (u >= 1) upw = u;
 }
 
@@ -97,11 +99,14 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   const bool wide = P.M > 16 || count_tiles(256) >= kWideTiles;
 
   // Measured on MI355X: wide W8 launches stream best as single-wave workgroups over
-  // 128-column tiles, wide W4 over 256-column tiles; narrow launches as 4-wave
-  // workgroups over 128-column tiles.
+  // 128-column tiles, wide W4 over 256-column tiles; narrow launches over 128-column
+  // tiles with K spread first over the waves of one workgroup (up to 8, reduced in
+  // LDS) and only then over workgroups.
   int cols = (wide && P.wk == WK_W4 && P.epi == EPI_STORE && P.M <= 16) ? 16 : 8;
-  int waves = (wide && P.M <= 16) ? 1 : 4, upw = 0;
-  plan_override(P.epi == EPI_STORE, cols, waves, upw);
+  int waves = (wide && P.M <= 16) ? 1 : (wide ? 4 : (skinny_big(P.act, P.wk, P.epi, cols) ? 8 : 4)), upw = 0;
+  plan_override(P, cols, waves, upw);
+  const int maxw = skinny_big(P.act, P.wk, P.epi, cols) ? 8 : 4;
+  if (waves > maxw) waves = maxw;
   const int TN = 16 * cols;
   const int ntiles = count_tiles(TN);
   int ntile_acc = 0;
@@ -158,7 +163,12 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   L.cols = cols;
   L.waves = waves;
   L.grid = dim3((unsigned)(ntiles * splits), (unsigned)rtiles, 1);
-  L.lds = (waves > 1 || splits > 1) ? (size_t)P.nsets * cols * 1024 : 0;
+  // LDS: the per-wave slots of the workgroup reduction (row groups holding real rows
+  // of the first row tile) and the tile buffer of the split-K reduction
+  const int rg0 = (((P.M < 16) ? P.M : 16) + 3) / 4;
+  const size_t lds_waves = (waves > 1) ? (size_t)waves * P.nsets * rg0 * cols * 64 * sizeof(float) : 0;
+  const size_t lds_split = (splits > 1) ? (size_t)P.nsets * cols * 1024 : 0;
+  L.lds = lds_waves > lds_split ? lds_waves : lds_split;
   if ((long long)ntiles * splits > 0x7FFFFFFFLL || rtiles > 65535)
     return fail(QLIN_ERR_UNSUPPORTED, "%s: grid too large (M=%d, N=%d)", fn, P.M, P.ncols);
   return hip_status(fn, launch_skinny(L, a, stream));

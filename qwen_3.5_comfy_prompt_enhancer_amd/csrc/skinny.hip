@@ -143,9 +143,11 @@ __device__ __forceinline__ void st_i8(int8_t* p, const int q[COLS]) {
 }
 
 // SPLIT: whether workgroups split K (partials + arrival counters).  Wide launches
-// (enough column or row tiles to fill the chip) use SPLIT = false.
-template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT>
-__global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
+// (enough column or row tiles to fill the chip) use SPLIT = false.  MAXW: most waves
+// per workgroup (4, or 8 for the decode variants that spread K over one workgroup's
+// waves instead of over workgroups).
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void skinny_kernel(const SkArgs a) {
   constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;  // weight sets feeding one output tile
   constexpr int TN = 16 * COLS;
   constexpr int NQ = COLS / 4;
@@ -414,23 +416,28 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
   }
 
   // ---------------- reduction over the waves of the workgroup (fixed order) ----------------
-  // `red` holds NS*COLS*256 floats: the per-wave partials here, the summed tile below.
+  // Every wave writes the row groups that hold real rows to its own LDS slot; all
+  // threads then sum the slots in wave order (0, 1, ..., nw-1) and wave 0 takes the
+  // totals.  `red` holds nw slots of NS*RG*COLS*64 floats here and NS*COLS*256 floats
+  // in the split-K reduction below.
   const int Mt = min(16, M - rt * 16);
   const int RG = (Mt + 3) >> 2;  // row groups (of 4 MFMA rows) that hold real rows
   if (nw > 1) {
-    for (int w = 1; w < nw; ++w) {
-      __syncthreads();
-      if (wave == w && g < RG) {
+    const int per = NS * RG * COLS * 64;
+    if (g < RG) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
+      for (int s = 0; s < NS; ++s)
 #pragma unroll
-          for (int t = 0; t < COLS; ++t)
+        for (int t = 0; t < COLS; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int idx = (((s * 4 + g) * COLS + t) * 4 + r) * 16 + j;
-              red[idx] = (w == 1) ? acc[s][t][r] : red[idx] + acc[s][t][r];
-            }
-      }
+          for (int r = 0; r < 4; ++r)
+            red[wave * per + (((s * RG + g) * COLS + t) * 4 + r) * 16 + j] = acc[s][t][r];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < per; e += blockDim.x) {
+      float v = red[e];
+      for (int w = 1; w < nw; ++w) v += red[w * per + e];
+      red[e] = v;
     }
     __syncthreads();
     if (wave == 0 && g < RG) {
@@ -439,8 +446,9 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
 #pragma unroll
         for (int t = 0; t < COLS; ++t)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[s][t][r] += red[(((s * 4 + g) * COLS + t) * 4 + r) * 16 + j];
+          for (int r = 0; r < 4; ++r) acc[s][t][r] = red[(((s * RG + g) * COLS + t) * 4 + r) * 16 + j];
     }
+    if (SPLIT) __syncthreads();  // the split-K reduction below reuses `red`
   }
 
   // ---------------- reduction over workgroups (split-K) ----------------
@@ -577,21 +585,49 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkArgs a) {
   }
 }
 
-template <int ACT, int WK, bool HZ, int EPI, int COLS>
-static hipError_t launch_t(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
-  if (a.splits > 1)
-    hipLaunchKernelGGL((skinny_kernel<ACT, WK, HZ, EPI, COLS, true>), L.grid, dim3(64 * L.waves), L.lds, st, a);
-  else
-    hipLaunchKernelGGL((skinny_kernel<ACT, WK, HZ, EPI, COLS, false>), L.grid, dim3(64 * L.waves), L.lds, st, a);
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW>
+static hipError_t launch_v(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
+  auto* k = skinny_kernel<ACT, WK, HZ, EPI, COLS, SPLIT, MAXW>;
+  if (L.lds > 65536) {
+    static bool attr_set = false;  // benign race: every caller sets the same value
+    if (!attr_set) {
+      const hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               160 * 1024);
+      if (e != hipSuccess) return e;
+      attr_set = true;
+    }
+  }
+  hipLaunchKernelGGL(k, L.grid, dim3(64 * L.waves), L.lds, st, a);
   return hipGetLastError();
 }
 
-#define QL_CASE(A, W, Z, E, C)                                                   \
-  if (L.act == A && L.wk == W && (L.hz != 0) == Z && L.epi == E && L.cols == C) \
-    return launch_t<A, W, Z, E, C>(L, a, st);
+// BIG: the variant also exists with up to 8 waves per workgroup.
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool BIG>
+static hipError_t launch_t(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
+  if (L.waves > 4) {
+    if constexpr (BIG) {
+      if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 8>(L, a, st);
+      return launch_v<ACT, WK, HZ, EPI, COLS, false, 8>(L, a, st);
+    }
+    return hipErrorInvalidValue;
+  }
+  if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 4>(L, a, st);
+  return launch_v<ACT, WK, HZ, EPI, COLS, false, 4>(L, a, st);
+}
 
-#define QL_COLS(A, W, Z, E) QL_CASE(A, W, Z, E, 8) QL_CASE(A, W, Z, E, 16)
-#define QL_C8(A, W, Z, E) QL_CASE(A, W, Z, E, 8)
+#define QL_CASE(A, W, Z, E, C, B)                                                \
+  if (L.act == A && L.wk == W && (L.hz != 0) == Z && L.epi == E && L.cols == C) \
+    return launch_t<A, W, Z, E, C, B>(L, a, st);
+
+#define QL_COLS(A, W, Z, E) QL_CASE(A, W, Z, E, 8, W == WK_W8) QL_CASE(A, W, Z, E, 16, false)
+#define QL_C8(A, W, Z, E) QL_CASE(A, W, Z, E, 8, false)
+
+// Measured: W8 decode streams best with 8-wave workgroups of short K ranges; W4
+// (twice the dequantization work per byte) with 4-wave ones.
+bool skinny_big(int act, int wk, int epi, int cols) {
+  (void)act;
+  return wk == WK_W8 && epi == EPI_STORE && cols == 8;
+}
 
 hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
   QL_COLS(ACT_F16, WK_W8, false, EPI_STORE)
