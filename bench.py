@@ -114,7 +114,7 @@ def decode_sweep(args, kind, shapes, head, ms, layers):
     gen = torch.Generator().manual_seed(1234)
     lw = [[Weights(kind, K, N, dev, gen) for (_, K, N) in shapes] for _ in range(layers)]
     hw = Weights(kind, head[1], head[2], dev, gen)
-    kmax = max(max(K for _, K, _ in shapes), head[1])
+    kmax = max([K for _, K, _ in shapes] + [head[1]])
     xs = {M: torch.randn((M, kmax), generator=gen).to(torch.float16).to(dev) for M in ms}
     outs = {M: [torch.empty((M, N), dtype=torch.float16, device=dev) for (_, _, N) in shapes] for M in ms}
     hout = {M: torch.empty((M, head[2]), dtype=torch.float16, device=dev) for M in ms}
@@ -160,7 +160,7 @@ def decode_sweep(args, kind, shapes, head, ms, layers):
             else:
                 hw.run(lin, xin(M, head[1]), hout[M])
 
-    total = sum(layers * sum(w.nbytes(M) for w in lw[0]) + hw.nbytes(M) for M in ms)
+    total = sum((layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0) + hw.nbytes(M) for M in ms)
     head_bytes = {M: hw.nbytes(M) for M in ms}
     return total, step, head_ev, head_bytes, record, (lw, hw, xs, outs, hout, lin)
 

@@ -49,7 +49,7 @@ struct SkLaunch {
 };
 
 hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
-// whether a skinny variant runs with up to 16 waves per workgroup (else 4)
+// whether a skinny variant runs with up to 8 waves per workgroup (else 4)
 bool skinny_big(int act, int wk, int epi, int cols);
 
 // Arguments of the LDS-tiled (prefill) fp16-activation MFMA kernel.
