@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -39,6 +41,15 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 template <typename T, typename F>
 __device__ __forceinline__ T bitcast(F f) {
   return __builtin_bit_cast(T, f);
+}
+
+// f(std::integral_constant<int, I>{}) for I = B .. E-1, unrolled at compile time.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -73,6 +84,17 @@ __device__ __forceinline__ uint32_t w4_pair_f16(uint32_t d, int b, f16x2 bias) {
 
 __device__ __forceinline__ f16x2 w4_bias(uint32_t z) {
   return f16x2{(_Float16)(-1024.0f - (float)z), (_Float16)(-64.0f - (float)z)};
+}
+
+// The two nibbles of one packed byte -> exact f16x2 (1024 + lo, 64 + hi) in two
+// instructions: perm puts the byte under the exponent byte 0x64 in half 0 and 0x54
+// in half 1; the mask keeps the low nibble in the unit bits of 0x6400 = 1024 and the
+// high nibble in bits 4-7 of 0x5400 = 64, where bit 4 has weight 1.  The caller
+// removes the offsets after the MFMA: sum_k x_k * offset_k is one more MFMA of the
+// activations against a constant operand, shared by every column.
+__device__ __forceinline__ uint32_t w4_pair_offset(uint32_t d, int b) {
+  const uint32_t sel = (uint32_t)b | (4u << 8) | ((uint32_t)b << 16) | (5u << 24);
+  return perm(0x00005464u, d, sel) & 0x54F0640Fu;
 }
 
 // ---------------------------------------------------------------------------

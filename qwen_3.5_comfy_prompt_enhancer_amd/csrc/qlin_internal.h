@@ -43,12 +43,18 @@ struct SkArgs {
 
 struct SkLaunch {
   int act, wk, hz, epi, cols;
+  int ks;          // K-loop fold structure (KStruct in skinny_kernel.h), set by launch_skinny
   int waves;       // waves per workgroup
   dim3 grid;
   size_t lds;      // dynamic LDS bytes
 };
 
 hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
+// the instantiations of each activation / weight family (skinny_f16.hip, skinny_i8w8.hip,
+// skinny_i8w4.hip)
+hipError_t launch_skinny_f16(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
+hipError_t launch_skinny_i8w8(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
+hipError_t launch_skinny_i8w4(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
 // whether a skinny variant runs with up to 8 waves per workgroup (else 4)
 bool skinny_big(int act, int wk, int epi, int cols);
 

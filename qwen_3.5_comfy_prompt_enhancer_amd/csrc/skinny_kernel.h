@@ -1,0 +1,674 @@
+// Skinny quantized GEMM for up to 16 activation rows per row tile (decode, best-of-N
+// rows), gfx950: the kernel template and its launchers.  The instantiations are
+// spread over skinny_f16.hip, skinny_i8w8.hip and skinny_i8w4.hip, which compile in
+// parallel; skinny.hip routes a launch to them.
+//
+// Replaces the decode-shaped launches of gemm_i8 / gemm_w4 / proj3(_w4) /
+// mlp_gate_up(_quant)(_w4) (kernels/gemm.py:20-312, kernels/w4.py:107-323).
+//
+// Work decomposition
+//   * A wave owns a column tile of TN = 16*COLS output columns and a K range.  Lane
+//     l = (g = l/16, j = l%16) loads, per 32-wide K step, COLS adjacent columns
+//     (one 8- or 16-byte load per weight row) of the 8 K rows 8g..8g+7 (W8), or of
+//     the 4 packed byte rows 4g..4g+3 (W4).  16 lanes x COLS bytes is a coalesced
+//     run along N, the engine layout's contiguous axis.
+//   * In registers the lane turns those rows into COLS MFMA B operands -- column
+//     t of its COLS columns for instruction t -- by byte permutes (qlin_dev.h), and
+//     issues COLS 16x16x32 MFMAs against the same A operand (activation rows
+//     0..15 of the row tile, the lane's 8 K values).  MFMA row i = activation row;
+//     MFMA column j = column j*COLS + t of the tile.  Rows >= M are zero.
+//   * fp16 activations: v_mfma_f32_16x16x32_f16 on exactly converted weights, fp32
+//     accumulation; W4 nibbles enter the MFMA with a constant offset that is
+//     removed per group, where the group scales are applied in fp32.
+//     int8 activations (engine signature): v_mfma_i32_16x16x32_i8, exact int32 per
+//     64-wide activation group (W4 per weight sub-block), then the reference's fp32
+//     epilogue `acc += float(i32) * a_s (* w_s)` (kernels/gemm.py:43-45,
+//     kernels/w4.py:103-104).
+//   * The K dimension is split over the `waves` of a workgroup (reduced in LDS in a
+//     fixed order) and over `splits` workgroups (fp32 partials in the caller's
+//     workspace, written and read as agent-scope atomics; the last workgroup to
+//     arrive at a per-tile counter sums them in split order and resets the counter).
+//     Split choices depend on K and N only, so each output row is computed
+//     identically for every M <= 16.
+//   * Every load of a 32-wide K step is issued D steps ahead from a register ring.
+#pragma once
+
+#include <type_traits>
+
+#include "qlin_dev.h"
+#include "qlin_internal.h"
+
+namespace qlin {
+
+template <int COLS>
+struct Row {
+  uint32_t d[COLS / 4];
+};
+
+template <int COLS>
+__device__ __forceinline__ Row<COLS> ld_row(const uint8_t* p, bool valid) {
+  Row<COLS> r;
+  if constexpr (COLS == 16) {
+    const u32x4 v = *(const u32x4*)p;
+    r.d[0] = valid ? v.x : 0u;
+    r.d[1] = valid ? v.y : 0u;
+    r.d[2] = valid ? v.z : 0u;
+    r.d[3] = valid ? v.w : 0u;
+  } else {
+    const u32x2 v = *(const u32x2*)p;
+    r.d[0] = valid ? v.x : 0u;
+    r.d[1] = valid ? v.y : 0u;
+  }
+  return r;
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t d, int b) { return (d >> (8 * b)) & 0xFFu; }
+
+// Raw dwords of COLS consecutive scale values (COLS/4 vectors for fp32, COLS/8 for
+// 16-bit types); the conversion is deferred to cvt_scales so the load latency is not
+// waited on where it is issued.
+template <int COLS>
+__device__ __forceinline__ void ld_scales_raw(const void* p, int dt, long long idx, u32x4 raw[COLS / 4]) {
+  if (dt == DT_F32) {
+    const u32x4* q = (const u32x4*)((const float*)p + idx);
+#pragma unroll
+    for (int c = 0; c < COLS / 4; ++c) raw[c] = q[c];
+  } else {
+    const u32x4* q = (const u32x4*)((const uint16_t*)p + idx);
+#pragma unroll
+    for (int c = 0; c < COLS / 8; ++c) raw[c] = q[c];
+  }
+}
+
+template <int COLS>
+__device__ __forceinline__ void cvt_scales(const u32x4 raw[COLS / 4], int dt, float out[COLS]) {
+  if (dt == DT_F32) {
+#pragma unroll
+    for (int c = 0; c < COLS / 4; ++c) {
+      out[4 * c] = bitcast<float>(raw[c].x);
+      out[4 * c + 1] = bitcast<float>(raw[c].y);
+      out[4 * c + 2] = bitcast<float>(raw[c].z);
+      out[4 * c + 3] = bitcast<float>(raw[c].w);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < COLS / 8; ++c) {
+      const uint32_t w[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        out[8 * c + e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+      }
+    }
+  }
+}
+
+// COLS consecutive 16-bit (fp16 / bf16) values -> fp32.
+template <int COLS>
+__device__ __forceinline__ void ld_act16(const void* p, int dt, long long idx, float out[COLS]) {
+  const uint16_t* q = (const uint16_t*)p + idx;
+#pragma unroll
+  for (int c = 0; c < COLS; c += 8) {
+    const u32x4 v = *(const u32x4*)(q + c);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      out[c + e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+    }
+  }
+}
+
+template <int COLS>
+__device__ __forceinline__ void st_out16(void* p, int dt, long long idx, const float v[COLS]) {
+  uint16_t* q = (uint16_t*)p + idx;
+#pragma unroll
+  for (int c = 0; c < COLS; c += 8) {
+    u32x4 w;
+    w.x = (uint32_t)to_out16(v[c + 0], dt) | ((uint32_t)to_out16(v[c + 1], dt) << 16);
+    w.y = (uint32_t)to_out16(v[c + 2], dt) | ((uint32_t)to_out16(v[c + 3], dt) << 16);
+    w.z = (uint32_t)to_out16(v[c + 4], dt) | ((uint32_t)to_out16(v[c + 5], dt) << 16);
+    w.w = (uint32_t)to_out16(v[c + 6], dt) | ((uint32_t)to_out16(v[c + 7], dt) << 16);
+    *(u32x4*)(q + c) = w;
+  }
+}
+
+template <int COLS>
+__device__ __forceinline__ void st_i8(int8_t* p, const int q[COLS]) {
+  uint32_t w[COLS / 4];
+#pragma unroll
+  for (int c = 0; c < COLS / 4; ++c)
+    w[c] = ((uint32_t)(q[4 * c] & 0xFF)) | ((uint32_t)(q[4 * c + 1] & 0xFF) << 8) |
+           ((uint32_t)(q[4 * c + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * c + 3] & 0xFF) << 24);
+  if constexpr (COLS == 16) {
+    *(u32x4*)p = u32x4{w[0], w[1], w[2], w[3]};
+  } else {
+    *(u32x2*)p = u32x2{w[0], w[1]};
+  }
+}
+
+// SPLIT: whether workgroups split K (partials + arrival counters).  Wide launches
+// (enough column or row tiles to fill the chip) use SPLIT = false.  MAXW: most waves
+// per workgroup (4, or 8 for the decode variants that spread K over one workgroup's
+// waves instead of over workgroups).
+// Two waves per SIMD (at most 256 registers) except for the fp16-activation W4
+// 16-column variant, which holds a deeper register ring and streams at one.
+// KS: where the scale folds of the K loop fall.  KS_STEP4: every 4th 32-wide step
+// (W4 group 128 with fp16 activations); KS_STEP2: every 2nd step (64-wide activation
+// blocks / W4 sub-blocks with int8 activations); KS_ANY: tested per step at run
+// time (other groups).  Static positions keep the accumulators in place across steps.
+enum KStruct { KS_ANY = 0, KS_STEP2 = 2, KS_STEP4 = 4 };
+
+// Waves per SIMD the register allocation must allow: 2 (at most 256 registers) for the
+// 8-column int8-activation variants whose natural allocation lands just above 256,
+// except the W4 gate/up ones, which need far more; 1 otherwise (no constraint).
+template <int ACT, int WK, int EPI, int COLS>
+struct SkOcc {
+  static constexpr int value = (ACT == ACT_I8 && COLS == 8 && !(WK == WK_W4 && EPI != EPI_STORE)) ? 2 : 1;
+};
+
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW, int KS>
+__global__ __launch_bounds__(64 * MAXW)
+__attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skinny_kernel(const SkArgs a) {
+  constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;  // weight sets feeding one output tile
+  constexpr int TN = 16 * COLS;
+  constexpr int NQ = COLS / 4;
+  constexpr int NR = (WK == WK_W8) ? 8 : 4;  // weight rows per lane per 32-wide K step
+  extern __shared__ float red[];
+
+  const int nw = blockDim.x >> 6;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15;
+  const int g = lane >> 4;
+  const int tile = SPLIT ? blockIdx.x / a.splits : blockIdx.x;
+  const int split = SPLIT ? blockIdx.x - tile * a.splits : 0;
+  const int rt = blockIdx.y;
+  const int M = a.M;
+  const int K = a.K;
+  const int G = a.group;
+
+  int si = 0;
+  if constexpr (EPI == EPI_STORE) {
+    if (a.nseg > 1 && tile >= a.seg[1].tile0) si = 1;
+    if (a.nseg > 2 && tile >= a.seg[2].tile0) si = 2;
+  }
+  const Seg sg0 = a.seg[si];
+  const uint8_t* wp[NS];
+  const void* sp[NS];
+  const uint8_t* zp[NS];
+  wp[0] = sg0.w;
+  sp[0] = sg0.s;
+  zp[0] = sg0.z;
+  if constexpr (NS == 2) {
+    wp[1] = a.seg[1].w;
+    sp[1] = a.seg[1].s;
+    zp[1] = a.seg[1].z;
+  }
+  const int n = sg0.n;
+  const int cseg = (tile - sg0.tile0) * TN + j * COLS;  // first column (within the matrix)
+  const bool cvalid = cseg < n;
+  const int ccl = cvalid ? cseg : 0;                     // in-bounds column for addressing
+  const int ocol = sg0.col0 + cseg;                      // first output column
+
+  const int arow = rt * 16 + j;  // activation row this lane feeds into the A operand
+  const bool avalid = arow < M;
+  const int kb = (split * nw + wave) * a.kchunk;
+  const int ke = min(K, kb + a.kchunk);
+
+  f32x4 acc[NS][COLS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int t = 0; t < COLS; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // ---------------- software-pipelined K loop ----------------
+  // Every load of one 32-wide K step (weights, activations, the step's group scales,
+  // zeros and activation scales) goes into slot d of a D-deep register ring and is
+  // issued D steps ahead, unconditionally (the step index is clamped to the wave's
+  // last step), so the loop body is straight-line and D steps of HBM latency overlap.
+  // Lanes past N or M read clamped in-bounds addresses; their MFMA columns / rows
+  // are never stored.
+  constexpr int D = (NS == 2) ? 2 : 4;
+  constexpr bool F16 = ACT == ACT_F16;
+  constexpr bool W4 = WK == WK_W4;
+  using XV = typename std::conditional<F16, u32x4, u32x2>::type;
+  struct Step {
+    Row<COLS> w[NS][NR];
+    XV xv;                            // fp16: 8 halves; int8: 8 bytes
+    u32x4 sraw[W4 ? NS : 1][COLS / 4];  // W4: raw scales of the step's group
+    Row<COLS> z[(W4 && HZ) ? NS : 1];   // W4: zeros of the step's group
+    float as_[F16 ? 1 : 4];           // int8: activation scales, rows 4g..4g+3
+  };
+  const long long xrow = (long long)(avalid ? arow : 0);
+  const _Float16* xpf = (const _Float16*)a.x + xrow * a.ldx + 8 * g;
+  const int8_t* xpi = (const int8_t*)a.x + xrow * K + 8 * g;
+  const int NG = K / 64;
+  long long asrow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int orow = rt * 16 + 4 * g + r;
+    asrow[r] = (long long)(orow < M ? orow : 0) * NG;
+  }
+  auto load_step = [&](Step& st, int k) {
+    if constexpr (F16) {
+      st.xv = *(const u32x4*)(xpf + k);
+    } else {
+      st.xv = *(const u32x2*)(xpi + k);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.as_[r] = a.xs[asrow[r] + k / 64];
+    }
+    const long long r0 = W4 ? (long long)(k / 2 + 4 * g) : (long long)(k + 8 * g);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint8_t* base = wp[s] + r0 * n + ccl;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) st.w[s][r] = ld_row<COLS>(base + (long long)r * n, true);
+      if constexpr (W4) {
+        const long long gi = (long long)(k / G) * n + ccl;
+        ld_scales_raw<COLS>(sp[s], a.sdt, gi, st.sraw[s]);
+        if constexpr (HZ) st.z[s] = ld_row<COLS>(zp[s] + gi, true);
+      }
+    }
+  };
+  const int nsteps = ke > kb ? (ke - kb) >> 5 : 0;
+  Step buf[D];
+  // The loop is unrolled by U = 4 steps, and compute() receives the step's position
+  // u = i % 4 as a compile-time constant.  Every wave's K range starts at a multiple
+  // of its K granule (64 for int8 activations, whole W4 groups), so the group and
+  // activation-block ends that are multiples of 4 steps apart are known statically
+  // and the accumulators stay in place across steps.
+  constexpr int U = 4;
+  auto run_pipeline = [&](auto&& compute) {
+    if (nsteps <= 0) return;
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_step(buf[d], kb + 32 * (d < nsteps ? d : nsteps - 1));
+    const int nfull = nsteps - nsteps % U;
+    for (int base = 0; base < nfull; base += U) {
+      static_for<0, U>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        const int i = base + u;
+        compute(buf[u % D], kb + 32 * i, uc);
+        const int nx = i + D < nsteps ? i + D : nsteps - 1;
+        load_step(buf[u % D], kb + 32 * nx);
+      });
+    }
+    static_for<0, U - 1>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      const int i = nfull + u;
+      if (i < nsteps) {
+        compute(buf[u % D], kb + 32 * i, uc);
+        if constexpr (U > D) {
+          const int nx = i + D < nsteps ? i + D : nsteps - 1;
+          load_step(buf[u % D], kb + 32 * nx);
+        }
+      }
+    });
+  };
+
+  if constexpr (F16) {
+    // ---------------- fp16 activations, fp16 MFMA ----------------
+    // W4: the B operand holds each packed byte as (1024 + lo, 64 + hi) (two
+    // instructions, w4_pair_offset).  Per group, two extra MFMAs of the activations
+    // against constant operands give c1 = sum(1024 x_even + 64 x_odd) and
+    // c2 = sum(x_even + x_odd) for every row; at the group end each column folds in
+    // scale * (acc - (c1 + z c2)), with z = 8 when the layout has no zeros, so an
+    // explicit all-8 zero tensor gives bit-identical results.
+    f32x4 tot[NS][COLS];
+    f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f}, c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int t = 0; t < COLS; ++t) tot[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f16x2 o12 = f16x2{(_Float16)1024.0f, (_Float16)64.0f};
+    const f16x2 one2 = f16x2{(_Float16)1.0f, (_Float16)1.0f};
+    const f16x8 boff = f16x8{o12[0], o12[1], o12[0], o12[1], o12[0], o12[1], o12[0], o12[1]};
+    const f16x8 bone = f16x8{one2[0], one2[1], one2[0], one2[1], one2[0], one2[1], one2[0], one2[1]};
+    run_pipeline([&](const Step& st, int k, auto uc) {
+      constexpr int u = decltype(uc)::value;
+      const f16x8 av = bitcast<f16x8>(st.xv);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+#pragma unroll
+        for (int t = 0; t < COLS; ++t) {
+          const int q = t >> 2, b = t & 3;
+          u32x4 bw;
+          if constexpr (W4) {
+            bw.x = w4_pair_offset(st.w[s][0].d[q], b);
+            bw.y = w4_pair_offset(st.w[s][1].d[q], b);
+            bw.z = w4_pair_offset(st.w[s][2].d[q], b);
+            bw.w = w4_pair_offset(st.w[s][3].d[q], b);
+          } else {
+            bw.x = w8_pair_f16(st.w[s][0].d[q], st.w[s][1].d[q], b);
+            bw.y = w8_pair_f16(st.w[s][2].d[q], st.w[s][3].d[q], b);
+            bw.z = w8_pair_f16(st.w[s][4].d[q], st.w[s][5].d[q], b);
+            bw.w = w8_pair_f16(st.w[s][6].d[q], st.w[s][7].d[q], b);
+          }
+          acc[s][t] = mfma_f16(av, bitcast<f16x8>(bw), acc[s][t]);
+        }
+      }
+      if constexpr (W4) {
+        c1 = mfma_f16(av, boff, c1);
+        c2 = mfma_f16(av, bone, c2);
+        // group end
+        if (KS == KS_STEP4 ? (u == 3) : ((k + 32) % G == 0)) {
+          f32x4 corr8;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) corr8[r] = fmaf(8.0f, c2[r], c1[r]);
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            float sc[COLS];
+            cvt_scales<COLS>(st.sraw[s], a.sdt, sc);
+#pragma unroll
+            for (int t = 0; t < COLS; ++t) {
+              f32x4 corr = corr8;
+              if constexpr (HZ) {
+                const float z = (float)byte_of(st.z[s].d[t >> 2], t & 3);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) corr[r] = fmaf(z, c2[r], c1[r]);
+              }
+#pragma unroll
+              for (int r = 0; r < 4; ++r) tot[s][t][r] = fmaf(sc[t], acc[s][t][r] - corr[r], tot[s][t][r]);
+              acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+          }
+          c1 = f32x4{0.f, 0.f, 0.f, 0.f};
+          c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    });
+    if constexpr (W4) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int t = 0; t < COLS; ++t) acc[s][t] = tot[s][t];
+    }
+  } else {
+    // ---------------- int8 activations (engine signature), int8 MFMA ----------------
+    const int SUB = W4 ? (G < 64 ? G : 64) : 64;
+    i32x4 iacc[NS][COLS];
+    i32x4 sx = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int t = 0; t < COLS; ++t) iacc[s][t] = i32x4{0, 0, 0, 0};
+    run_pipeline([&](const Step& st, int k, auto uc) {
+      constexpr int u = decltype(uc)::value;
+      uint64_t ap = (uint64_t)st.xv.x | ((uint64_t)st.xv.y << 32);
+      if constexpr (W4) {
+        // k slots: even K values first, then odd (the nibble split order below)
+        ap = (uint64_t)perm(st.xv.y, st.xv.x, 0x06040200u) |
+             ((uint64_t)perm(st.xv.y, st.xv.x, 0x07050301u) << 32);
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          uint32_t lo4[4], hi4[4];
+          if constexpr (W4) {
+            uint32_t L[4], H[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w4_split_i8x16(st.w[s][r].d[q], L[r], H[r]);
+            tr4(L[0], L[1], L[2], L[3], lo4);
+            tr4(H[0], H[1], H[2], H[3], hi4);
+          } else {
+            tr4(st.w[s][0].d[q], st.w[s][1].d[q], st.w[s][2].d[q], st.w[s][3].d[q], lo4);
+            tr4(st.w[s][4].d[q], st.w[s][5].d[q], st.w[s][6].d[q], st.w[s][7].d[q], hi4);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const uint64_t bv = (uint64_t)lo4[u] | ((uint64_t)hi4[u] << 32);
+            iacc[s][4 * q + u] = mfma_i8(ap, bv, iacc[s][4 * q + u]);
+          }
+        }
+      }
+      if constexpr (W4 && HZ) sx = mfma_i8(ap, 0x0101010101010101ull, sx);
+      // end of an activation block / weight sub-block
+      if (KS == KS_STEP2 ? (u & 1) == 1 : ((k + 32) % SUB == 0)) {
+        if constexpr (!W4) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int t = 0; t < COLS; ++t) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc[s][t][r] = fmaf((float)iacc[s][t][r], st.as_[r], acc[s][t][r]);
+              iacc[s][t] = i32x4{0, 0, 0, 0};
+            }
+        } else {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            float ws[COLS];
+            cvt_scales<COLS>(st.sraw[s], a.sdt, ws);
+#pragma unroll
+            for (int t = 0; t < COLS; ++t) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                int v = iacc[s][t][r] >> 4;  // exact: the MFMA summed 16 * (nibble - 8)
+                if constexpr (HZ) v += (8 - (int)byte_of(st.z[s].d[t >> 2], t & 3)) * sx[r];
+                acc[s][t][r] = fmaf((float)v, st.as_[r] * ws[t], acc[s][t][r]);
+              }
+              iacc[s][t] = i32x4{0, 0, 0, 0};
+            }
+          }
+          if constexpr (HZ) sx = i32x4{0, 0, 0, 0};
+        }
+      }
+    });
+  }
+
+  // Per-column scales of the W8 epilogue, issued now so their latency overlaps the
+  // reductions below.
+  u32x4 csraw[NS][COLS / 4];
+  if constexpr (WK == WK_W8) {
+    if (wave == 0) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) ld_scales_raw<COLS>(sp[s], a.sdt, ccl, csraw[s]);
+    }
+  }
+
+  // ---------------- reduction over the waves of the workgroup (fixed order) ----------------
+  // Every wave writes the row groups that hold real rows to its own LDS slot; all
+  // threads then sum the slots in wave order (0, 1, ..., nw-1) and wave 0 takes the
+  // totals.  `red` holds nw slots of NS*RG*COLS*64 floats here and NS*COLS*256 floats
+  // in the split-K reduction below.
+  const int Mt = min(16, M - rt * 16);
+  const int RG = (Mt + 3) >> 2;  // row groups (of 4 MFMA rows) that hold real rows
+  if (nw > 1) {
+    const int per = NS * RG * COLS * 64;
+    if (g < RG) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int t = 0; t < COLS; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            red[wave * per + (((s * RG + g) * COLS + t) * 4 + r) * 16 + j] = acc[s][t][r];
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < per; e += blockDim.x) {
+      float v = red[e];
+      for (int w = 1; w < nw; ++w) v += red[w * per + e];
+      red[e] = v;
+    }
+    __syncthreads();
+    if (wave == 0 && g < RG) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int t = 0; t < COLS; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[s][t][r] = red[(((s * RG + g) * COLS + t) * 4 + r) * 16 + j];
+    }
+    if (SPLIT) __syncthreads();  // the split-K reduction below reuses `red`
+  }
+
+  // ---------------- reduction over workgroups (split-K) ----------------
+  // Partials travel as agent-scope atomic stores / loads (coherent across XCDs by
+  // themselves, so no whole-L2 writeback or invalidate is needed).  Each workgroup
+  // waits until its partial stores have completed before it increments the tile's
+  // arrival counter; the workgroup that sees the final count reads every partial.
+  if constexpr (SPLIT) {
+    __shared__ int s_last;
+    const long long MN = (long long)M * a.ncols;
+    if (wave == 0) {
+      if (g < RG && cvalid) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int orow = rt * 16 + 4 * g + r;
+            if (orow < M) {
+              float* pp = a.part + ((long long)split * NS + s) * MN + (long long)orow * a.ncols + ocol;
+#pragma unroll
+              for (int t = 0; t < COLS; ++t)
+                __hip_atomic_store(pp + t, acc[s][t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      unsigned* cp = a.cnt + (long long)rt * a.ntiles + tile;
+      if (lane == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (unsigned)(a.splits - 1);
+        if (last) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+    }
+    __syncthreads();
+    if (!s_last) return;  // uniform over the workgroup
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // The last workgroup sums the tile's partials in split order, every thread on
+    // its own (set, row, column) elements, into red[s][row][col].
+    const int tcol0 = (tile - sg0.tile0) * TN;  // tile's first column within the matrix
+    const int nel = NS * Mt * TN;
+    for (int e = threadIdx.x; e < nel; e += blockDim.x) {
+      const int s = e / (Mt * TN);
+      const int rem = e - s * (Mt * TN);
+      const int row = rem / TN;
+      const int col = rem - row * TN;
+      float v = 0.0f;
+      if (tcol0 + col < n) {
+        const float* pp = a.part + (long long)s * MN + (long long)(rt * 16 + row) * a.ncols + sg0.col0 + tcol0 + col;
+        const long long stride = (long long)NS * MN;
+        v = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll 8
+        for (int p = 1; p < a.splits; ++p)
+          v += __hip_atomic_load(pp + p * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      red[(s * 16 + row) * TN + col] = v;
+    }
+    __syncthreads();
+    if (wave == 0 && g < RG) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int t = 0; t < COLS; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r;
+            acc[s][t][r] = row < Mt ? red[(s * 16 + row) * TN + j * COLS + t] : 0.0f;
+          }
+    }
+  }
+  if (wave != 0) return;
+
+  // ---------------- epilogue ----------------
+  if (g >= RG) return;
+  if constexpr (EPI == EPI_STORE) {
+    if (!cvalid) return;
+    float cs[COLS];
+    if constexpr (WK == WK_W8) cvt_scales<COLS>(csraw[0], a.sdt, cs);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int orow = rt * 16 + 4 * g + r;
+      if (orow >= M) break;
+      float y[COLS];
+#pragma unroll
+      for (int t = 0; t < COLS; ++t) y[t] = (WK == WK_W8) ? acc[0][t][r] * cs[t] : acc[0][t][r];
+      if (a.res != nullptr) {
+        float rv[COLS];
+        ld_act16<COLS>(a.res, a.odt, (long long)orow * a.ldr + ocol, rv);
+#pragma unroll
+        for (int t = 0; t < COLS; ++t) y[t] += rv[t];
+      }
+      st_out16<COLS>(a.out, a.odt, (long long)orow * a.ldo + ocol, y);
+    }
+  } else {
+    float cg[COLS], cu[COLS];
+    if constexpr (WK == WK_W8) {
+      cvt_scales<COLS>(csraw[0], a.sdt, cg);
+      cvt_scales<COLS>(csraw[1], a.sdt, cu);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int orow = rt * 16 + 4 * g + r;
+      if (orow >= M) break;  // uniform over the 16 lanes of a row group
+      float h[COLS];
+#pragma unroll
+      for (int t = 0; t < COLS; ++t) {
+        const float gv = (WK == WK_W8) ? acc[0][t][r] * cg[t] : acc[0][t][r];
+        const float uv = (WK == WK_W8) ? acc[1][t][r] * cu[t] : acc[1][t][r];
+        h[t] = silu(gv) * uv;
+      }
+      if constexpr (EPI == EPI_GATEUP) {
+        if (cvalid) st_out16<COLS>(a.out, DT_BF16, (long long)orow * a.ncols + ocol, h);
+      } else {
+        float am = 0.0f;
+#pragma unroll
+        for (int t = 0; t < COLS; ++t) {
+          h[t] = bf16_to_f32(f32_to_bf16(h[t]));  // bf16 round trip (kernels/gemm.py:198-200)
+          am = fmaxf(am, fabsf(h[t]));
+        }
+#pragma unroll
+        for (int m = 1; m < 64 / COLS; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
+        const float sc = fmaxf(am / 127.0f, 1e-8f);
+        int q[COLS];
+#pragma unroll
+        for (int t = 0; t < COLS; ++t) q[t] = round_i8(h[t] / sc);
+        if (cvalid) {
+          st_i8<COLS>(a.oq + (long long)orow * a.ncols + ocol, q);
+          if ((j & (64 / COLS - 1)) == 0) a.os[(long long)orow * (a.ncols / 64) + ocol / 64] = sc;
+        }
+      }
+    }
+  }
+}
+
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW, int KS>
+hipError_t launch_v(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
+  auto* k = skinny_kernel<ACT, WK, HZ, EPI, COLS, SPLIT, MAXW, KS>;
+  if (L.lds > 65536) {
+    static bool attr_set = false;  // benign race: every caller sets the same value
+    if (!attr_set) {
+      const hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               160 * 1024);
+      if (e != hipSuccess) return e;
+      attr_set = true;
+    }
+  }
+  hipLaunchKernelGGL(k, L.grid, dim3(64 * L.waves), L.lds, st, a);
+  return hipGetLastError();
+}
+
+// BIG: the variant also exists with up to 8 waves per workgroup.
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool BIG, int KS>
+hipError_t launch_t(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
+  if (L.waves > 4) {
+    if constexpr (BIG) {
+      if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 8, KS>(L, a, st);
+      return launch_v<ACT, WK, HZ, EPI, COLS, false, 8, KS>(L, a, st);
+    }
+    return hipErrorInvalidValue;
+  }
+  if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 4, KS>(L, a, st);
+  return launch_v<ACT, WK, HZ, EPI, COLS, false, 4, KS>(L, a, st);
+}
+
+#define QL_CASE(A, W, Z, E, C, B, KSV)                                                          \
+  if (L.act == A && L.wk == W && (L.hz != 0) == Z && L.epi == E && L.cols == C && L.ks == KSV) \
+    return launch_t<A, W, Z, E, C, B, KSV>(L, a, st);
+
+}  // namespace qlin
