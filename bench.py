@@ -227,37 +227,59 @@ def prefill_bench(args):
     lin = importlib.import_module(f"{ALIAS}.kernels.linear")
     gen = torch.Generator().manual_seed(99)
     ms = [128, 512, 2048]
-    items = []
-    for kind in ("w4", "w8"):  # W4 first: graph A below then holds most of the step
-        for (name, K, N) in PREFILL_SHAPES:
-            w = Weights(kind, K, N, dev, gen)
-            for M in ms:
-                x = torch.randn((M, K), generator=gen).to(torch.float16).to(dev)
-                o = torch.empty((M, N), dtype=torch.float16, device=dev)
-                items.append((kind, name, M, K, N, w, x, o))
+    # The weights exist in several copy sets (about 45 MB each, > 512 MB in all) and
+    # consecutive steps use different sets, so every step streams its weights from
+    # HBM rather than the 256 MB last-level cache, as consecutive layers would.
+    set_bytes = sum(bytes_w8(0, K, N) + bytes_w4(0, K, N) for (_, K, N) in PREFILL_SHAPES)
+    nsets = max(1, -(-600_000_000 // set_bytes))
+    xs = {}
+    outs = {}
+    for (name, K, N) in PREFILL_SHAPES:
+        for M in ms:
+            if (K, M) not in xs:
+                xs[(K, M)] = torch.randn((M, K), generator=gen).to(torch.float16).to(dev)
+            if (N, M) not in outs:
+                outs[(N, M)] = torch.empty((M, N), dtype=torch.float16, device=dev)
+    sets = []
+    for _ in range(nsets):
+        items = []
+        for kind in ("w4", "w8"):  # W4 first: graph A below then holds most of the step
+            for (name, K, N) in PREFILL_SHAPES:
+                w = Weights(kind, K, N, dev, gen)
+                for M in ms:
+                    items.append((kind, name, M, K, N, w, xs[(K, M)], outs[(N, M)]))
+        sets.append(items)
+    items = sets[0]
 
     # The cases before and after the dominant launch (the largest W8 case: M=2048,
-    # 2048x6144) replay as two HIP graphs; the dominant launch itself runs eagerly
-    # between them with HIP events on its launch stream, issued while graph A still
-    # occupies the GPU so that no host launch latency enters its timing.
+    # 2048x6144) replay as two HIP graphs per copy set; the dominant launch itself runs
+    # eagerly between them with HIP events on its launch stream, issued while graph A
+    # still occupies the GPU so that no host launch latency enters its timing.
     dom = next(i for i, it in enumerate(items) if it[0] == "w8" and it[2] == 2048 and it[1] == "gate")
-    for (_, _, _, _, _, w, x, o) in items:  # eager warm-up (workspace, LDS attributes)
-        w.run(lin, x, o)
+    for its in sets:  # eager warm-up (workspace, LDS attributes)
+        for (_, _, _, _, _, w, x, o) in its:
+            w.run(lin, x, o)
     torch.cuda.synchronize()
     graphs = []
-    for part in (items[:dom], items[dom + 1:]):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for (_, _, _, _, _, w, x, o) in part:
-                w.run(lin, x, o)
-        graphs.append(g)
+    for its in sets:
+        pair = []
+        for part in (its[:dom], its[dom + 1:]):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for (_, _, _, _, _, w, x, o) in part:
+                    w.run(lin, x, o)
+            pair.append(g)
+        graphs.append(pair)
     torch.cuda.synchronize()
     dom_ev = []
     record = {"on": False}
-    dw, dx, do = items[dom][5], items[dom][6], items[dom][7]
+    state = {"n": 0}
 
     def step():
-        graphs[0].replay()
+        c = state["n"] % nsets
+        state["n"] += 1
+        dw, dx, do = sets[c][dom][5], sets[c][dom][6], sets[c][dom][7]
+        graphs[c][0].replay()
         if record["on"]:
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
@@ -267,7 +289,7 @@ def prefill_bench(args):
             dom_ev.append((e0, e1))
         else:
             dw.run(lin, dx, do)
-        graphs[1].replay()
+        graphs[c][1].replay()
 
     flops = sum(2 * M * K * N for (_, _, M, K, N, _, _, _) in items)
     t = time_steps(step, args.steps, args.warmup, record)
@@ -279,16 +301,20 @@ def prefill_bench(args):
             "kernel": f"prefill_kernel w8 M={M} K={K} N={N}", "flops_per_launch": 2 * M * K * N,
             "avg_launch_us": round(dur * 1e6, 2)}
     if args.detail:
-        for (kind, name, M, K, N, w, x, o) in items:
+        # per case: one launch per copy set in turn (weights from HBM), HIP events
+        for i, (kind, name, M, K, N, _, x, o) in enumerate(items):
+            for its in sets:
+                its[i][5].run(lin, x, o)
+            torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            for _ in range(10):
-                w.run(lin, x, o)
+            for its in sets:
+                its[i][5].run(lin, x, o)
             e1.record()
             torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 100
+            us = e0.elapsed_time(e1) * 1e3 / nsets
             log(f"{kind} {name:>5} M={M:5d} K={K} N={N}: {us:9.1f} us {2 * M * K * N / us / 1e6:8.1f} TFLOP/s")
-    return flops, t, roof
+    return flops, t, roof, nsets
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -490,11 +516,13 @@ def main() -> int:
                   "launch": "hipgraph per M for layer shapes, eager vocab head" if not args.no_graph else "eager"}
         dtype = "f16 x int8" if kind == "w8" else "f16 x int4"
     else:
-        flops, t, roof = prefill_bench(args)
+        flops, t, roof, nsets = prefill_bench(args)
         value = flops / t / 1e12
         unit = "TFLOP/s"
         config = {"workload": "prefill GEMM, int8 and W4 g128, M in 128/512/2048",
-                  "shapes_KN": [[K, N] for (_, K, N) in PREFILL_SHAPES], "flops_per_step": flops}
+                  "shapes_KN": [[K, N] for (_, K, N) in PREFILL_SHAPES], "flops_per_step": flops,
+                  "weight_copy_sets": nsets,
+                  "launch": "hipgraph per copy set for 17 cases, eager dominant case"}
         dtype = "f16 x int8/int4"
 
     cpu = None

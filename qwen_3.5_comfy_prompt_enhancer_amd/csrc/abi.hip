@@ -355,7 +355,8 @@ int engine_gate_up(const char* fn, int wk, int epi, const int8_t* a_q, const flo
 // skinny kernel over row tiles, whichever a time model fitted to MI355X
 // measurements (fp16 x int8, W4 about 1.3x slower per tile) prefers:
 //   tiled:  fixed + rounds x (K tiles per workgroup) x t_tile(workgroups per CU)
-//           + split-K partial traffic (about 3.6 us per MB written and read back)
+//           + split-K: about 3 us of arrival round trips plus 0.5 us per MB of
+//             partials written and read back
 //   skinny: fixed + cost per (row x MB of int8-sized weights): its 16-row tiles
 //           re-read the weights from L2
 struct PfPlan {
@@ -386,7 +387,7 @@ PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
       const long long wgs = tiles * S;
       const int occ = (wgs > 256 && c.per_cu > 1) ? 2 : 1;
       const double rounds = (double)((wgs + 256LL * occ - 1) / (256LL * occ));
-      const double t = 5e-6 + rounds * (nk / S) * c.t_tile[occ - 1] * w4f + (S > 1 ? part_bytes * 3.6e-12 : 0.0);
+      const double t = 5e-6 + rounds * (nk / S) * c.t_tile[occ - 1] * w4f + (S > 1 ? 3e-6 + part_bytes * 0.5e-12 : 0.0);
       if (t < best_t) {
         best_t = t;
         best = PfPlan{true, c.shape, S};
@@ -457,6 +458,8 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
         int bm, bn, waves;
         prefill_geometry(p.shape, &bm, &bn, &waves);
         const size_t tiles = (size_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        if (!prefill_shape_ok(p.shape))
+          return fail(QLIN_ERR_UNSUPPORTED, "%s: QLIN_PREFILL_SHAPE=%d unknown", fn, p.shape);
         if (p.splits < 1 || (K / 64) % p.splits != 0 ||
             (p.splits > 1 && (tiles * p.splits * waves * 128 * 64 * sizeof(float) > part_cap ||
                               tiles > kCounterBytes / sizeof(unsigned))))

@@ -33,11 +33,11 @@
 //     would otherwise drain every in-flight copy before each LDS read, leaves the
 //     ring alone; the waits are explicit and count this kernel's own copies only.
 //   * Split-K: `splits` workgroups share an output tile, each over a contiguous
-//     range of K tiles.  Each stores its fp32 partial tile (agent-scope atomic
-//     stores, coherent across XCDs), waits for the stores, and bumps the tile's
-//     arrival counter; the last to arrive sums the partials in split order, resets
-//     the counter and runs the epilogue.  The sum order is fixed, so results are
-//     deterministic.
+//     range of K tiles.  Each stores its fp32 partial tile (16-byte device-coherent
+//     stores, readable from every XCD), waits for the stores, and bumps the tile's
+//     arrival counter; the last to arrive sums the partials in split order (all
+//     loads of one split in flight together), resets the counter and runs the
+//     epilogue.  The sum order is fixed, so results are deterministic.
 //   * The K order of every output element is fixed (tiles in order, two 32-wide
 //     substeps each, partials summed in split order), so a row's result depends on
 //     the split count and the number of wave groups but not on M or the tile size.
@@ -379,20 +379,21 @@ void prefill_kernel(const TlArgs a) {
   }
 
   if (S > 1) {
-    // partial tile of this wave: element e = (rb * 4 + t) * 4 + r of every lane,
-    // lane-minor so each store instruction writes 256 contiguous bytes
+    // Partial tile of this wave: the float4 (rb, t) of every lane at byte
+    // ((rb * 4 + t) * 64 + lane) * 16 of the wave's slot, so each store or load
+    // instruction moves 1 KiB contiguous.  Device-coherent (SC1) stores and loads;
+    // each workgroup's stores complete before it counts its arrival.
     __shared__ int s_last;
-    const long long wslot = 128LL * 64;
-    float* mine = a.part + (((long long)tile * S + split) * G::WAVES + wl) * wslot + lane;
+    constexpr unsigned kSlot = 128u * 64u * 4u;  // bytes of one wave's partial tile
+    const __amdgpu_buffer_rsrc_t rs =
+        part_rsrc(a.part + (long long)tile * S * G::WAVES * (128 * 64), (unsigned)(S * G::WAVES) * kSlot);
+    const unsigned lane_off = (unsigned)lane * 16u;
     if (kg == 0) {
+      const unsigned base = (unsigned)(split * G::WAVES + wl) * kSlot + lane_off;
 #pragma unroll
       for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            __hip_atomic_store(mine + ((rb * 4 + t) * 4 + r) * 64, acc[rb][t][r], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        for (int t = 0; t < 4; ++t) st_coherent(acc[rb][t], rs, base + (unsigned)(rb * 4 + t) * 1024u);
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
@@ -407,20 +408,17 @@ void prefill_kernel(const TlArgs a) {
     __syncthreads();
     if (!s_last || kg != 0) return;  // uniform over each wave
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    const float* base = a.part + ((long long)tile * S * G::WAVES + wl) * wslot + lane;
-    const long long sstride = (long long)G::WAVES * wslot;
+    // the last workgroup sums the partials in split order: 32 independent loads per split
+    for (int sp = 0; sp < S; ++sp) {
+      const unsigned base = (unsigned)(sp * G::WAVES + wl) * kSlot + lane_off;
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb)
+      for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float* pp = base + ((rb * 4 + t) * 4 + r) * 64;
-          float v = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          for (int sp = 1; sp < S; ++sp)
-            v += __hip_atomic_load(pp + sp * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          acc[rb][t][r] = v;
+        for (int t = 0; t < 4; ++t) {
+          const f32x4 v = ld_coherent(rs, base + (unsigned)(rb * 4 + t) * 1024u);
+          acc[rb][t] = (sp == 0) ? v : acc[rb][t] + v;
         }
+    }
   }
 
   // epilogue: lane holds rows 4g..4g+3 of each 16-row block, columns 4j..4j+3 of the
@@ -487,11 +485,14 @@ void prefill_geometry(int shape, int* bm, int* bn, int* waves) {
   else *bm = G1::BM, *bn = G1::BN, *waves = G1::WAVES;
 }
 
+bool prefill_shape_ok(int shape) { return shape >= 0 && shape < PF_SHAPES; }
+
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t st) {
   switch (shape) {
     case PF_128x128: return launch_prefill_g<1, 2, 1, 3>(a, wk, hz, st);
     case PF_128x128_K2: return launch_prefill_g<1, 2, 2, 3>(a, wk, hz, st);
-    default: return launch_prefill_g<2, 4, 1, 3>(a, wk, hz, st);
+    case PF_256x256: return launch_prefill_g<2, 4, 1, 3>(a, wk, hz, st);
+    default: return hipErrorInvalidValue;
   }
 }
 

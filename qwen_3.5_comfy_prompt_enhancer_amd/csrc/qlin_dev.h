@@ -124,6 +124,29 @@ __device__ __forceinline__ void w4_split_i8x16(uint32_t d, uint32_t& lo, uint32_
 }
 
 // ---------------------------------------------------------------------------
+// Split-K partials in the caller's workspace
+// ---------------------------------------------------------------------------
+
+// 16-byte loads and stores with the SC1 cache policy: device-coherent, the form that
+// agent-scope atomics take on gfx950.  A partial written this way by a workgroup on
+// one XCD is read correctly by a workgroup on another, without an L2 writeback or
+// invalidate, and the compiler tracks the loads like ordinary ones.
+constexpr int kCpolSc1 = 16;
+
+// raw buffer over `bytes` bytes from `base` (gfx9 descriptor word 3)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void st_coherent(const f32x4 v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+  __builtin_amdgcn_raw_buffer_store_b128(bitcast<u32x4>(v), r, off, 0, kCpolSc1);
+}
+
+__device__ __forceinline__ f32x4 ld_coherent(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return bitcast<f32x4>(__builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
+}
+
+// ---------------------------------------------------------------------------
 // MFMA wrappers (16x16 output; lane l holds D[4*(l/16)+r][l%16], r = 0..3)
 // ---------------------------------------------------------------------------
 

@@ -73,7 +73,7 @@ struct TlArgs {
   int odt;
   const void* res;    // 16-bit [M][ldr] or nullptr
   long long ldr;
-  int splits;         // workgroups per output tile along K (LDS-DMA kernel)
+  int splits;         // workgroups per output tile along K
   float* part;        // split-K partials [tiles][splits][waves][128 * 64], or nullptr
   unsigned* cnt;      // split-K arrival counters [tiles], zero between calls
 };
@@ -81,10 +81,11 @@ struct TlArgs {
 // LDS-DMA prefill kernel; `shape` picks the workgroup tile (rows x columns):
 // PF_128x128 (2 waves), PF_256x256 (8 waves, two per SIMD) and PF_128x128_K2 (two
 // wave groups split every K tile's substeps: 4 waves).
-enum PrefillShape { PF_128x128 = 0, PF_256x256 = 1, PF_128x128_K2 = 2 };
+enum PrefillShape { PF_128x128 = 0, PF_256x256 = 1, PF_128x128_K2 = 2, PF_SHAPES = 3 };
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t stream);
 // rows, columns and waves of a prefill workgroup tile
 void prefill_geometry(int shape, int* bm, int* bn, int* waves);
+bool prefill_shape_ok(int shape);
 
 hipError_t launch_w4_unpack(const uint8_t* p, int K, int N, uint8_t* out, hipStream_t st);
 hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uint8_t* z,

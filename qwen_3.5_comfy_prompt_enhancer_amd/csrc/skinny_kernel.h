@@ -504,13 +504,14 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   }
 
   // ---------------- reduction over workgroups (split-K) ----------------
-  // Partials travel as agent-scope atomic stores / loads (coherent across XCDs by
-  // themselves, so no whole-L2 writeback or invalidate is needed).  Each workgroup
-  // waits until its partial stores have completed before it increments the tile's
-  // arrival counter; the workgroup that sees the final count reads every partial.
+  // Partials travel as 16-byte device-coherent (SC1) stores and loads, readable from
+  // every XCD without a whole-L2 writeback or invalidate.  Each workgroup waits until
+  // its partial stores have completed before it increments the tile's arrival
+  // counter; the workgroup that sees the final count reads every partial.
   if constexpr (SPLIT) {
     __shared__ int s_last;
     const long long MN = (long long)M * a.ncols;
+    const __amdgpu_buffer_rsrc_t rs = part_rsrc(a.part, (unsigned)((long long)a.splits * NS * MN * 4));
     if (wave == 0) {
       if (g < RG && cvalid) {
 #pragma unroll
@@ -519,10 +520,12 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
           for (int r = 0; r < 4; ++r) {
             const int orow = rt * 16 + 4 * g + r;
             if (orow < M) {
-              float* pp = a.part + ((long long)split * NS + s) * MN + (long long)orow * a.ncols + ocol;
+              const unsigned off =
+                  (unsigned)((((long long)split * NS + s) * MN + (long long)orow * a.ncols + ocol) * 4);
 #pragma unroll
-              for (int t = 0; t < COLS; ++t)
-                __hip_atomic_store(pp + t, acc[s][t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              for (int q = 0; q < COLS / 4; ++q)
+                st_coherent(f32x4{acc[s][4 * q][r], acc[s][4 * q + 1][r], acc[s][4 * q + 2][r], acc[s][4 * q + 3][r]},
+                            rs, off + 16u * q);
             }
           }
       }
@@ -541,24 +544,25 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
     if (!s_last) return;  // uniform over the workgroup
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     // The last workgroup sums the tile's partials in split order, every thread on
-    // its own (set, row, column) elements, into red[s][row][col].
+    // its own (set, row, 4-column) groups, into red[s][row][col].
     const int tcol0 = (tile - sg0.tile0) * TN;  // tile's first column within the matrix
-    const int nel = NS * Mt * TN;
-    for (int e = threadIdx.x; e < nel; e += blockDim.x) {
-      const int s = e / (Mt * TN);
-      const int rem = e - s * (Mt * TN);
-      const int row = rem / TN;
-      const int col = rem - row * TN;
-      float v = 0.0f;
+    constexpr int TN4 = TN / 4;
+    const int nel4 = NS * Mt * TN4;
+    const unsigned sstride = (unsigned)(NS * MN * 4);
+    for (int e = threadIdx.x; e < nel4; e += blockDim.x) {
+      const int s = e / (Mt * TN4);
+      const int rem = e - s * (Mt * TN4);
+      const int row = rem / TN4;
+      const int col = (rem - row * TN4) * 4;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
       if (tcol0 + col < n) {
-        const float* pp = a.part + (long long)s * MN + (long long)(rt * 16 + row) * a.ncols + sg0.col0 + tcol0 + col;
-        const long long stride = (long long)NS * MN;
-        v = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned off =
+            (unsigned)(((long long)s * MN + (long long)(rt * 16 + row) * a.ncols + sg0.col0 + tcol0 + col) * 4);
+        v = ld_coherent(rs, off);
 #pragma unroll 8
-        for (int p = 1; p < a.splits; ++p)
-          v += __hip_atomic_load(pp + p * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int p = 1; p < a.splits; ++p) v += ld_coherent(rs, off + (unsigned)p * sstride);
       }
-      red[(s * 16 + row) * TN + col] = v;
+      *(f32x4*)&red[(s * 16 + row) * TN + col] = v;
     }
     __syncthreads();
     if (wave == 0 && g < RG) {

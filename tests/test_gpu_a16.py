@@ -247,24 +247,25 @@ def test_prefill_w4(M, group, zeros, sdt, shape, monkeypatch):
                                                np.arange(N)))
 
 
-def test_prefill_tile_shapes_agree(monkeypatch):
+@pytest.mark.parametrize("shapes", [(0, 1)])
+def test_prefill_tile_shapes_agree(shapes, monkeypatch):
     """The single-group workgroup tiles (128x128, 256x256) accumulate each output
     element over the same K order, so they give bit-identical results (W8 and W4
     with zeros).  The two-group shape sums its groups' substeps separately (another
-    rounding order) and is checked against the oracle instead."""
+    rounding order) and is checked against the oracle in the tests above."""
     M, K, N = 300, 1024, 1280
     x = H.act_f16(M, K, seed=340)
     w, s = H.w8(K, N, seed=341)
     packed, s4, z = H.w4(K, N, seed=342, group=64, zeros="random")
     outs = []
-    for shape in (0, 1):
+    for shape in shapes:
         _force_tiled(monkeypatch, shape)
         outs.append((_run_w8(x, w, s), _run_w4(x, packed, s4, z)))
     for o in outs[1:]:
         assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1])
 
 
-@pytest.mark.parametrize("shape,splits", [(0, 2), (0, 16), (1, 4), (1, 8), (2, 4)])
+@pytest.mark.parametrize("shape,splits", [(0, 2), (0, 16), (1, 4), (1, 8), (2, 4), (2, 16)])
 def test_prefill_split_k(shape, splits, monkeypatch):
     """Split-K: each of `splits` workgroups per tile covers K/splits; the last to
     arrive sums the fp32 partials in split order.  Checked against the oracle (W8
