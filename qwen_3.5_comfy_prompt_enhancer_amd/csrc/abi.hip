@@ -75,6 +75,24 @@ void plan_override(const Problem& P, int& cols, int& waves, int& upw) {
 // is computed the same way for every M <= 16.
 int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
                     hipStream_t stream) {
+  // Engine-signature stores with more than 16 rows (prefill chunks): the tiled int8
+  // kernel where it applies and a time model fitted to MI355X measurements prefers it
+  // to the 16-row tiles:
+  //   tiled:  4 us + rounds of 256 workgroups x 128-wide K stages x 1.5 us
+  //   rows:   10 us + 7 ns per row per MB of int8-sized weights
+  // QLIN_ENGINE_PREFILL ("tiled" or "skinny") overrides the choice (tests, tuning).
+  if (P.act == ACT_I8 && P.epi == EPI_STORE && prefill_i8_ok(a, P.wk)) {
+    const char* e = getenv("QLIN_ENGINE_PREFILL");
+    const bool force_rows = e && strcmp(e, "skinny") == 0;
+    const bool force_tiled = e && strcmp(e, "tiled") == 0;
+    long long tiles_n = 0;
+    for (int s = 0; s < a.nseg; ++s) tiles_n += a.seg[s].n / 128;
+    const long long tiles = (long long)((P.M + 127) / 128) * tiles_n;
+    const double t_tiled = 4e-6 + (double)((tiles + 255) / 256) * ((P.K / 64 + 1) / 2) * 1.5e-6;
+    const double t_rows = 10e-6 + 7e-9 * P.M * ((double)P.K * P.ncols / 1e6);
+    if (force_tiled || (!force_rows && t_tiled < t_rows))
+      return hip_status(fn, launch_prefill_i8(a, P.wk, P.hz, stream));
+  }
   SkLaunch L;
   L.act = P.act;
   L.wk = P.wk;

@@ -217,3 +217,125 @@ def test_bad_arguments_raise_before_launch():
     out = torch.empty((2, 40), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError):
         gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)
+
+
+# ---------------------------------------------------------------- prefill-sized M (tiled int8 kernel)
+#
+# Engine-signature stores with more than 16 rows can run on the tiled int8 MFMA
+# kernel when K % 64 == 0, every projection is a multiple of 128 columns and W4
+# groups are at least 64; a time model picks it or the 16-row tiles.  The tests
+# force it with QLIN_ENGINE_PREFILL=tiled (=skinny forces the row tiles).
+
+
+@pytest.fixture
+def tiled(monkeypatch):
+    monkeypatch.setenv("QLIN_ENGINE_PREFILL", "tiled")
+    return monkeypatch
+
+@pytest.mark.parametrize("M", [17, 130, 300])
+@pytest.mark.parametrize("K", [64, 192, 2048])
+def test_gemm_i8_prefill_tiled(M, K, tiled):
+    gemm, _ = _g()
+    N = 1024
+    a, as_ = H.engine_act(M, K, seed=400 + M + K)
+    b, bs = H.engine_w8(K, N, seed=401)
+    hid = torch.randn((M, N), generator=H.gen(402)).to(torch.bfloat16)
+    ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy(), bs.numpy(), residual=_bf16(hid))
+    h = hid.cuda()
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), h, residual=h)   # in place (engine.py:238-240)
+    H.assert_out_close(h, ref)
+    assert R.rel_l2(H.to_f32(h), ref) < 3e-3
+
+
+@pytest.mark.parametrize("group,zeros", [(64, "none"), (128, "random"), (128, "eight"), (256, "random")])
+@pytest.mark.parametrize("M", [40, 256])
+def test_gemm_w4_prefill_tiled(group, zeros, M, tiled):
+    gemm, _ = _g()
+    K, N = 1024, 1280
+    a, as_ = H.engine_act(M, K, seed=410 + M)
+    b, bs, bz = _w4_engine(K, N, seed=411, group=group, zeros=zeros)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    res = torch.randn((M, N), generator=H.gen(412)).to(torch.bfloat16)
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out, residual=res.cuda(),
+                 b_z=None if bz is None else bz.cuda())
+    ref = R.gemm_w4_ref(a.numpy(), as_.numpy(), b.numpy(), _bf16(bs),
+                        None if bz is None else bz.numpy(), residual=_bf16(res))
+    H.assert_out_close(out, ref)
+
+
+def test_prefill_tiled_w4_explicit_zero_eight_is_identical(tiled):
+    _, w4 = _g()
+    M, K, N = 64, 1024, 1024
+    a, as_ = H.engine_act(M, K, seed=420)
+    b, bs, _ = _w4_engine(K, N, seed=421)
+    z8 = torch.full((K // 128, N), 8, dtype=torch.uint8, device="cuda")
+    o0 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    o1 = torch.empty_like(o0)
+    w4.gemm_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), o0)
+    w4.gemm_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), o1, b_z=z8)
+    assert torch.equal(o0, o1)
+
+
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+def test_prefill_tiled_rows_independent_of_chunking(kind, tiled):
+    """Rows of an M=300 call equal the same rows computed as an M=100 chunk: the
+    tiled kernel's K order does not depend on M (chunked prefill, ENGINEERING.md:453-455)."""
+    gemm, _ = _g()
+    K, N = 2048, 1024
+    a, as_ = H.engine_act(300, K, seed=430)
+    if kind == "w8":
+        b, bs = H.engine_w8(K, N, seed=431)
+        bz = None
+    else:
+        b, bs, bz = _w4_engine(K, N, seed=431, zeros="random")
+    cu = lambda t: None if t is None else t.cuda()
+    y = torch.empty((300, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y, b_z=cu(bz))
+    yc = torch.empty((100, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a[100:200].contiguous().cuda(), as_[100:200].contiguous().cuda(), b.cuda(), bs.cuda(), yc, b_z=cu(bz))
+    assert torch.equal(y[100:200], yc)
+
+
+def test_prefill_tiled_matches_row_tiles(tiled):
+    """The tiled kernel and the 16-row skinny kernel compute the same products and
+    block scales in different fp32 orders: they agree to the GEMM tolerance."""
+    gemm, _ = _g()
+    M, K, N = 96, 2048, 2048
+    a, as_ = H.engine_act(M, K, seed=440)
+    b, bs = H.engine_w8(K, N, seed=441)
+    y0 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y0)
+    tiled.setenv("QLIN_ENGINE_PREFILL", "skinny")
+    y1 = torch.empty_like(y0)
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y1)
+    f0, f1 = H.to_f32(y0).astype(np.float64), H.to_f32(y1).astype(np.float64)
+    # both are bf16-rounded: allow the tolerance plus one bf16 ulp
+    assert np.all(np.abs(f0 - f1) <= 2e-3 * np.abs(f1).max() + 2 * H.half_ulp(f1, torch.bfloat16))
+
+
+@pytest.mark.parametrize("N,group", [(1040, 128), (1024, 32)])
+def test_prefill_outside_tiled_kernel(N, group, tiled):
+    """Column counts that are not a multiple of 128 and W4 group 32 stay on the
+    16-row tiles; still checked against the oracle."""
+    gemm, _ = _g()
+    M, K = 40, 1024
+    a, as_ = H.engine_act(M, K, seed=450)
+    b, bs, bz = _w4_engine(K, N, seed=451, group=group, zeros="random")
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out, b_z=bz.cuda())
+    ref = R.gemm_w4_ref(a.numpy(), as_.numpy(), b.numpy(), _bf16(bs), bz.numpy())
+    H.assert_out_close(out, ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 6144), (512, 6144, 2048)])
+def test_engine_prefill_default_dispatch(M, K, N):
+    """Engine prefill chunk sizes with the library's own choice of kernel (tiled int8
+    for the wide shape, 16-row tiles for the deep one), sampled columns."""
+    gemm, _ = _g()
+    a, as_ = H.engine_act(M, K, seed=460)
+    b, bs = H.engine_w8(K, N, seed=461)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)
+    cols = H.sample_cols(N, 512, seed=462)
+    ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy()[:, cols], bs.numpy()[cols])
+    H.assert_out_close(out.cpu()[:, cols], ref)
