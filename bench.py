@@ -16,7 +16,8 @@ dominant kernel's live per-launch time for the roofline object.
 
 Other workloads (`--workload`): decode-w4 (same shapes, W4 group 128), prefill
 (M in 128/512/2048, TFLOP/s), chain-w4 (9B-class 32-layer W4 decode chain), single
-(one 2048x6144 int8 linear, M=1).
+(one 2048x6144 int8 linear, M=1), engine-w8 / engine-w4 (the engine-signature calls
+of one layer at decode rows and a 512-row prefill chunk).
 
 Prints ONE JSON line (rank 0).  Synthetic data; weights are random in the engine
 layouts.
@@ -317,6 +318,90 @@ def prefill_bench(args):
     return flops, t, roof, nsets
 
 
+# ------------------------------------------------------------------ engine layer
+
+ENGINE_LAYER = [  # the engine's four quantized calls of one 2B-class layer (engine.py:221-340)
+    ("proj3 lin_qkv+lin_z", 2048, 6144 + 2048),
+    ("gemm_i8 o + residual", 2048, 2048),
+    ("mlp_gate_up_quant", 2048, 2 * 6144),
+    ("gemm_i8 down + residual", 6144, 2048),
+]
+
+
+def engine_bench(args, kind):
+    """The engine-signature calls of one layer (int8 activations with per-64 scales,
+    bf16 outputs, in-place residuals, the fused gate/up + requantization) over
+    `layers` weight copies, at decode rows M = 1, 4 and a prefill chunk M = 512.
+    Returns (bytes per step at M = 1, 4; flops per step at M = 512; per-M times)."""
+    import torch
+    dev = torch.device("cuda", 0)
+    gemm = importlib.import_module(f"{ALIAS}.kernels.gemm")
+    gen = torch.Generator().manual_seed(77)
+    layers = max(1, args.layers)
+
+    def wmat(K, N):
+        if kind == "w8":
+            return (torch.randint(-127, 128, (K, N), generator=gen, dtype=torch.int8).to(dev),
+                    (torch.rand(N, generator=gen) * 1e-3).to(dev), None)
+        return (torch.randint(0, 256, (K // 2, N), generator=gen, dtype=torch.uint8).to(dev),
+                (torch.rand(K // 128, N, generator=gen) * 1e-3).to(torch.bfloat16).to(dev), None)
+
+    lw = [dict(qkv=wmat(2048, 6144), z=wmat(2048, 2048), o=wmat(2048, 2048), g=wmat(2048, 6144),
+               u=wmat(2048, 6144), d=wmat(6144, 2048)) for _ in range(layers)]
+
+    def wbytes(K, N):
+        return K * N if kind == "w8" else K * N // 2 + (K // 128) * N * 2
+
+    layer_wbytes = wbytes(2048, 8192) + wbytes(2048, 2048) + 2 * wbytes(2048, 6144) + wbytes(6144, 2048)
+    res = {}
+    for M in (1, 4, 512):
+        a = torch.randint(-127, 128, (M, 2048), generator=gen, dtype=torch.int8).to(dev)
+        s = (torch.rand(M, 32, generator=gen) * 1e-2).to(dev)
+        a6 = torch.randint(-127, 128, (M, 6144), generator=gen, dtype=torch.int8).to(dev)
+        s6 = (torch.rand(M, 96, generator=gen) * 1e-2).to(dev)
+        qkvz = torch.empty(M, 8192, dtype=torch.bfloat16, device=dev)
+        hid = torch.zeros(M, 2048, dtype=torch.bfloat16, device=dev)
+        hq = torch.empty(M, 6144, dtype=torch.int8, device=dev)
+        hs = torch.empty(M, 96, dtype=torch.float32, device=dev)
+        if kind == "w8":
+            fns = (gemm.proj3, gemm.gemm_i8, gemm.mlp_gate_up_quant)
+        else:
+            w4 = importlib.import_module(f"{ALIAS}.kernels.w4")
+            fns = (w4.proj3_w4, w4.gemm_w4, w4.mlp_gate_up_quant_w4)
+
+        def run_layers():
+            for L in lw:
+                fns[0](a, s, L["qkv"][0], L["qkv"][1], L["z"][0], L["z"][1], None, None, qkvz)
+                fns[1](a, s, L["o"][0], L["o"][1], hid, residual=hid)
+                fns[2](a, s, L["g"][0], L["g"][1], L["u"][0], L["u"][1], hq, hs)
+                fns[1](a6, s6, L["d"][0], L["d"][1], hid, residual=hid)
+
+        run_layers()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run_layers()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        res[M] = e0.elapsed_time(e1) * 1e-3 / args.steps / layers
+    act_bytes = lambda M: M * (2048 * 3 + 6144) + M * 4 * (32 * 3 + 96)
+    out_bytes = lambda M: M * 2 * (8192 + 2048 * 2 * 2) + M * (6144 + 96 * 4)
+    dec_bytes = {M: layer_wbytes + act_bytes(M) + out_bytes(M) for M in (1, 4)}
+    flops = 2 * 512 * (2048 * 8192 + 2048 * 2048 + 2048 * 12288 + 6144 * 2048)
+    for M in (1, 4, 512):
+        extra = (f"{dec_bytes[M] / res[M] / 1e9:7.0f} GB/s" if M in dec_bytes
+                 else f"{flops / res[M] / 1e12:7.1f} TOPS")
+        log(f"engine {kind} layer M={M:4d}: {res[M] * 1e6:8.1f} us per layer  {extra}")
+    return dec_bytes, flops, res
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(kind, shapes, head, budget_s=15.0):
@@ -451,7 +536,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode-w8",
                     choices=["decode-w8", "decode-w4", "prefill", "chain-w4", "single", "head-pmc",
-                             "prefill-pmc"])
+                             "prefill-pmc", "engine-w8", "engine-w4"])
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -515,6 +600,21 @@ def main() -> int:
                   "bytes_per_step": total,
                   "launch": "hipgraph per M for layer shapes, eager vocab head" if not args.no_graph else "eager"}
         dtype = "f16 x int8" if kind == "w8" else "f16 x int4"
+    elif wl in ("engine-w8", "engine-w4"):
+        kind = wl.split("-")[1]
+        dec_bytes, pf_flops, res = engine_bench(args, kind)
+        # value: decode rows M = 1 and 4 through the engine's calls, weight-streaming GB/s
+        t = (res[1] + res[4]) / 2
+        value = (dec_bytes[1] + dec_bytes[4]) / (res[1] + res[4]) / 1e9
+        unit = "GB/s"
+        config = {"workload": f"engine-signature calls of one 2B-class layer ({kind}): proj3, gemm_i8 + "
+                              "residual, mlp_gate_up_quant, gemm_i8 + residual",
+                  "rows_M": [1, 4], "layer_copies": args.layers,
+                  "shapes_KN": [[K, N] for (_, K, N) in ENGINE_LAYER],
+                  "prefill_chunk_M512_us_per_layer": round(res[512] * 1e6, 1),
+                  "prefill_chunk_M512_tops": round(pf_flops / res[512] / 1e12, 1),
+                  "launch": "hipgraph of all layers per M"}
+        dtype = "i8 x int8" if kind == "w8" else "i8 x int4"
     else:
         flops, t, roof, nsets = prefill_bench(args)
         value = flops / t / 1e12

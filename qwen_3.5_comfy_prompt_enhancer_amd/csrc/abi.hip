@@ -81,17 +81,18 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   //   tiled:  4 us + rounds of 256 workgroups x 128-wide K stages x 1.5 us
   //   rows:   10 us + 7 ns per row per MB of int8-sized weights
   // QLIN_ENGINE_PREFILL ("tiled" or "skinny") overrides the choice (tests, tuning).
-  if (P.act == ACT_I8 && P.epi == EPI_STORE && prefill_i8_ok(a, P.wk)) {
+  if (P.act == ACT_I8 && prefill_i8_ok(a, P.wk, P.epi)) {
     const char* e = getenv("QLIN_ENGINE_PREFILL");
     const bool force_rows = e && strcmp(e, "skinny") == 0;
     const bool force_tiled = e && strcmp(e, "tiled") == 0;
     long long tiles_n = 0;
-    for (int s = 0; s < a.nseg; ++s) tiles_n += a.seg[s].n / 128;
+    for (int s = 0; s < (P.epi == EPI_STORE ? a.nseg : 1); ++s) tiles_n += a.seg[s].n / 128;
     const long long tiles = (long long)((P.M + 127) / 128) * tiles_n;
-    const double t_tiled = 4e-6 + (double)((tiles + 255) / 256) * ((P.K / 64 + 1) / 2) * 1.5e-6;
-    const double t_rows = 10e-6 + 7e-9 * P.M * ((double)P.K * P.ncols / 1e6);
+    // gate/up computes two weight sets per tile
+    const double t_tiled = 4e-6 + (double)((tiles + 255) / 256) * ((P.K / 64 + 1) / 2) * 1.5e-6 * P.nsets;
+    const double t_rows = 10e-6 + 7e-9 * P.M * ((double)P.K * P.ncols * P.nsets / 1e6);
     if (force_tiled || (!force_rows && t_tiled < t_rows))
-      return hip_status(fn, launch_prefill_i8(a, P.wk, P.hz, stream));
+      return hip_status(fn, launch_prefill_i8(a, P.wk, P.hz, P.epi, stream));
   }
   SkLaunch L;
   L.act = P.act;

@@ -1,12 +1,16 @@
 // Tiled int8-activation GEMM for the engine-signature calls with more than 16 rows
-// (prefill chunks), gfx950: int8 or W4 weights, the store epilogue.
+// (prefill chunks), gfx950: int8 or W4 weights; the store epilogue and the fused
+// gate/up epilogues (silu(g) * u, optionally requantized per 64 columns).
 //
-// Replaces the prefill-sized launches of gemm_i8, gemm_w4 and proj3(_w4)
-// (kernels/gemm.py:20-92, 234-312; kernels/w4.py:64-166, 169-251) with the
+// Replaces the prefill-sized launches of gemm_i8, gemm_w4, proj3(_w4) and
+// mlp_gate_up(_quant)(_w4) (kernels/gemm.py:20-312; kernels/w4.py:64-323) with the
 // reference's arithmetic: an exact int32 dot per 64-wide activation block, then
 // `acc += float(dot) * a_s[m, block]` in fp32 (W4: per 64-wide weight sub-block,
 // `acc += float(dot) * (a_s * b_s[group, n])`, w4.py:103-104), then the column scale
-// (W8), the residual and a 16-bit store (gemm.py:43-57).
+// (W8) and either the residual and a 16-bit store (gemm.py:43-57) or, for gate/up
+// (two weight sets feeding one tile), h = silu(g) * u, stored as bf16 or rounded
+// through bf16 and quantized per 64 columns with max(amax / 127, 1e-8) and round
+// half away from zero (gemm.py:195-211).
 //
 //   * Workgroup tile 128 x 128, 8 waves: 2 x 2 wave tiles of 64 x 64, times two K
 //     groups.  A stage of the LDS ring holds two activation blocks (128 K); group kg
@@ -20,8 +24,8 @@
 //     nibbles become int8 16 * (n - 8) (even K then odd K), the activation operand
 //     is permuted to the same order, and the dot is shifted right by 4 (exact);
 //     explicit zeros add (8 - z) * sum(a) from one more MFMA against all-ones.
-//   * Copies: global -> registers (three stages ahead) -> LDS (one stage ahead), one
-//     barrier per stage.
+//   * Copies: global -> registers (three stages ahead, two for gate/up) -> LDS (one
+//     stage ahead), one barrier per stage.
 //   * The K order of every output element is fixed (blocks in order within each K
 //     group, then group 0 + group 1), so rows do not depend on M or on the chunking.
 #include "qlin_dev.h"
@@ -36,17 +40,18 @@ constexpr int WAVES = 8;
 constexpr int THREADS = 64 * WAVES;
 constexpr int GROUP_M = 8;  // tile order: 8 row tiles per group share weight column tiles in L2
 
-template <int WK>
+template <int WK, int NS>
 struct Gi8 {
   static constexpr bool W4 = WK == WK_W4;
   static constexpr int A_BLK = BM * 64;                 // activation bytes of one block
   static constexpr int B_ROWS = W4 ? 32 : 64;           // weight rows of one block
-  static constexpr int B_BLK = B_ROWS * BN;             // weight bytes of one block
-  static constexpr int AS_OFF = 2 * A_BLK + 2 * B_BLK;  // activation scales: [2][128] fp32
-  static constexpr int BS_OFF = AS_OFF + 2 * BM * 4;    // W4 group scales: [2][128] fp32
-  static constexpr int BZ_OFF = BS_OFF + (W4 ? 2 * BN * 4 : 0);  // W4 zeros: [2][128] bytes
-  static constexpr int STAGE = BZ_OFF + (W4 ? 2 * BN : 0);
-  static constexpr int RED = 4 * 64 * 64 * 4;  // group 1's accumulators at the end
+  static constexpr int B_BLK = B_ROWS * BN;             // weight bytes of one block of one set
+  static constexpr int B_OFF = 2 * A_BLK;               // weights: [set][2 blocks]
+  static constexpr int AS_OFF = B_OFF + NS * 2 * B_BLK;  // activation scales: [2][128] fp32
+  static constexpr int BS_OFF = AS_OFF + 2 * BM * 4;    // W4 group scales: [set][2][128] fp32
+  static constexpr int BZ_OFF = BS_OFF + (W4 ? NS * 2 * BN * 4 : 0);  // W4 zeros: [set][2][128] bytes
+  static constexpr int STAGE = BZ_OFF + (W4 ? NS * 2 * BN : 0);
+  static constexpr int RED = 4 * 64 * 64 * 4;  // one set of group 1's accumulators at the end
   static constexpr int LDS = (2 * STAGE > RED) ? 2 * STAGE : RED;
 };
 
@@ -58,9 +63,10 @@ __device__ __forceinline__ int a_off(int r, int c) { return r * 64 + 16 * (c ^ (
 
 }  // namespace
 
-template <int WK, bool HZ>
+template <int WK, bool HZ, int EPI>
 __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
-  using G = Gi8<WK>;
+  constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;  // weight sets feeding one tile
+  using G = Gi8<WK, NS>;
   constexpr bool W4 = G::W4;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -81,9 +87,20 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   const int tm = first_m + (tile % per_group) % gsize;
   const int tn = (tile % per_group) / gsize;
   int si = 0;
-  if (a.nseg > 1 && tn >= a.seg[1].tile0) si = 1;
-  if (a.nseg > 2 && tn >= a.seg[2].tile0) si = 2;
+  if constexpr (EPI == EPI_STORE) {
+    if (a.nseg > 1 && tn >= a.seg[1].tile0) si = 1;
+    if (a.nseg > 2 && tn >= a.seg[2].tile0) si = 2;
+  }
   const Seg sg = a.seg[si];
+  const uint8_t* wset[NS];
+  const void* sset[NS];
+  const uint8_t* zset[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    wset[s] = a.seg[si + s].w;
+    sset[s] = a.seg[si + s].s;
+    zset[s] = a.seg[si + s].z;
+  }
   const int n = sg.n;
   const int ncol0 = (tn - sg.tile0) * BN;  // tile's first column within its matrix
   const int m0 = tm * BM;
@@ -96,10 +113,10 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   const int NG = K / 64;
   struct Regs {
     u32x4 av[2];
-    u32x4 bv[W4 ? 1 : 2];
+    u32x4 bv[NS][W4 ? 1 : 2];
     float as_;
-    float bs;
-    uint32_t bz;
+    float bs;     // W4: one group scale of set tid / 256
+    uint32_t bz;  // W4 with zeros: the matching zero
   };
   auto fetch = [&](Regs& rg, int st) {
 #pragma unroll
@@ -110,30 +127,38 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
       const int row = min(m0 + r, M - 1);
       rg.av[i] = *(const u32x4*)(xq + (long long)row * K + blk * 64 + 16 * c);
     }
-    if constexpr (W4) {
-      const int k2 = tid >> 8, r = (tid & 255) >> 3, c = tid & 7;
-      const int blk = min(2 * st + k2, nk - 1);
-      rg.bv[0] = *(const u32x4*)(sg.w + (long long)(blk * 32 + r) * n + ncol0 + 16 * c);
-    } else {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int q = tid + THREADS * i;
-        const int k2 = q >> 9, r = (q & 511) >> 3, c = q & 7;
+    for (int s = 0; s < NS; ++s) {
+      if constexpr (W4) {
+        const int k2 = tid >> 8, r = (tid & 255) >> 3, c = tid & 7;
         const int blk = min(2 * st + k2, nk - 1);
-        rg.bv[i] = *(const u32x4*)(sg.w + (long long)(blk * 64 + r) * n + ncol0 + 16 * c);
+        rg.bv[s][0] = *(const u32x4*)(wset[s] + (long long)(blk * 32 + r) * n + ncol0 + 16 * c);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int q = tid + THREADS * i;
+          const int k2 = q >> 9, r = (q & 511) >> 3, c = q & 7;
+          const int blk = min(2 * st + k2, nk - 1);
+          rg.bv[s][i] = *(const u32x4*)(wset[s] + (long long)(blk * 64 + r) * n + ncol0 + 16 * c);
+        }
       }
     }
     if (tid < 256) {
       const int k2 = tid >> 7, r = tid & 127;
       const int blk = min(2 * st + k2, nk - 1);
       rg.as_ = a.xs[(long long)min(m0 + r, M - 1) * NG + blk];
-    } else if constexpr (W4) {
-      const int t2 = tid - 256;
-      const int k2 = t2 >> 7, c = t2 & 127;
-      const int blk = min(2 * st + k2, nk - 1);
-      const long long gi = (long long)(blk * 64 / a.group) * n + ncol0 + c;
-      rg.bs = load_scale(sg.s, a.sdt, gi);
-      if constexpr (HZ) rg.bz = sg.z[gi];
+    }
+    if constexpr (W4) {
+      // group scales (and zeros) of both blocks: 256 per set, thread tid takes one of
+      // set tid / 256
+      const int s = tid >> 8;
+      if (s < NS) {
+        const int t2 = tid & 255, k2 = t2 >> 7, c = t2 & 127;
+        const int blk = min(2 * st + k2, nk - 1);
+        const long long gi = (long long)(blk * 64 / a.group) * n + ncol0 + c;
+        rg.bs = load_scale(sset[s], a.sdt, gi);
+        if constexpr (HZ) rg.bz = zset[s][gi];
+      }
     }
   };
   auto store = [&](const Regs& rg, int buf) {
@@ -144,31 +169,37 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
       const int k2 = q >> 9, r = (q & 511) >> 2, c = q & 3;
       *(u32x4*)(base + k2 * G::A_BLK + a_off(r, c)) = rg.av[i];
     }
-    if constexpr (W4) {
-      const int k2 = tid >> 8, r = (tid & 255) >> 3, c = tid & 7;
-      *(u32x4*)(base + 2 * G::A_BLK + k2 * G::B_BLK + r * BN + 16 * c) = rg.bv[0];
-    } else {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int q = tid + THREADS * i;
-        const int k2 = q >> 9, r = (q & 511) >> 3, c = q & 7;
-        *(u32x4*)(base + 2 * G::A_BLK + k2 * G::B_BLK + r * BN + 16 * c) = rg.bv[i];
+    for (int s = 0; s < NS; ++s) {
+      uint8_t* sb = base + G::B_OFF + s * 2 * G::B_BLK;
+      if constexpr (W4) {
+        const int k2 = tid >> 8, r = (tid & 255) >> 3, c = tid & 7;
+        *(u32x4*)(sb + k2 * G::B_BLK + r * BN + 16 * c) = rg.bv[s][0];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int q = tid + THREADS * i;
+          const int k2 = q >> 9, r = (q & 511) >> 3, c = q & 7;
+          *(u32x4*)(sb + k2 * G::B_BLK + r * BN + 16 * c) = rg.bv[s][i];
+        }
       }
     }
-    if (tid < 256) {
-      ((float*)(base + G::AS_OFF))[tid] = rg.as_;
-    } else if constexpr (W4) {
-      const int t2 = tid - 256;
-      ((float*)(base + G::BS_OFF))[t2] = rg.bs;
-      if constexpr (HZ) base[G::BZ_OFF + t2] = (uint8_t)rg.bz;
+    if (tid < 256) ((float*)(base + G::AS_OFF))[tid] = rg.as_;
+    if constexpr (W4) {
+      if ((tid >> 8) < NS) {
+        ((float*)(base + G::BS_OFF))[tid] = rg.bs;
+        if constexpr (HZ) base[G::BZ_OFF + tid] = (uint8_t)rg.bz;
+      }
     }
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[NS][4][4];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int s = 0; s < NS; ++s)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[rb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[s][rb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const i32x4 izero = i32x4{0, 0, 0, 0};
   const int cb = wn * 64 + 4 * j;  // lane's first column within the tile
@@ -177,7 +208,6 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   auto compute = [&](int buf) {
     const uint8_t* base = lds + buf * G::STAGE;
     const uint8_t* sa = base + kg * G::A_BLK;
-    const uint8_t* sb = base + 2 * G::A_BLK + kg * G::B_BLK;
     i32x4 av[4];
     f32x4 asv[4];
 #pragma unroll
@@ -186,179 +216,262 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
       av[rb] = *(const i32x4*)(sa + a_off(r, g));
       asv[rb] = *(const f32x4*)(base + G::AS_OFF + (kg * BM + wm * 64 + rb * 16 + 4 * g) * 4);
     }
-    u32x4 bv[4];
     if constexpr (W4) {
-      uint32_t lo[8], hi[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) w4_split_i8x16(*(const uint32_t*)(sb + (8 * g + i) * BN + cb), lo[i], hi[i]);
-      uint32_t e0[4], e1[4], o0[4], o1[4];
-      tr4(lo[0], lo[1], lo[2], lo[3], e0);
-      tr4(lo[4], lo[5], lo[6], lo[7], e1);
-      tr4(hi[0], hi[1], hi[2], hi[3], o0);
-      tr4(hi[4], hi[5], hi[6], hi[7], o1);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) bv[t] = u32x4{e0[t], e1[t], o0[t], o1[t]};
-      // activation slots in the same order: even K of the 16, then odd K
+      // activation slots in the order of the nibble split: even K of the 16, then odd K
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
         const u32x4 x = bitcast<u32x4>(av[rb]);
         av[rb] = bitcast<i32x4>(u32x4{perm(x.y, x.x, 0x06040200u), perm(x.w, x.z, 0x06040200u),
                                       perm(x.y, x.x, 0x07050301u), perm(x.w, x.z, 0x07050301u)});
       }
-    } else {
-      uint32_t d[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) d[i] = *(const uint32_t*)(sb + (16 * g + i) * BN + cb);
-      uint32_t x0[4], x1[4], x2[4], x3[4];
-      tr4(d[0], d[1], d[2], d[3], x0);
-      tr4(d[4], d[5], d[6], d[7], x1);
-      tr4(d[8], d[9], d[10], d[11], x2);
-      tr4(d[12], d[13], d[14], d[15], x3);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) bv[t] = u32x4{x0[t], x1[t], x2[t], x3[t]};
     }
-    if constexpr (W4) {
-      const f32x4 bsv = *(const f32x4*)(base + G::BS_OFF + (kg * BN + cb) * 4);
-      uint32_t zw = 0;
-      if constexpr (HZ) zw = *(const uint32_t*)(base + G::BZ_OFF + kg * BN + cb);
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        i32x4 sx = izero;
-        if constexpr (HZ)
-          sx = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(u32x4{0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u}), izero, 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            int v = p[r] >> 4;  // exact: the MFMA summed 16 * (nibble - 8)
-            if constexpr (HZ) v += (8 - (int)((zw >> (8 * t)) & 0xFFu)) * sx[r];
-            acc[rb][t][r] = fmaf((float)v, asv[rb][r] * bsv[t], acc[rb][t][r]);
-          }
-        }
-      }
-    } else {
+    i32x4 sx[4];
+    if constexpr (W4 && HZ) {
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb)
+        sx[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+            av[rb], bitcast<i32x4>(u32x4{0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u}), izero, 0, 0, 0);
+    }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0);
+    for (int s = 0; s < NS; ++s) {
+      const uint8_t* sb = base + G::B_OFF + (s * 2 + kg) * G::B_BLK;
+      u32x4 bv[4];
+      if constexpr (W4) {
+        uint32_t lo[8], hi[8];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[rb][t][r] = fmaf((float)p[r], asv[rb][r], acc[rb][t][r]);
-        }
+        for (int i = 0; i < 8; ++i) w4_split_i8x16(*(const uint32_t*)(sb + (8 * g + i) * BN + cb), lo[i], hi[i]);
+        uint32_t e0[4], e1[4], o0[4], o1[4];
+        tr4(lo[0], lo[1], lo[2], lo[3], e0);
+        tr4(lo[4], lo[5], lo[6], lo[7], e1);
+        tr4(hi[0], hi[1], hi[2], hi[3], o0);
+        tr4(hi[4], hi[5], hi[6], hi[7], o1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bv[t] = u32x4{e0[t], e1[t], o0[t], o1[t]};
+        const f32x4 bsv = *(const f32x4*)(base + G::BS_OFF + (s * 256 + kg * BN + cb) * 4);
+        uint32_t zw = 0;
+        if constexpr (HZ) zw = *(const uint32_t*)(base + G::BZ_OFF + s * 256 + kg * BN + cb);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              int v = p[r] >> 4;  // exact: the MFMA summed 16 * (nibble - 8)
+              if constexpr (HZ) v += (8 - (int)((zw >> (8 * t)) & 0xFFu)) * sx[rb][r];
+              acc[s][rb][t][r] = fmaf((float)v, asv[rb][r] * bsv[t], acc[s][rb][t][r]);
+            }
+          }
+      } else {
+        uint32_t d[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d[i] = *(const uint32_t*)(sb + (16 * g + i) * BN + cb);
+        uint32_t x0[4], x1[4], x2[4], x3[4];
+        tr4(d[0], d[1], d[2], d[3], x0);
+        tr4(d[4], d[5], d[6], d[7], x1);
+        tr4(d[8], d[9], d[10], d[11], x2);
+        tr4(d[12], d[13], d[14], d[15], x3);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bv[t] = u32x4{x0[t], x1[t], x2[t], x3[t]};
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[s][rb][t][r] = fmaf((float)p[r], asv[rb][r], acc[s][rb][t][r]);
+          }
+      }
     }
   };
 
   // ---------------- K loop: stage st holds blocks 2st and 2st+1 ----------------
-  // Stage s is fetched into registers rg[s & 1] three iterations ahead, stored to LDS
-  // buffer s & 1 one iteration ahead (after the barrier that ended the last read of
-  // that buffer), and computed in iteration s: two iterations of compute cover the
-  // load latency.  The loop body is written for even and odd st so the register set
-  // indices are static.
+  // Stage s is stored to LDS buffer s & 1 one iteration ahead (after the barrier that
+  // ended the last read of that buffer) and computed in iteration s.  Its copy into
+  // registers is issued three iterations ahead with one weight set (two register
+  // sets, the loop written for even and odd st so their indices are static) and two
+  // iterations ahead with two (one register set: the gate/up accumulators need the
+  // registers).
   const int nst = (nk + 1) / 2;
-  Regs rg0, rg1;
-  fetch(rg0, 0);
-  store(rg0, 0);
-  if (nst > 1) fetch(rg1, 1);
-  if (nst > 2) fetch(rg0, 2);
-  __syncthreads();
-  // next: the registers holding stage st+1, stored now and refilled with stage st+3
-  auto iter = [&](int st, Regs& next) {
-    if (2 * st + kg < nk) compute(st & 1);
-    if (st + 1 < nst) store(next, (st + 1) & 1);
+  if constexpr (NS == 1) {
+    Regs rg0, rg1;
+    fetch(rg0, 0);
+    store(rg0, 0);
+    if (nst > 1) fetch(rg1, 1);
+    if (nst > 2) fetch(rg0, 2);
     __syncthreads();
-    if (st + 3 < nst) fetch(next, st + 3);
-  };
-  int st = 0;
-  for (; st + 1 < nst; st += 2) {
-    iter(st, rg1);
-    iter(st + 1, rg0);
+    // next: the registers holding stage st+1, stored now and refilled with stage st+3
+    auto iter = [&](int st, Regs& next) {
+      if (2 * st + kg < nk) compute(st & 1);
+      if (st + 1 < nst) store(next, (st + 1) & 1);
+      __syncthreads();
+      if (st + 3 < nst) fetch(next, st + 3);
+    };
+    int st = 0;
+    for (; st + 1 < nst; st += 2) {
+      iter(st, rg1);
+      iter(st + 1, rg0);
+    }
+    if (st < nst) iter(st, rg1);
+  } else {
+    Regs rg;
+    fetch(rg, 0);
+    store(rg, 0);
+    if (nst > 1) fetch(rg, 1);
+    __syncthreads();
+    for (int st = 0; st < nst; ++st) {
+      if (2 * st + kg < nk) compute(st & 1);
+      if (st + 1 < nst) store(rg, (st + 1) & 1);
+      __syncthreads();
+      if (st + 2 < nst) fetch(rg, st + 2);
+    }
   }
-  if (st < nst) iter(st, rg1);
 
-  // ---------------- K groups: group 0 + group 1 (fixed order) ----------------
+  // ---------------- K groups: group 0 + group 1 (fixed order), one set at a time ----------------
   float* red = (float*)lds + (wave & 3) * (64 * 64) + lane;
-  if (kg == 1) {
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    if (s > 0) __syncthreads();  // group 0 has read the previous set
+    if (kg == 1) {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[((rb * 4 + t) * 4 + r) * 64] = acc[s][rb][t][r];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[s][rb][t][r] += red[((rb * 4 + t) * 4 + r) * 64];
+    }
+  }
+  if (kg != 0) return;
+
+  // ---------------- epilogue ----------------
+  const int col = ncol0 + cb;  // within the matrix
+  if (col >= n) return;
+  float cs[NS][4];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) cs[s][t] = W4 ? 1.0f : load_scale(sset[s], a.sdt, col + t);
+  if constexpr (EPI == EPI_STORE) {
+    // column scale (W8), residual, 16-bit store
+    const int ocol = sg.col0 + col;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + rb * 16 + 4 * g + r;
+        if (row >= M) continue;
+        float y[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[((rb * 4 + t) * 4 + r) * 64] = acc[rb][t][r];
-  }
-  __syncthreads();
-  if (kg != 0) return;
+        for (int t = 0; t < 4; ++t) y[t] = acc[0][rb][t][r] * cs[0][t];
+        if (a.res) {
+          const u32x2 rv = *(const u32x2*)((const uint16_t*)a.res + (long long)row * a.ldr + ocol);
+          const uint16_t rh[4] = {(uint16_t)rv.x, (uint16_t)(rv.x >> 16), (uint16_t)rv.y, (uint16_t)(rv.y >> 16)};
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[rb][t][r] += red[((rb * 4 + t) * 4 + r) * 64];
-
-  // ---------------- epilogue: column scale (W8), residual, 16-bit store ----------------
-  const int col = ncol0 + cb;  // within the matrix
-  if (col >= n) return;
-  const int ocol = sg.col0 + col;
-  float cs[4] = {1.f, 1.f, 1.f, 1.f};
-  if constexpr (!W4) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) cs[t] = load_scale(sg.s, a.sdt, col + t);
-  }
-#pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + wm * 64 + rb * 16 + 4 * g + r;
-      if (row >= M) continue;
-      float y[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) y[t] = acc[rb][t][r] * cs[t];
-      if (a.res) {
-        const u32x2 rv = *(const u32x2*)((const uint16_t*)a.res + (long long)row * a.ldr + ocol);
-        const uint16_t rh[4] = {(uint16_t)rv.x, (uint16_t)(rv.x >> 16), (uint16_t)rv.y, (uint16_t)(rv.y >> 16)};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) y[t] += (a.odt == DT_BF16) ? bf16_to_f32(rh[t]) : (float)bitcast<_Float16>(rh[t]);
+          for (int t = 0; t < 4; ++t) y[t] += (a.odt == DT_BF16) ? bf16_to_f32(rh[t]) : (float)bitcast<_Float16>(rh[t]);
+        }
+        u32x2 o;
+        o.x = (uint32_t)to_out16(y[0], a.odt) | ((uint32_t)to_out16(y[1], a.odt) << 16);
+        o.y = (uint32_t)to_out16(y[2], a.odt) | ((uint32_t)to_out16(y[3], a.odt) << 16);
+        *(u32x2*)((uint16_t*)a.out + (long long)row * a.ldo + ocol) = o;
       }
-      u32x2 o;
-      o.x = (uint32_t)to_out16(y[0], a.odt) | ((uint32_t)to_out16(y[1], a.odt) << 16);
-      o.y = (uint32_t)to_out16(y[2], a.odt) | ((uint32_t)to_out16(y[3], a.odt) << 16);
-      *(u32x2*)((uint16_t*)a.out + (long long)row * a.ldo + ocol) = o;
-    }
+  } else {
+    // h = silu(g) * u; bf16 store, or bf16 round trip and per-64-column int8 quant.
+    // A row's 64 columns of this wave tile are the 16 lanes of its row group (4
+    // columns each): the amax reduces over those lanes.
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + rb * 16 + 4 * g + r;
+        float h[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) h[t] = silu(acc[0][rb][t][r] * cs[0][t]) * (acc[1][rb][t][r] * cs[1][t]);
+        if constexpr (EPI == EPI_GATEUP) {
+          if (row < M) {
+            u32x2 o;
+            o.x = (uint32_t)f32_to_bf16(h[0]) | ((uint32_t)f32_to_bf16(h[1]) << 16);
+            o.y = (uint32_t)f32_to_bf16(h[2]) | ((uint32_t)f32_to_bf16(h[3]) << 16);
+            *(u32x2*)((uint16_t*)a.out + (long long)row * a.ncols + col) = o;
+          }
+        } else {
+          float am = 0.0f;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            h[t] = bf16_to_f32(f32_to_bf16(h[t]));  // bf16 round trip (kernels/gemm.py:198-200)
+            am = fmaxf(am, fabsf(h[t]));
+          }
+#pragma unroll
+          for (int m = 1; m < 16; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
+          const float sc = fmaxf(am / 127.0f, 1e-8f);
+          if (row < M) {
+            uint32_t qw = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qw |= ((uint32_t)(round_i8(h[t] / sc) & 0xFF)) << (8 * t);
+            *(uint32_t*)(a.oq + (long long)row * a.ncols + col) = qw;
+            if (j == 0) a.os[(long long)row * (a.ncols / 64) + col / 64] = sc;
+          }
+        }
+      }
+  }
 }
 
-template <int WK, bool HZ>
+template <int WK, bool HZ, int EPI>
 static hipError_t launch_i8_t(const SkArgs& a, int tiles, hipStream_t st) {
-  using G = Gi8<WK>;
+  using G = Gi8<WK, (EPI == EPI_STORE) ? 1 : 2>;
   static bool attr_set = false;  // benign race: every caller sets the same value
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)prefill_i8_kernel<WK, HZ>,
+    const hipError_t e = hipFuncSetAttribute((const void*)prefill_i8_kernel<WK, HZ, EPI>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((prefill_i8_kernel<WK, HZ>), dim3(tiles), dim3(THREADS), (size_t)G::LDS, st, a);
+  hipLaunchKernelGGL((prefill_i8_kernel<WK, HZ, EPI>), dim3(tiles), dim3(THREADS), (size_t)G::LDS, st, a);
   return hipGetLastError();
 }
 
-bool prefill_i8_ok(const SkArgs& a, int wk) {
+template <int EPI>
+static hipError_t launch_i8_e(const SkArgs& a, int wk, bool hz, int tiles, hipStream_t st) {
+  if (wk == WK_W8) return launch_i8_t<WK_W8, false, EPI>(a, tiles, st);
+  if (hz) return launch_i8_t<WK_W4, true, EPI>(a, tiles, st);
+  return launch_i8_t<WK_W4, false, EPI>(a, tiles, st);
+}
+
+bool prefill_i8_ok(const SkArgs& a, int wk, int epi) {
   if (a.M <= 16 || a.K % 64 != 0 || ((uintptr_t)a.x & 15) != 0) return false;
   if (wk == WK_W4 && a.group < 64) return false;
-  for (int s = 0; s < a.nseg; ++s)
+  const int nsets = (epi == EPI_STORE) ? a.nseg : 1;  // gate/up: one column range, two weight sets
+  for (int s = 0; s < nsets; ++s)
     if (a.seg[s].n % BN != 0) return false;
   return true;
 }
 
-hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, hipStream_t st) {
+hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t st) {
   int tn = 0;
-  for (int s = 0; s < a.nseg; ++s) {
-    a.seg[s].tile0 = tn;
-    tn += a.seg[s].n / BN;
+  if (epi == EPI_STORE) {
+    for (int s = 0; s < a.nseg; ++s) {
+      a.seg[s].tile0 = tn;
+      tn += a.seg[s].n / BN;
+    }
+  } else {
+    a.seg[0].tile0 = a.seg[1].tile0 = 0;
+    tn = a.seg[0].n / BN;
   }
   a.ntiles = tn;
   const int tiles = ((a.M + BM - 1) / BM) * tn;
-  if (wk == WK_W8) return launch_i8_t<WK_W8, false>(a, tiles, st);
-  if (hz) return launch_i8_t<WK_W4, true>(a, tiles, st);
-  return launch_i8_t<WK_W4, false>(a, tiles, st);
+  switch (epi) {
+    case EPI_STORE: return launch_i8_e<EPI_STORE>(a, wk, hz, tiles, st);
+    case EPI_GATEUP: return launch_i8_e<EPI_GATEUP>(a, wk, hz, tiles, st);
+    default: return launch_i8_e<EPI_GATEUP_Q>(a, wk, hz, tiles, st);
+  }
 }
 
 }  // namespace qlin

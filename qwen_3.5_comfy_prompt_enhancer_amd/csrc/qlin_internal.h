@@ -55,11 +55,11 @@ hipError_t launch_skinny(const SkLaunch& L, const SkArgs& a, hipStream_t stream)
 hipError_t launch_skinny_f16(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
 hipError_t launch_skinny_i8w8(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
 hipError_t launch_skinny_i8w4(const SkLaunch& L, const SkArgs& a, hipStream_t stream);
-// Tiled int8-activation kernel for the engine-signature store epilogue with more than
-// 16 rows (prefill_i8.hip): whether it covers the call (K % 64 == 0, W4 groups of at
-// least 64, every segment a multiple of 128 columns), and its launch.
-bool prefill_i8_ok(const SkArgs& a, int wk);
-hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, hipStream_t stream);
+// Tiled int8-activation kernel for the engine-signature calls with more than 16 rows
+// (prefill_i8.hip), store and gate/up epilogues: whether it covers the call (K % 64
+// == 0, W4 groups of at least 64, every column range a multiple of 128), and its launch.
+bool prefill_i8_ok(const SkArgs& a, int wk, int epi);
+hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t stream);
 // whether a skinny variant runs with up to 8 waves per workgroup (else 4)
 bool skinny_big(int act, int wk, int epi, int cols);
 

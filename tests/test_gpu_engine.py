@@ -339,3 +339,29 @@ def test_engine_prefill_default_dispatch(M, K, N):
     cols = H.sample_cols(N, 512, seed=462)
     ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy()[:, cols], bs.numpy()[cols])
     H.assert_out_close(out.cpu()[:, cols], ref)
+
+
+@pytest.mark.parametrize("M", [17, 200])
+def test_mlp_gate_up_prefill_tiled(M, tiled):
+    """Fused gate/up (bf16 h) on the tiled int8 kernel, against the oracle."""
+    gemm, _ = _g()
+    K, N = 1024, 1280
+    a, as_ = H.engine_act(M, K, seed=470 + M)
+    wg, sg = H.engine_w8(K, N, seed=471)
+    wu, su = H.engine_w8(K, N, seed=472)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    gemm.mlp_gate_up(a.cuda(), as_.cuda(), wg.cuda(), sg.cuda(), wu.cuda(), su.cuda(), out)
+    ref = R.mlp_gate_up_ref(a.numpy(), as_.numpy(), wg.numpy(), sg.numpy(), wu.numpy(), su.numpy())
+    H.assert_out_close(out, ref)
+
+
+@pytest.mark.parametrize("M", [17, 200])
+def test_mlp_gate_up_quant_w8_prefill_tiled(M, tiled):
+    """mlp_gate_up_quant on the tiled kernel: bit-identical to quantizing its own
+    bf16 h, and within tolerance of the oracle."""
+    _fused_vs_unfused(M)
+
+
+@pytest.mark.parametrize("zeros,group", [("none", 128), ("random", 64)])
+def test_mlp_gate_up_quant_w4_prefill_tiled(zeros, group, tiled):
+    _fused_vs_unfused(96, w4_=True, zeros=zeros, group=group)
