@@ -310,3 +310,56 @@ def test_prefill_default_dispatch(M, K, N):
     cols = H.sample_cols(N, 512, seed=353)
     H.assert_out_close(_run_w8(x, w, s).cpu()[:, cols], H.linear_w8_ref_cols(x, w, s, cols))
     H.assert_out_close(_run_w4(x, packed, s4, z).cpu()[:, cols], H.linear_w4_ref_cols(x, packed, s4, z, cols))
+
+
+# ---------------------------------------------------------------- the configs at full size
+#
+# Config 3 (prefill, M = 2048) and config 4 (9B-class W4 chain shapes) at their real
+# sizes, checked against the oracle on sampled columns, plus a size-independent
+# property: scaling the activations by 2 scales every output by exactly 2 (fp32 sums
+# and the 16-bit rounding commute with a power of two when nothing overflows or
+# underflows), so the whole output is checked bit for bit, not only the sample.
+
+
+def _assert_doubled(y, y2):
+    """y2 == 2 * y bit for bit where y is a normal fp16 number above the smallest one;
+    where the sum v lies in the subnormal range (fixed spacing 2**-24, so also where
+    round(v) = 2**-14 exactly) rounding 2v and doubling round(v) may differ by one
+    step of 2**-24."""
+    a, b = y.float().cpu(), y2.float().cpu()
+    normal = a.abs() > 2.0 ** -14
+    assert torch.equal(b[normal], 2 * a[normal])
+    if (~normal).any():
+        assert float((b[~normal] - 2 * a[~normal]).abs().max()) <= 2.0 ** -24
+
+
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+@pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048), (2048, 2048)])
+def test_config3_prefill_full_size(kind, K, N):
+    M = 2048
+    x = H.act_f16(M, K, seed=500 + K)
+    cols = H.sample_cols(N, 256, seed=501)
+    if kind == "w8":
+        w, s = H.w8(K, N, seed=502)
+        y = _run_w8(x, w, s)
+        y2 = _run_w8((x * 2).to(torch.float16), w, s)
+        ref = H.linear_w8_ref_cols(x, w, s, cols)
+    else:
+        packed, s, z = H.w4(K, N, seed=502)
+        y = _run_w4(x, packed, s, z)
+        y2 = _run_w4((x * 2).to(torch.float16), packed, s, z)
+        ref = H.linear_w4_ref_cols(x, packed, s, z, cols)
+    H.assert_out_close(y.cpu()[:, cols], ref)
+    _assert_doubled(y, y2)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("K,N", [(4096, 12288), (12288, 4096), (4096, 4096), (4096, 1024), (4096, 248320)])
+def test_config4_chain_shapes_full_size(M, K, N):
+    x = H.act_f16(M, K, seed=510 + M)
+    packed, s, z = H.w4(K, N, seed=511 + K // 1024)
+    y = _run_w4(x, packed, s, z)
+    cols = H.sample_cols(N, 4096, seed=512)
+    H.assert_out_close(y.cpu()[:, cols], H.linear_w4_ref_cols(x, packed, s, z, cols))
+    y2 = _run_w4((x * 2).to(torch.float16), packed, s, z)
+    _assert_doubled(y, y2)

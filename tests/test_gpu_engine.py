@@ -365,3 +365,19 @@ def test_mlp_gate_up_quant_w8_prefill_tiled(M, tiled):
 @pytest.mark.parametrize("zeros,group", [("none", 128), ("random", 64)])
 def test_mlp_gate_up_quant_w4_prefill_tiled(zeros, group, tiled):
     _fused_vs_unfused(96, w4_=True, zeros=zeros, group=group)
+
+
+@pytest.mark.parametrize("M", [1, 4, 512])
+def test_engine_scale_property_full_size(M):
+    """Doubling the per-64 activation scales doubles every bf16 output exactly (the
+    int32 dots are unchanged and the fp32 fold and the rounding commute with 2), over
+    the whole 2048 x 6144 output at decode and prefill-chunk sizes."""
+    gemm, _ = _g()
+    K, N = 2048, 6144
+    a, as_ = H.engine_act(M, K, seed=490 + M)
+    b, bs = H.engine_w8(K, N, seed=491)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    y2 = torch.empty_like(y)
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y)
+    gemm.gemm_i8(a.cuda(), (as_ * 2).cuda(), b.cuda(), bs.cuda(), y2)
+    assert torch.equal(y2, (y.float() * 2).to(torch.bfloat16))
