@@ -237,25 +237,30 @@ void prefill_kernel(const TlArgs a) {
     }
   };
 
+  // B operand of MFMA column t (output column 4j + t) from the raw weight dwords
+  auto dequant = [&](const Ops& o, int t) -> f16x8 {
+    u32x4 h;
+    if constexpr (WK == WK_W8) {
+      h = u32x4{w8_pair_f16(o.d[0], o.d[1], t), w8_pair_f16(o.d[2], o.d[3], t), w8_pair_f16(o.d[4], o.d[5], t),
+                w8_pair_f16(o.d[6], o.d[7], t)};
+    } else {
+      const f16x2 bias = w4_bias((o.zv >> (8 * t)) & 0xFFu);
+      const _Float16 sc = scale_f16(o.sv[t], a.sdt);
+      const f16x2 s2 = f16x2{sc, sc};
+      h.x = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[0], t, bias)) * s2);
+      h.y = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[1], t, bias)) * s2);
+      h.z = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[2], t, bias)) * s2);
+      h.w = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[3], t, bias)) * s2);
+    }
+    return bitcast<f16x8>(h);
+  };
+
   // column-outer order: the dequantization of column t + 1 overlaps the 8 MFMAs of
   // column t
   auto mma = [&](const Ops& o) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      u32x4 h;
-      if constexpr (WK == WK_W8) {
-        h = u32x4{w8_pair_f16(o.d[0], o.d[1], t), w8_pair_f16(o.d[2], o.d[3], t), w8_pair_f16(o.d[4], o.d[5], t),
-                  w8_pair_f16(o.d[6], o.d[7], t)};
-      } else {
-        const f16x2 bias = w4_bias((o.zv >> (8 * t)) & 0xFFu);
-        const _Float16 sc = scale_f16(o.sv[t], a.sdt);
-        const f16x2 s2 = f16x2{sc, sc};
-        h.x = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[0], t, bias)) * s2);
-        h.y = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[1], t, bias)) * s2);
-        h.z = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[2], t, bias)) * s2);
-        h.w = bitcast<uint32_t>(bitcast<f16x2>(w4_pair_f16(o.d[3], t, bias)) * s2);
-      }
-      const f16x8 bv = bitcast<f16x8>(h);
+      const f16x8 bv = dequant(o, t);
 #pragma unroll
       for (int rb = 0; rb < 8; ++rb) acc[rb][t] = mfma_f16(o.av[rb], bv, acc[rb][t]);
     }
@@ -430,27 +435,55 @@ void prefill_kernel(const TlArgs a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) cs[t] = load_scale(a.s, a.sdt, colb + t);
   }
+  // The output type and the residual are uniform: branch once here, so each of the
+  // 128 values of a lane costs a multiply, a conversion and (with a residual) an add.
+  // Row addresses are a uniform base (the wave's first row) plus a per-lane offset
+  // computed once, plus a uniform multiple of the row stride.
+  const int r0 = m0 + wm * 128;       // first row of the wave
+  const int nrows = M - r0;           // rows of the wave below M (may exceed 128)
+  uint16_t* const obase = (uint16_t*)a.out + (long long)r0 * a.ldo;
+  const uint16_t* const rbase = a.res ? (const uint16_t*)a.res + (long long)r0 * a.ldr : nullptr;
+  const long long oofs = (long long)(4 * g) * a.ldo + colb, rofs = (long long)(4 * g) * a.ldr + colb;
+  auto store_all = [&](auto bf16, auto with_res) {
+    constexpr bool BF = decltype(bf16)::value, RES = decltype(with_res)::value;
+    // two values -> one dword of 16-bit outputs (fp16: one packed RNE conversion)
+    auto cvt2 = [](float v0, float v1) -> uint32_t {
+      if constexpr (BF) return (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
+      else return bitcast<uint32_t>(__builtin_convertvector((float __attribute__((ext_vector_type(2)))){v0, v1}, f16x2));
+    };
 #pragma unroll
-  for (int rb = 0; rb < 8; ++rb)
+    for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + wm * 128 + rb * 16 + 4 * g + r;
-      if (row >= M) continue;
-      float y[4];
+      for (int r = 0; r < 4; ++r) {
+        if (rb * 16 + 4 * g + r >= nrows) continue;
+        const int ur = rb * 16 + r;  // uniform part of the row
+        float y[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) y[t] = acc[rb][t][r] * cs[t];
-      if (a.res) {
-        const u32x2 rv = *(const u32x2*)((const uint16_t*)a.res + (long long)row * a.ldr + colb);
-        const uint16_t rh[4] = {(uint16_t)rv.x, (uint16_t)(rv.x >> 16), (uint16_t)rv.y, (uint16_t)(rv.y >> 16)};
+        for (int t = 0; t < 4; ++t) y[t] = acc[rb][t][r] * cs[t];
+        if constexpr (RES) {
+          const u32x2 rv = *(const u32x2*)(rbase + (long long)ur * a.ldr + rofs);
+          const uint32_t rw[2] = {rv.x, rv.y};
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          y[t] += (a.odt == DT_BF16) ? bf16_to_f32(rh[t]) : (float)bitcast<_Float16>(rh[t]);
+          for (int t = 0; t < 4; ++t) {
+            const uint16_t h = (uint16_t)(rw[t >> 1] >> (16 * (t & 1)));
+            y[t] += BF ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+          }
+        }
+        u32x2 o;
+        o.x = cvt2(y[0], y[1]);
+        o.y = cvt2(y[2], y[3]);
+        *(u32x2*)(obase + (long long)ur * a.ldo + oofs) = o;
       }
-      u32x2 o;
-      o.x = (uint32_t)to_out16(y[0], a.odt) | ((uint32_t)to_out16(y[1], a.odt) << 16);
-      o.y = (uint32_t)to_out16(y[2], a.odt) | ((uint32_t)to_out16(y[3], a.odt) << 16);
-      *(u32x2*)((uint16_t*)a.out + (long long)row * a.ldo + colb) = o;
-    }
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  if (a.odt == DT_BF16) {
+    if (a.res) store_all(T{}, T{});
+    else store_all(T{}, F{});
+  } else {
+    if (a.res) store_all(F{}, T{});
+    else store_all(F{}, F{});
+  }
 }
 
 template <int WK, bool HZ, int WM, int WN, int KG, int NS>

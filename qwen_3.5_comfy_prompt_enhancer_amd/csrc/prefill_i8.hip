@@ -361,28 +361,54 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) cs[s][t] = W4 ? 1.0f : load_scale(sset[s], a.sdt, col + t);
   if constexpr (EPI == EPI_STORE) {
-    // column scale (W8), residual, 16-bit store
+    // column scale (W8), residual, 16-bit store.  The output type and the residual
+    // are uniform: branch once, outside the per-value code.  Row addresses: uniform
+    // base of the wave's first row, per-lane offset, uniform multiple of the stride.
     const int ocol = sg.col0 + col;
+    const int r0 = m0 + wm * 64;
+    const int nrows = M - r0;
+    uint16_t* const obase = (uint16_t*)a.out + (long long)r0 * a.ldo;
+    const uint16_t* const rbase = a.res ? (const uint16_t*)a.res + (long long)r0 * a.ldr : nullptr;
+    const long long oofs = (long long)(4 * g) * a.ldo + ocol, rofs = (long long)(4 * g) * a.ldr + ocol;
+    auto store_all = [&](auto bf16, auto with_res) {
+      constexpr bool BF = decltype(bf16)::value, RES = decltype(with_res)::value;
+      auto cvt2 = [](float v0, float v1) -> uint32_t {
+        if constexpr (BF) return (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
+        else return bitcast<uint32_t>(__builtin_convertvector((float __attribute__((ext_vector_type(2)))){v0, v1}, f16x2));
+      };
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + rb * 16 + 4 * g + r;
-        if (row >= M) continue;
-        float y[4];
+        for (int r = 0; r < 4; ++r) {
+          if (rb * 16 + 4 * g + r >= nrows) continue;
+          const int ur = rb * 16 + r;
+          float y[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) y[t] = acc[0][rb][t][r] * cs[0][t];
-        if (a.res) {
-          const u32x2 rv = *(const u32x2*)((const uint16_t*)a.res + (long long)row * a.ldr + ocol);
-          const uint16_t rh[4] = {(uint16_t)rv.x, (uint16_t)(rv.x >> 16), (uint16_t)rv.y, (uint16_t)(rv.y >> 16)};
+          for (int t = 0; t < 4; ++t) y[t] = acc[0][rb][t][r] * cs[0][t];
+          if constexpr (RES) {
+            const u32x2 rv = *(const u32x2*)(rbase + (long long)ur * a.ldr + rofs);
+            const uint32_t rw[2] = {rv.x, rv.y};
 #pragma unroll
-          for (int t = 0; t < 4; ++t) y[t] += (a.odt == DT_BF16) ? bf16_to_f32(rh[t]) : (float)bitcast<_Float16>(rh[t]);
+            for (int t = 0; t < 4; ++t) {
+              const uint16_t hh = (uint16_t)(rw[t >> 1] >> (16 * (t & 1)));
+              y[t] += BF ? bf16_to_f32(hh) : (float)bitcast<_Float16>(hh);
+            }
+          }
+          u32x2 o;
+          o.x = cvt2(y[0], y[1]);
+          o.y = cvt2(y[2], y[3]);
+          *(u32x2*)(obase + (long long)ur * a.ldo + oofs) = o;
         }
-        u32x2 o;
-        o.x = (uint32_t)to_out16(y[0], a.odt) | ((uint32_t)to_out16(y[1], a.odt) << 16);
-        o.y = (uint32_t)to_out16(y[2], a.odt) | ((uint32_t)to_out16(y[3], a.odt) << 16);
-        *(u32x2*)((uint16_t*)a.out + (long long)row * a.ldo + ocol) = o;
-      }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (a.odt == DT_BF16) {
+      if (a.res) store_all(T{}, T{});
+      else store_all(T{}, F{});
+    } else {
+      if (a.res) store_all(F{}, T{});
+      else store_all(F{}, F{});
+    }
   } else {
     // h = silu(g) * u; bf16 store, or bf16 round trip and per-64-column int8 quant.
     // A row's 64 columns of this wave tile are the 16 lanes of its row group (4
