@@ -41,6 +41,9 @@ constexpr long long kTargetWavesW8 = 2048;
 constexpr long long kTargetWavesW4 = 1024;
 constexpr int kMinWaveKW8 = 64;
 constexpr int kMinWaveKW4 = 128;
+// largest one-pass tile (weight bytes per set; measured with the weights streaming
+// from HBM: 64 KB tiles win, 128 KB tiles lose to split-K)
+constexpr long long kOnePassTileBytes = 64 * 1024;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 bool dtype_scale_ok(int dt) { return dt == QLIN_F16 || dt == QLIN_BF16 || dt == QLIN_F32; }
@@ -64,9 +67,9 @@ void plan_override(const Problem& P, int& cols, int& waves, int& upw) {
   if (!e || !*e) return;
   int c = 0, w = 0, u = 0;
   if (sscanf(e, "%d,%d,%d", &c, &w, &u) != 3) return;
-  if (c == 8 || c == 16) cols = c;
-  if (P.epi != EPI_STORE) cols = 8;  // gate/up kernels exist with 8-column tiles only
-  if (w >= 1 && w <= 8) waves = w;  // clamped to the variant's maximum by the caller
+  if (c == 4 || c == 8 || c == 16) cols = c;
+  if (P.epi != EPI_STORE && cols == 16) cols = 8;  // gate/up kernels: 4- and 8-column tiles
+  if (w >= 1 && w <= 16) waves = w;  // clamped to the variant's maximum by the caller
   if (u >= 1) upw = u;
 }
 
@@ -123,8 +126,15 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   // LDS) and only then over workgroups.
   int cols = (wide && P.wk == WK_W4 && P.epi == EPI_STORE && P.M <= 16) ? 16 : 8;
   int waves = (wide && P.M <= 16) ? 1 : (wide ? 4 : (skinny_big(P.act, P.wk, P.epi, cols) ? 8 : 4)), upw = 0;
+  // Narrow launches whose whole-K 64-column tile of one weight set is small read it in
+  // one pass: 4-column lanes, K over the 8 waves of one workgroup, no split-K exchange
+  // (partial store, arrival counter and final read are three memory round trips).
+  // Larger tiles keep split-K: a CU moves only 16 bytes per cycle with 4-byte lanes.
+  const long long tile_bytes = (long long)P.K * 64 / (P.wk == WK_W4 ? 2 : 1);
+  if (!wide && tile_bytes <= kOnePassTileBytes) cols = 4, waves = 8;
   plan_override(P, cols, waves, upw);
-  const int maxw = skinny_big(P.act, P.wk, P.epi, cols) ? 8 : 4;
+  const bool one_pass = cols == 4;
+  const int maxw = one_pass ? 8 : (skinny_big(P.act, P.wk, P.epi, cols) ? 8 : 4);
   if (waves > maxw) waves = maxw;
   const int TN = 16 * cols;
   const int ntiles = count_tiles(TN);
@@ -136,7 +146,11 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   a.ntiles = ntiles;
 
   int splits;
-  if (wide) {
+  if (one_pass) {
+    if (waves > nunits) waves = nunits;
+    upw = (nunits + waves - 1) / waves;
+    splits = 1;
+  } else if (wide) {
     if (waves > nunits) waves = nunits;
     if (upw == 0) upw = (nunits + waves - 1) / waves;
     splits = (nunits + upw * waves - 1) / (upw * waves);

@@ -25,17 +25,20 @@ static bool force_ks_any() {
   return v;
 }
 
+// The K-loop fold structure of a launch.  fp16 activations fold once per W4 group:
+// statically every 4th step for group 128.  int8 activations fold per 64-wide
+// activation block (and W4 sub-block of min(group, 64)): every 2nd step unless the
+// W4 group is 32.
+static int fold_structure(int act, int wk, int group) {
+  if (act == ACT_F16) return (wk == WK_W4 && group == 128 && !force_ks_any()) ? KS_STEP4 : KS_ANY;
+  if (force_ks_any() && wk == WK_W4) return KS_ANY;
+  return (wk == WK_W8 || group >= 64) ? KS_STEP2 : KS_ANY;
+}
+
 hipError_t launch_skinny(const SkLaunch& L0, const SkArgs& a, hipStream_t st) {
   SkLaunch L = L0;
-  if (L.act == ACT_F16) {
-    // fp16 activations fold once per W4 group: statically every 4th step for group 128
-    L.ks = (L.wk == WK_W4 && a.group == 128 && !force_ks_any()) ? KS_STEP4 : KS_ANY;
-    return launch_skinny_f16(L, a, st);
-  }
-  // int8 activations fold per 64-wide activation block (and W4 sub-block of
-  // min(group, 64)): every 2nd step unless the W4 group is 32
-  L.ks = (L.wk == WK_W8 || a.group >= 64) ? KS_STEP2 : KS_ANY;
-  if (force_ks_any() && L.wk == WK_W4) L.ks = KS_ANY;
+  L.ks = fold_structure(L.act, L.wk, a.group);
+  if (L.act == ACT_F16) return launch_skinny_f16(L, a, st);
   return (L.wk == WK_W8) ? launch_skinny_i8w8(L, a, st) : launch_skinny_i8w4(L, a, st);
 }
 

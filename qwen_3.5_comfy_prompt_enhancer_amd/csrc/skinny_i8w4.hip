@@ -12,7 +12,13 @@ namespace qlin {
   QL_CASE(ACT_I8, WK_W4, false, EPI_GATEUP, 8, false, KSV)       \
   QL_CASE(ACT_I8, WK_W4, true, EPI_GATEUP, 8, false, KSV)        \
   QL_CASE(ACT_I8, WK_W4, false, EPI_GATEUP_Q, 8, false, KSV)     \
-  QL_CASE(ACT_I8, WK_W4, true, EPI_GATEUP_Q, 8, false, KSV)
+  QL_CASE(ACT_I8, WK_W4, true, EPI_GATEUP_Q, 8, false, KSV)     \
+  QL_CASE(ACT_I8, WK_W4, false, EPI_STORE, 4, false, KSV)        \
+  QL_CASE(ACT_I8, WK_W4, true, EPI_STORE, 4, false, KSV)         \
+  QL_CASE(ACT_I8, WK_W4, false, EPI_GATEUP, 4, false, KSV)       \
+  QL_CASE(ACT_I8, WK_W4, true, EPI_GATEUP, 4, false, KSV)        \
+  QL_CASE(ACT_I8, WK_W4, false, EPI_GATEUP_Q, 4, false, KSV)     \
+  QL_CASE(ACT_I8, WK_W4, true, EPI_GATEUP_Q, 4, false, KSV)
 
 hipError_t launch_skinny_i8w4(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
   QL_I8W4(KS_STEP2)

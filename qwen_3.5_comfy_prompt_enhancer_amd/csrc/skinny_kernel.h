@@ -54,10 +54,13 @@ __device__ __forceinline__ Row<COLS> ld_row(const uint8_t* p, bool valid) {
     r.d[1] = valid ? v.y : 0u;
     r.d[2] = valid ? v.z : 0u;
     r.d[3] = valid ? v.w : 0u;
-  } else {
+  } else if constexpr (COLS == 8) {
     const u32x2 v = *(const u32x2*)p;
     r.d[0] = valid ? v.x : 0u;
     r.d[1] = valid ? v.y : 0u;
+  } else {
+    const uint32_t v = *(const uint32_t*)p;
+    r.d[0] = valid ? v : 0u;
   }
   return r;
 }
@@ -73,6 +76,9 @@ __device__ __forceinline__ void ld_scales_raw(const void* p, int dt, long long i
     const u32x4* q = (const u32x4*)((const float*)p + idx);
 #pragma unroll
     for (int c = 0; c < COLS / 4; ++c) raw[c] = q[c];
+  } else if constexpr (COLS == 4) {
+    const u32x2 v = *(const u32x2*)((const uint16_t*)p + idx);
+    raw[0] = u32x4{v.x, v.y, 0u, 0u};
   } else {
     const u32x4* q = (const u32x4*)((const uint16_t*)p + idx);
 #pragma unroll
@@ -89,6 +95,13 @@ __device__ __forceinline__ void cvt_scales(const u32x4 raw[COLS / 4], int dt, fl
       out[4 * c + 1] = bitcast<float>(raw[c].y);
       out[4 * c + 2] = bitcast<float>(raw[c].z);
       out[4 * c + 3] = bitcast<float>(raw[c].w);
+    }
+  } else if constexpr (COLS == 4) {
+    const uint32_t w[2] = {raw[0].x, raw[0].y};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      out[e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
     }
   } else {
 #pragma unroll
@@ -107,6 +120,16 @@ __device__ __forceinline__ void cvt_scales(const u32x4 raw[COLS / 4], int dt, fl
 template <int COLS>
 __device__ __forceinline__ void ld_act16(const void* p, int dt, long long idx, float out[COLS]) {
   const uint16_t* q = (const uint16_t*)p + idx;
+  if constexpr (COLS == 4) {
+    const u32x2 v = *(const u32x2*)q;
+    const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      out[e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+    }
+    return;
+  }
 #pragma unroll
   for (int c = 0; c < COLS; c += 8) {
     const u32x4 v = *(const u32x4*)(q + c);
@@ -122,6 +145,13 @@ __device__ __forceinline__ void ld_act16(const void* p, int dt, long long idx, f
 template <int COLS>
 __device__ __forceinline__ void st_out16(void* p, int dt, long long idx, const float v[COLS]) {
   uint16_t* q = (uint16_t*)p + idx;
+  if constexpr (COLS == 4) {
+    u32x2 w;
+    w.x = (uint32_t)to_out16(v[0], dt) | ((uint32_t)to_out16(v[1], dt) << 16);
+    w.y = (uint32_t)to_out16(v[2], dt) | ((uint32_t)to_out16(v[3], dt) << 16);
+    *(u32x2*)q = w;
+    return;
+  }
 #pragma unroll
   for (int c = 0; c < COLS; c += 8) {
     u32x4 w;
@@ -142,8 +172,10 @@ __device__ __forceinline__ void st_i8(int8_t* p, const int q[COLS]) {
            ((uint32_t)(q[4 * c + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * c + 3] & 0xFF) << 24);
   if constexpr (COLS == 16) {
     *(u32x4*)p = u32x4{w[0], w[1], w[2], w[3]};
-  } else {
+  } else if constexpr (COLS == 8) {
     *(u32x2*)p = u32x2{w[0], w[1]};
+  } else {
+    *(uint32_t*)p = w[0];
   }
 }
 
@@ -221,6 +253,16 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int t = 0; t < COLS; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Per-column scales of the W8 epilogue, issued first so their latency overlaps the
+  // weight loads: a later workgroup barrier would otherwise wait for them.
+  u32x4 csraw[NS][COLS / 4];
+  if constexpr (WK == WK_W8) {
+    if (wave == 0) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) ld_scales_raw<COLS>(sp[s], a.sdt, ccl, csraw[s]);
+    }
+  }
 
   // ---------------- software-pipelined K loop ----------------
   // Every load of one 32-wide K step (weights, activations, the step's group scales,
@@ -457,15 +499,6 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
     });
   }
 
-  // Per-column scales of the W8 epilogue, issued now so their latency overlaps the
-  // reductions below.
-  u32x4 csraw[NS][COLS / 4];
-  if constexpr (WK == WK_W8) {
-    if (wave == 0) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) ld_scales_raw<COLS>(sp[s], a.sdt, ccl, csraw[s]);
-    }
-  }
 
   // ---------------- reduction over the waves of the workgroup (fixed order) ----------------
   // Every wave writes the row groups that hold real rows to its own LDS slot; all
@@ -657,18 +690,24 @@ hipError_t launch_v(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// BIG: the variant also exists with up to 8 waves per workgroup.
+// BIG: the variant also exists with up to 8 waves per workgroup.  COLS = 4: the
+// one-pass variants (K over up to 8 waves of one workgroup, no split).
 template <int ACT, int WK, bool HZ, int EPI, int COLS, bool BIG, int KS>
 hipError_t launch_t(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
-  if (L.waves > 4) {
-    if constexpr (BIG) {
-      if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 8, KS>(L, a, st);
-      return launch_v<ACT, WK, HZ, EPI, COLS, false, 8, KS>(L, a, st);
+  if constexpr (COLS == 4) {
+    if (a.splits > 1 || L.waves > 8) return hipErrorInvalidValue;
+    return launch_v<ACT, WK, HZ, EPI, 4, false, 8, KS>(L, a, st);
+  } else {
+    if (L.waves > 4) {
+      if constexpr (BIG) {
+        if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 8, KS>(L, a, st);
+        return launch_v<ACT, WK, HZ, EPI, COLS, false, 8, KS>(L, a, st);
+      }
+      return hipErrorInvalidValue;
     }
-    return hipErrorInvalidValue;
+    if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 4, KS>(L, a, st);
+    return launch_v<ACT, WK, HZ, EPI, COLS, false, 4, KS>(L, a, st);
   }
-  if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 4, KS>(L, a, st);
-  return launch_v<ACT, WK, HZ, EPI, COLS, false, 4, KS>(L, a, st);
 }
 
 #define QL_CASE(A, W, Z, E, C, B, KSV)                                                          \

@@ -181,18 +181,40 @@ def test_linear_residual_and_bf16_out():
     H.assert_out_close(y, ref)
 
 
-def test_rows_independent_of_batch():
-    """Row m of an M=4 call is bit-identical to the same row run alone (every
-    split choice depends on K and N only)."""
-    K, N = 2048, 6144
-    x = H.act_f16(4, K, seed=71)
+@pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
+def test_rows_independent_of_batch(K, N):
+    """Row m of an M=16 call is bit-identical to the same row run alone (every plan
+    choice depends on K and N only): one-pass tiles (K=2048) and split-K (K=6144)."""
+    x = H.act_f16(16, K, seed=71)
     w, s = H.w8(K, N, seed=72)
     packed, s4, _ = H.w4(K, N, seed=73)
     y = _run_w8(x, w, s)
     y4 = _run_w4(x, packed, s4, None)
-    for m in range(4):
+    for m in (0, 5, 15):
         assert torch.equal(_run_w8(x[m:m + 1], w, s)[0], y[m])
         assert torch.equal(_run_w4(x[m:m + 1], packed, s4, None)[0], y4[m])
+
+
+@pytest.mark.parametrize("plan", ["4,8,0", "8,8,0", "8,4,0", "16,4,0"])
+@pytest.mark.parametrize("K,N", [(2048, 2048), (6144, 1024)])
+def test_decode_forced_plans(plan, K, N, monkeypatch):
+    """Every decode plan family on the same shapes, whatever the default picks:
+    one-pass 64-column tiles (4 columns per lane), split-K over 128- and 256-column
+    tiles.  Oracle parity for W8 (+ residual) and W4 with zeros, M = 1, 4, 16, and
+    rows independent of M within the plan."""
+    monkeypatch.setenv("QLIN_SKINNY_PLAN", plan)
+    x = H.act_f16(16, K, seed=90)
+    w, s = H.w8(K, N, seed=91)
+    packed, s4, z = H.w4(K, N, seed=92, zeros="random")
+    res = torch.randn((16, N), generator=H.gen(93)).to(torch.float16)
+    for M in (1, 4, 16):
+        y = _run_w8(x[:M], w, s, residual=res[:M])
+        H.assert_out_close(y, H.linear_w8_ref_cols(x[:M], w, s, np.arange(N), residual=res[:M]))
+        y4 = _run_w4(x[:M], packed, s4, z)
+        H.assert_out_close(y4, H.linear_w4_ref_cols(x[:M], packed, s4, z, np.arange(N)))
+        if M == 16:
+            assert torch.equal(_run_w8(x[3:4], w, s, residual=res[3:4])[0], y[3])
+            assert torch.equal(_run_w4(x[3:4], packed, s4, z)[0], y4[3])
 
 
 def test_repeat_calls_are_deterministic():

@@ -192,6 +192,29 @@ def test_mlp_gate_up_quant_w4(M, zeros, group):
     _fused_vs_unfused(M, w4_=True, zeros=zeros, group=group)
 
 
+@pytest.mark.parametrize("plan", ["4,8,0", "8,4,0"])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_engine_decode_forced_plans(plan, M, monkeypatch):
+    """One-pass 64-column tiles and split-K 128-column tiles for every engine call
+    kind (store + residual, proj3, gate/up + quant; W8 and W4), whatever the
+    default plan is for the shape."""
+    monkeypatch.setenv("QLIN_SKINNY_PLAN", plan)
+    gemm, w4 = _g()
+    K, N = 2048, 2048
+    a, as_ = H.engine_act(M, K, seed=60 + M)
+    b, bs = H.engine_w8(K, N, seed=61)
+    res = torch.randn((M, N), generator=H.gen(62)).to(torch.bfloat16)
+    out = res.clone().cuda()
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out, residual=out)
+    H.assert_out_close(out, R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy(), bs.numpy(), residual=_bf16(res)))
+    packed, s4, z = _w4_engine(K, N, seed=63, zeros="random")
+    out4 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    w4.gemm_w4(a.cuda(), as_.cuda(), packed.cuda(), s4.cuda(), out4, b_z=z.cuda())
+    H.assert_out_close(out4, R.gemm_w4_ref(a.numpy(), as_.numpy(), packed.numpy(), H.np_(s4), z.numpy()))
+    _fused_vs_unfused(M)
+    _fused_vs_unfused(M, w4_=True, zeros="random")
+
+
 def test_engine_rows_independent_of_batch():
     gemm, _ = _g()
     K, N = 2048, 6144
