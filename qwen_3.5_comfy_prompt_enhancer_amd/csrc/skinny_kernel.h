@@ -68,8 +68,9 @@ __device__ __forceinline__ Row<COLS> ld_row(const uint8_t* p, bool valid) {
 __device__ __forceinline__ uint32_t byte_of(uint32_t d, int b) { return (d >> (8 * b)) & 0xFFu; }
 
 // Raw dwords of COLS consecutive scale values (COLS/4 vectors for fp32, COLS/8 for
-// 16-bit types); the conversion is deferred to cvt_scales so the load latency is not
-// waited on where it is issued.
+// 16-bit types, half a vector for 4 columns of 16-bit values); the conversion is
+// deferred to cvt_scales so the load latency is not waited on where it is issued.
+// The dtype branch is loop-invariant where this is used in a K loop.
 template <int COLS>
 __device__ __forceinline__ void ld_scales_raw(const void* p, int dt, long long idx, u32x4 raw[COLS / 4]) {
   if (dt == DT_F32) {
@@ -83,6 +84,24 @@ __device__ __forceinline__ void ld_scales_raw(const void* p, int dt, long long i
     const u32x4* q = (const u32x4*)((const uint16_t*)p + idx);
 #pragma unroll
     for (int c = 0; c < COLS / 8; ++c) raw[c] = q[c];
+  }
+}
+
+// The same without a branch, for loads issued ahead of a control-flow join: every
+// dtype issues the fp32 count of loads (16-bit types re-read their last vector), so
+// the compiler need not copy the results at the join and wait for them there.
+template <int COLS>
+__device__ __forceinline__ void ld_scales_raw_nb(const void* p, int dt, long long idx, u32x4 raw[COLS / 4]) {
+  const bool f32 = dt == DT_F32;
+  const uint8_t* base = (const uint8_t*)p + idx * (f32 ? 4 : 2);
+  if constexpr (COLS == 4) {
+    const u32x2 v0 = *(const u32x2*)base;
+    const u32x2 v1 = *(const u32x2*)(base + (f32 ? 8 : 0));
+    raw[0] = u32x4{v0.x, v0.y, v1.x, v1.y};
+  } else {
+    const int last16 = COLS / 8 - 1;  // last vector of 16-bit scales
+#pragma unroll
+    for (int c = 0; c < COLS / 4; ++c) raw[c] = *(const u32x4*)(base + 16 * (f32 ? c : min(c, last16)));
   }
 }
 
@@ -255,13 +274,13 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
     for (int t = 0; t < COLS; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Per-column scales of the W8 epilogue, issued first so their latency overlaps the
-  // weight loads: a later workgroup barrier would otherwise wait for them.
+  // weight loads (a later workgroup barrier would otherwise wait for them).  Every
+  // wave issues them, only wave 0 uses them: a branch here would make the compiler
+  // copy the results at the join and wait for the loads right away.
   u32x4 csraw[NS][COLS / 4];
   if constexpr (WK == WK_W8) {
-    if (wave == 0) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s) ld_scales_raw<COLS>(sp[s], a.sdt, ccl, csraw[s]);
-    }
+    for (int s = 0; s < NS; ++s) ld_scales_raw_nb<COLS>(sp[s], a.sdt, ccl, csraw[s]);
   }
 
   // ---------------- software-pipelined K loop ----------------
@@ -308,7 +327,10 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       for (int r = 0; r < NR; ++r) st.w[s][r] = ld_row<COLS>(base + (long long)r * n, true);
       if constexpr (W4) {
         const long long gi = (long long)(k / G) * n + ccl;
-        ld_scales_raw<COLS>(sp[s], a.sdt, gi, st.sraw[s]);
+        // measured: the fp16-activation loops run best with the dtype branch (the
+        // compiler unswitches them), the int8-activation ones without it
+        if constexpr (F16) ld_scales_raw<COLS>(sp[s], a.sdt, gi, st.sraw[s]);
+        else ld_scales_raw_nb<COLS>(sp[s], a.sdt, gi, st.sraw[s]);
         if constexpr (HZ) st.z[s] = ld_row<COLS>(zp[s] + gi, true);
       }
     }
