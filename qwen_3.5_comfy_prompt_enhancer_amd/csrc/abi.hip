@@ -196,12 +196,10 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   L.cols = cols;
   L.waves = waves;
   L.grid = dim3((unsigned)(ntiles * splits), (unsigned)rtiles, 1);
-  // LDS: the per-wave slots of the workgroup reduction (row groups holding real rows
-  // of the first row tile) and the tile buffer of the split-K reduction
+  // LDS: one finish-layout slot per wave ([set][row][column], rows of the first row
+  // tile rounded up to 4, row stride TN + 4 floats), then the tile's column scales
   const int rg0 = (((P.M < 16) ? P.M : 16) + 3) / 4;
-  const size_t lds_waves = (waves > 1) ? (size_t)waves * P.nsets * rg0 * cols * 64 * sizeof(float) : 0;
-  const size_t lds_split = (splits > 1) ? (size_t)P.nsets * cols * 1024 : 0;
-  L.lds = lds_waves > lds_split ? lds_waves : lds_split;
+  L.lds = ((size_t)waves * P.nsets * rg0 * 4 * (TN + 4) + (size_t)P.nsets * TN) * sizeof(float);
   if ((long long)ntiles * splits > 0x7FFFFFFFLL || rtiles > 65535)
     return fail(QLIN_ERR_UNSUPPORTED, "%s: grid too large (M=%d, N=%d)", fn, P.M, P.ncols);
   return hip_status(fn, launch_skinny(L, a, stream));

@@ -260,7 +260,6 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   const int cseg = (tile - sg0.tile0) * TN + j * COLS;  // first column (within the matrix)
   const bool cvalid = cseg < n;
   const int ccl = cvalid ? cseg : 0;                     // in-bounds column for addressing
-  const int ocol = sg0.col0 + cseg;                      // first output column
 
   const int arow = rt * 16 + j;  // activation row this lane feeds into the A operand
   const bool avalid = arow < M;
@@ -273,14 +272,31 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
 #pragma unroll
     for (int t = 0; t < COLS; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Per-column scales of the W8 epilogue, issued first so their latency overlaps the
-  // weight loads (a later workgroup barrier would otherwise wait for them).  Every
-  // wave issues them, only wave 0 uses them: a branch here would make the compiler
-  // copy the results at the join and wait for the loads right away.
-  u32x4 csraw[NS][COLS / 4];
-  if constexpr (WK == WK_W8) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) ld_scales_raw_nb<COLS>(sp[s], a.sdt, ccl, csraw[s]);
+  // ---------------- epilogue prefetch ----------------
+  // The finish runs from LDS on chunks of 8 output columns of one row, spread over
+  // every thread of the workgroup (item = pass * blockDim + thread).  What it reads
+  // from memory -- the tile's W8 column scales (staged into LDS before the finish) and
+  // the residual chunk of the first pass -- is loaded here, with clamped addresses and
+  // no branch (a dummy residual address when there is none): its latency then overlaps
+  // the weight loads, where a branch would make the compiler wait for it at the join.
+  const int tid = threadIdx.x;
+  const int Mt = min(16, M - rt * 16);        // rows of this row tile
+  const int R4 = ((Mt + 3) >> 2) * 4;          // rows of the finish layout
+  const int tcol0 = (tile - sg0.tile0) * TN;   // tile's first column within the matrix
+  constexpr int TNP = TN + 4;                  // padded row stride of the finish layout
+  constexpr int CPR = TN / 8;                  // 8-column chunks per row
+  constexpr int NSQ = NS * TN / 4;             // 4-column scale groups of the tile
+  const int sq = min(tid, NSQ - 1);
+  const int sq_s = sq / (TN / 4), sq_c = (sq % (TN / 4)) * 4;
+  u32x4 sraw4[1] = {u32x4{0u, 0u, 0u, 0u}};
+  if constexpr (WK == WK_W8) ld_scales_raw_nb<4>(sp[sq_s], a.sdt, min(tcol0 + sq_c, n - 4), sraw4);
+  u32x4 rpre = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (EPI == EPI_STORE) {
+    const int prow = min(tid / CPR, Mt - 1);
+    const int pcol = min(tcol0 + (tid % CPR) * 8, n - 8);
+    const uint16_t* rb = (const uint16_t*)(a.res ? a.res : a.out);
+    const long long rld = a.res ? a.ldr : a.ldo;
+    rpre = *(const u32x4*)(rb + (long long)(rt * 16 + prow) * rld + sg0.col0 + pcol);
   }
 
   // ---------------- software-pipelined K loop ----------------
@@ -522,89 +538,79 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   }
 
 
-  // ---------------- reduction over the waves of the workgroup (fixed order) ----------------
-  // Every wave writes the row groups that hold real rows to its own LDS slot; all
-  // threads then sum the slots in wave order (0, 1, ..., nw-1) and wave 0 takes the
-  // totals.  `red` holds nw slots of NS*RG*COLS*64 floats here and NS*COLS*256 floats
-  // in the split-K reduction below.
-  const int Mt = min(16, M - rt * 16);
-  const int RG = (Mt + 3) >> 2;  // row groups (of 4 MFMA rows) that hold real rows
-  if (nw > 1) {
-    const int per = NS * RG * COLS * 64;
-    if (g < RG) {
+  // ---------------- finish layout: workgroup sums in LDS ----------------
+  // Every wave writes its accumulators (the row groups that hold real rows) as
+  // [set][row][column] (row stride TNP) into its own slot; the slots are summed in wave
+  // order (0, 1, ..., nw-1) into slot 0.  The W8 column scales follow the slots as fp32
+  // [set][column].  `red` holds nw slots of NS*R4*TNP floats plus NS*TN floats.
+  const int per = NS * R4 * TNP;
+  float* const scl = red + nw * per;
+  if (g < R4 / 4) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int t = 0; t < COLS; ++t)
+      for (int t = 0; t < COLS; ++t)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            red[wave * per + (((s * RG + g) * COLS + t) * 4 + r) * 16 + j] = acc[s][t][r];
+        for (int r = 0; r < 4; ++r) red[wave * per + (s * R4 + 4 * g + r) * TNP + j * COLS + t] = acc[s][t][r];
+  }
+  if constexpr (WK == WK_W8) {
+    if (tid < NSQ) {
+      float c4[4];
+      cvt_scales<4>(sraw4, a.sdt, c4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) scl[sq_s * TN + sq_c + e] = c4[e];
     }
-    __syncthreads();
-    for (int e = threadIdx.x; e < per; e += blockDim.x) {
+  }
+  __syncthreads();
+  if (nw > 1) {
+    for (int e = tid; e < per; e += blockDim.x) {
       float v = red[e];
       for (int w = 1; w < nw; ++w) v += red[w * per + e];
       red[e] = v;
     }
     __syncthreads();
-    if (wave == 0 && g < RG) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int t = 0; t < COLS; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[s][t][r] = red[(((s * RG + g) * COLS + t) * 4 + r) * 16 + j];
-    }
-    if (SPLIT) __syncthreads();  // the split-K reduction below reuses `red`
   }
 
   // ---------------- reduction over workgroups (split-K) ----------------
   // Partials travel as 16-byte device-coherent (SC1) stores and loads, readable from
-  // every XCD without a whole-L2 writeback or invalidate.  Each workgroup waits until
-  // its partial stores have completed before it increments the tile's arrival
-  // counter; the workgroup that sees the final count reads every partial.
+  // every XCD without a whole-L2 writeback or invalidate.  Every thread stores its
+  // (set, row, 4-column) groups of the workgroup's sums and waits for its stores;
+  // after a barrier one thread increments the tile's arrival counter, and the
+  // workgroup that sees the final count sums every split's partial in split order
+  // (8 splits' loads in flight at a time) back into the finish layout.
   if constexpr (SPLIT) {
     __shared__ int s_last;
     const long long MN = (long long)M * a.ncols;
     const __amdgpu_buffer_rsrc_t rs = part_rsrc(a.part, (unsigned)((long long)a.splits * NS * MN * 4));
-    if (wave == 0) {
-      if (g < RG && cvalid) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int orow = rt * 16 + 4 * g + r;
-            if (orow < M) {
-              const unsigned off =
-                  (unsigned)((((long long)split * NS + s) * MN + (long long)orow * a.ncols + ocol) * 4);
-#pragma unroll
-              for (int q = 0; q < COLS / 4; ++q)
-                st_coherent(f32x4{acc[s][4 * q][r], acc[s][4 * q + 1][r], acc[s][4 * q + 2][r], acc[s][4 * q + 3][r]},
-                            rs, off + 16u * q);
-            }
-          }
+    constexpr int TN4 = TN / 4;
+    const int nel4 = NS * Mt * TN4;
+    const unsigned sstride = (unsigned)(NS * MN * 4);
+    for (int e = tid; e < nel4; e += blockDim.x) {
+      const int s = e / (Mt * TN4);
+      const int rem = e - s * (Mt * TN4);
+      const int row = rem / TN4;
+      const int col = (rem - row * TN4) * 4;
+      if (tcol0 + col < n) {
+        const unsigned off = (unsigned)((((long long)split * NS + s) * MN + (long long)(rt * 16 + row) * a.ncols +
+                                         sg0.col0 + tcol0 + col) * 4);
+        st_coherent(*(const f32x4*)&red[(s * R4 + row) * TNP + col], rs, off);
       }
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // every partial store of this thread has completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) {
       unsigned* cp = a.cnt + (long long)rt * a.ntiles + tile;
-      if (lane == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = prev == (unsigned)(a.splits - 1);
-        if (last) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-      }
+      const unsigned prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev == (unsigned)(a.splits - 1);
+      if (last) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
     }
     __syncthreads();
     if (!s_last) return;  // uniform over the workgroup
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    // The last workgroup sums the tile's partials in split order, every thread on
-    // its own (set, row, 4-column) groups, into red[s][row][col].
-    const int tcol0 = (tile - sg0.tile0) * TN;  // tile's first column within the matrix
-    constexpr int TN4 = TN / 4;
-    const int nel4 = NS * Mt * TN4;
-    const unsigned sstride = (unsigned)(NS * MN * 4);
-    for (int e = threadIdx.x; e < nel4; e += blockDim.x) {
+    for (int e = tid; e < nel4; e += blockDim.x) {
       const int s = e / (Mt * TN4);
       const int rem = e - s * (Mt * TN4);
       const int row = rem / TN4;
@@ -613,83 +619,79 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       if (tcol0 + col < n) {
         const unsigned off =
             (unsigned)(((long long)s * MN + (long long)(rt * 16 + row) * a.ncols + sg0.col0 + tcol0 + col) * 4);
-        v = ld_coherent(rs, off);
-#pragma unroll 8
-        for (int p = 1; p < a.splits; ++p) v += ld_coherent(rs, off + (unsigned)p * sstride);
+        for (int p0 = 0; p0 < a.splits; p0 += 8) {
+          f32x4 part[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) part[q] = ld_coherent(rs, off + (unsigned)min(p0 + q, a.splits - 1) * sstride);
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (p0 + q < a.splits) v = (p0 + q == 0) ? part[q] : v + part[q];
+        }
       }
-      *(f32x4*)&red[(s * 16 + row) * TN + col] = v;
+      *(f32x4*)&red[(s * R4 + row) * TNP + col] = v;
     }
     __syncthreads();
-    if (wave == 0 && g < RG) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int t = 0; t < COLS; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = 4 * g + r;
-            acc[s][t][r] = row < Mt ? red[(s * 16 + row) * TN + j * COLS + t] : 0.0f;
-          }
-    }
   }
-  if (wave != 0) return;
 
-  // ---------------- epilogue ----------------
-  if (g >= RG) return;
-  if constexpr (EPI == EPI_STORE) {
-    if (!cvalid) return;
-    float cs[COLS];
-    if constexpr (WK == WK_W8) cvt_scales<COLS>(csraw[0], a.sdt, cs);
+  // ---------------- epilogue: every thread, 8-column chunks of one row ----------------
+  // The pass count is uniform, so every lane of a wave reaches the amax shuffles;
+  // items past the tile compute on clamped rows and store nothing.
+  const int nitems = Mt * CPR;
+  for (int base = 0; base < nitems; base += blockDim.x) {
+    const int it = base + tid;
+    const int row = min(it / CPR, Mt - 1);
+    const int c = (it % CPR) * 8;                // chunk's first column within the tile
+    const bool cval = it < nitems && tcol0 + c < n;
+    const int orow = rt * 16 + row;
+    const long long oc = (long long)sg0.col0 + tcol0 + c;  // first output column
+    float v[NS][8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int orow = rt * 16 + 4 * g + r;
-      if (orow >= M) break;
-      float y[COLS];
+    for (int s = 0; s < NS; ++s) {
+      const f32x4 lo = *(const f32x4*)&red[(s * R4 + row) * TNP + c];
+      const f32x4 hi = *(const f32x4*)&red[(s * R4 + row) * TNP + c + 4];
 #pragma unroll
-      for (int t = 0; t < COLS; ++t) y[t] = (WK == WK_W8) ? acc[0][t][r] * cs[t] : acc[0][t][r];
+      for (int e = 0; e < 4; ++e) v[s][e] = lo[e], v[s][4 + e] = hi[e];
+      if constexpr (WK == WK_W8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[s][e] *= scl[s * TN + c + e];
+      }
+    }
+    if constexpr (EPI == EPI_STORE) {
       if (a.res != nullptr) {
-        float rv[COLS];
-        ld_act16<COLS>(a.res, a.odt, (long long)orow * a.ldr + ocol, rv);
+        const u32x4 rr = (base == 0) ? rpre : *(const u32x4*)((const uint16_t*)a.res + (long long)orow * a.ldr + oc);
+        const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
 #pragma unroll
-        for (int t = 0; t < COLS; ++t) y[t] += rv[t];
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t h = (uint16_t)(rw[e >> 1] >> (16 * (e & 1)));
+          v[0][e] += (a.odt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+        }
       }
-      st_out16<COLS>(a.out, a.odt, (long long)orow * a.ldo + ocol, y);
-    }
-  } else {
-    float cg[COLS], cu[COLS];
-    if constexpr (WK == WK_W8) {
-      cvt_scales<COLS>(csraw[0], a.sdt, cg);
-      cvt_scales<COLS>(csraw[1], a.sdt, cu);
-    }
+      if (cval) st_out16<8>(a.out, a.odt, (long long)orow * a.ldo + oc, v[0]);
+    } else {
+      float h[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int orow = rt * 16 + 4 * g + r;
-      if (orow >= M) break;  // uniform over the 16 lanes of a row group
-      float h[COLS];
-#pragma unroll
-      for (int t = 0; t < COLS; ++t) {
-        const float gv = (WK == WK_W8) ? acc[0][t][r] * cg[t] : acc[0][t][r];
-        const float uv = (WK == WK_W8) ? acc[1][t][r] * cu[t] : acc[1][t][r];
-        h[t] = silu(gv) * uv;
-      }
+      for (int e = 0; e < 8; ++e) h[e] = silu(v[0][e]) * v[1][e];
       if constexpr (EPI == EPI_GATEUP) {
-        if (cvalid) st_out16<COLS>(a.out, DT_BF16, (long long)orow * a.ncols + ocol, h);
+        if (cval) st_out16<8>(a.out, DT_BF16, (long long)orow * a.ncols + oc, h);
       } else {
+        // bf16 round trip (kernels/gemm.py:198-200), then the amax of the 64-column
+        // group over its 8 chunks (8 consecutive lanes)
         float am = 0.0f;
 #pragma unroll
-        for (int t = 0; t < COLS; ++t) {
-          h[t] = bf16_to_f32(f32_to_bf16(h[t]));  // bf16 round trip (kernels/gemm.py:198-200)
-          am = fmaxf(am, fabsf(h[t]));
+        for (int e = 0; e < 8; ++e) {
+          h[e] = bf16_to_f32(f32_to_bf16(h[e]));
+          am = fmaxf(am, fabsf(h[e]));
         }
+        if (!cval) am = 0.0f;
 #pragma unroll
-        for (int m = 1; m < 64 / COLS; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
+        for (int m = 1; m < 8; m <<= 1) am = fmaxf(am, __shfl_xor(am, m));
         const float sc = fmaxf(am / 127.0f, 1e-8f);
-        int q[COLS];
+        int q[8];
 #pragma unroll
-        for (int t = 0; t < COLS; ++t) q[t] = round_i8(h[t] / sc);
-        if (cvalid) {
-          st_i8<COLS>(a.oq + (long long)orow * a.ncols + ocol, q);
-          if ((j & (64 / COLS - 1)) == 0) a.os[(long long)orow * (a.ncols / 64) + ocol / 64] = sc;
+        for (int e = 0; e < 8; ++e) q[e] = round_i8(h[e] / sc);
+        if (cval) {
+          st_i8<8>(a.oq + (long long)orow * a.ncols + oc, q);
+          if ((c & 63) == 0) a.os[(long long)orow * (a.ncols / 64) + oc / 64] = sc;
         }
       }
     }
@@ -699,11 +701,17 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
 template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW, int KS>
 hipError_t launch_v(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
   auto* k = skinny_kernel<ACT, WK, HZ, EPI, COLS, SPLIT, MAXW, KS>;
-  if (L.lds > 65536) {
+  // Largest dynamic LDS of this variant (MAXW finish slots of 16 rows, the column
+  // scales); the kernel's static LDS comes on top, so the limit is raised to exactly
+  // this, not to the whole 160 KB.
+  constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;
+  constexpr size_t kMaxLds = ((size_t)MAXW * NS * 16 * (16 * COLS + 4) + (size_t)NS * 16 * COLS) * sizeof(float);
+  if (L.lds > kMaxLds) return hipErrorInvalidValue;
+  if constexpr (kMaxLds > 65536) {
     static bool attr_set = false;  // benign race: every caller sets the same value
     if (!attr_set) {
-      const hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               160 * 1024);
+      const hipError_t e =
+          hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
       if (e != hipSuccess) return e;
       attr_set = true;
     }
