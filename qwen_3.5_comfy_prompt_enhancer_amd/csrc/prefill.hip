@@ -207,6 +207,11 @@ void prefill_kernel(const TlArgs a) {
     uint32_t zv;
   };
   const int cc = wn * 64 + 4 * j;  // first of this lane's 4 columns within the tile
+  // W8 column scales of the epilogue, loaded now (every wave, no branch) so their
+  // latency hides behind the K loop; issued before the first copy, they only make
+  // the first copy wait count cover one more (older) load
+  u32x4 csraw = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (WK == WK_W8) csraw = ld_scale4_raw(a.s, a.sdt, min(n0 + cc, N - 4));
   const int cb = (wn >> 1) * G::HB_BLOCKS * WBLK + (wn & 1) * 64 + 4 * j;  // its byte in a weight half
 
   auto load_ops = [&](int st, int ks, Ops& o) {
@@ -431,10 +436,7 @@ void prefill_kernel(const TlArgs a) {
   const int colb = n0 + wn * 64 + 4 * j;
   if (kg != 0 || colb >= N) return;
   float cs[4] = {1.f, 1.f, 1.f, 1.f};
-  if constexpr (WK == WK_W8) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) cs[t] = load_scale(a.s, a.sdt, colb + t);
-  }
+  if constexpr (WK == WK_W8) cvt_scale4(csraw, a.sdt, cs);
   // The output type and the residual are uniform: branch once here, so each of the
   // 128 values of a lane costs a multiply, a conversion and (with a residual) an add.
   // Row addresses are a uniform base (the wave's first row) plus a per-lane offset

@@ -115,7 +115,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
     u32x4 av[2];
     u32x4 bv[NS][W4 ? 1 : 2];
     float as_;
-    float bs;     // W4: one group scale of set tid / 256
+    uint32_t bs;  // W4: raw dword of one group scale of set tid / 256
     uint32_t bz;  // W4 with zeros: the matching zero
   };
   auto fetch = [&](Regs& rg, int st) {
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
         const int t2 = tid & 255, k2 = t2 >> 7, c = t2 & 127;
         const int blk = min(2 * st + k2, nk - 1);
         const long long gi = (long long)(blk * 64 / a.group) * n + ncol0 + c;
-        rg.bs = load_scale(sset[s], a.sdt, gi);
+        rg.bs = ld_scale1_raw(sset[s], a.sdt, gi);  // converted at the LDS store
         if constexpr (HZ) rg.bz = zset[s][gi];
       }
     }
@@ -187,7 +187,8 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
     if (tid < 256) ((float*)(base + G::AS_OFF))[tid] = rg.as_;
     if constexpr (W4) {
       if ((tid >> 8) < NS) {
-        ((float*)(base + G::BS_OFF))[tid] = rg.bs;
+        // gi of the fetch has the parity of tid (n and ncol0 are even)
+        ((float*)(base + G::BS_OFF))[tid] = cvt_scale1(rg.bs, a.sdt, tid);
         if constexpr (HZ) base[G::BZ_OFF + tid] = (uint8_t)rg.bz;
       }
     }
@@ -203,6 +204,12 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
 
   const i32x4 izero = i32x4{0, 0, 0, 0};
   const int cb = wn * 64 + 4 * j;  // lane's first column within the tile
+  // W8 column scales of the epilogue, loaded now (no branch) so their latency hides
+  // behind the K loop
+  u32x4 csraw[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    csraw[s] = W4 ? u32x4{0u, 0u, 0u, 0u} : ld_scale4_raw(sset[s], a.sdt, min(ncol0 + cb, n - 4));
 
   // one 64-wide block of this wave's K group from LDS stage `buf`
   auto compute = [&](int buf) {
@@ -357,9 +364,13 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   if (col >= n) return;
   float cs[NS][4];
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) cs[s][t] = W4 ? 1.0f : load_scale(sset[s], a.sdt, col + t);
+  for (int s = 0; s < NS; ++s) {
+    if constexpr (W4) {
+      cs[s][0] = cs[s][1] = cs[s][2] = cs[s][3] = 1.0f;
+    } else {
+      cvt_scale4(csraw[s], a.sdt, cs[s]);
+    }
+  }
   if constexpr (EPI == EPI_STORE) {
     // column scale (W8), residual, 16-bit store.  The output type and the residual
     // are uniform: branch once, outside the per-value code.  Row addresses: uniform

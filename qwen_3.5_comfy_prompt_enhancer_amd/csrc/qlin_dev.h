@@ -179,6 +179,45 @@ __device__ __forceinline__ float load_scale(const void* p, int dt, long long i) 
   return (float)((const _Float16*)p)[i];
 }
 
+// Raw bits of 4 consecutive scale values (fp32: 16 bytes; 16-bit types: 8 bytes,
+// read twice), loaded without a branch on the dtype: a load issued early and merged
+// at a control-flow join is waited for at the join.  idx must be a multiple of 4.
+__device__ __forceinline__ u32x4 ld_scale4_raw(const void* p, int dt, long long idx) {
+  const bool f32 = dt == DT_F32;
+  const uint8_t* base = (const uint8_t*)p + idx * (f32 ? 4 : 2);
+  const u32x2 v0 = *(const u32x2*)base;
+  const u32x2 v1 = *(const u32x2*)(base + (f32 ? 8 : 0));
+  return u32x4{v0.x, v0.y, v1.x, v1.y};
+}
+
+__device__ __forceinline__ void cvt_scale4(const u32x4 raw, int dt, float out[4]) {
+  if (dt == DT_F32) {
+    out[0] = bitcast<float>(raw.x), out[1] = bitcast<float>(raw.y);
+    out[2] = bitcast<float>(raw.z), out[3] = bitcast<float>(raw.w);
+    return;
+  }
+  const uint32_t w[2] = {raw.x, raw.y};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+    out[e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+  }
+}
+
+// One scale value as raw bits, loaded without a branch on the dtype: the aligned
+// dword holding element idx (for 16-bit types it also holds the neighbour).
+__device__ __forceinline__ uint32_t ld_scale1_raw(const void* p, int dt, long long idx) {
+  const long long byte = (dt == DT_F32) ? idx * 4 : ((idx * 2) & ~3LL);
+  return *(const uint32_t*)((const uint8_t*)p + byte);
+}
+
+// The value of ld_scale1_raw's dword for element idx (only idx's parity is used).
+__device__ __forceinline__ float cvt_scale1(uint32_t raw, int dt, long long idx) {
+  if (dt == DT_F32) return bitcast<float>(raw);
+  const uint16_t h = (uint16_t)(raw >> (16 * (int)(idx & 1)));
+  return (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+}
+
 __device__ __forceinline__ float load_act16(const void* p, int dt, long long i) {
   if (dt == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
   return (float)((const _Float16*)p)[i];
