@@ -563,9 +563,16 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   }
   __syncthreads();
   if (nw > 1) {
+    // every slot's value is read before the first add (a loop over the run-time wave
+    // count would wait out one LDS latency per wave); slots past nw re-read the last
     for (int e = tid; e < per; e += blockDim.x) {
-      float v = red[e];
-      for (int w = 1; w < nw; ++w) v += red[w * per + e];
+      float p[MAXW];
+#pragma unroll
+      for (int w = 0; w < MAXW; ++w) p[w] = red[min(w, nw - 1) * per + e];
+      float v = p[0];
+#pragma unroll
+      for (int w = 1; w < MAXW; ++w)
+        if (w < nw) v += p[w];
       red[e] = v;
     }
     __syncthreads();
