@@ -302,8 +302,7 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   // ---------------- software-pipelined K loop ----------------
   // Every load of one 32-wide K step (weights, activations, the step's group scales,
   // zeros and activation scales) goes into slot d of a D-deep register ring and is
-  // issued D steps ahead, unconditionally (the step index is clamped to the wave's
-  // last step), so the loop body is straight-line and D steps of HBM latency overlap.
+  // issued D steps ahead, so D steps of HBM latency overlap.
   // Lanes past N or M read clamped in-bounds addresses; their MFMA columns / rows
   // are never stored.
   constexpr int D = (NS == 2) ? 2 : 4;
@@ -358,32 +357,77 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   // of its K granule (64 for int8 activations, whole W4 groups), so the group and
   // activation-block ends that are multiples of 4 steps apart are known statically
   // and the accumulators stay in place across steps.
+  // fp16-activation W8 waves load no step twice: a wave64 memory instruction costs its
+  // CU about 16 cycles of address processing, and the decode split-K waves are 2-4
+  // steps long, so loads re-issued for a clamped step index (the pipeline's last D)
+  // doubled the issue time before the first weights could arrive.  Long ranges run a
+  // straight-line main loop (every load valid); the last steps, and short ranges, test
+  // each load.  The other variants keep the clamped, branch-free form (measured
+  // faster for them: their waves are longer and hold more registers).
   constexpr int U = 4;
+  constexpr bool kExactLoads = F16 && !W4;
   auto run_pipeline = [&](auto&& compute) {
     if (nsteps <= 0) return;
+    if constexpr (kExactLoads) {
+      // steps [base0, nsteps): fewer than U + D, in at most two static chunks of U
+      auto tail = [&](int base0) {
+        static_for<0, 2>([&](auto cc) {
+          constexpr int c = decltype(cc)::value;
+          static_for<0, U>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            const int i = base0 + c * U + u;
+            if (i < nsteps) {
+              compute(buf[u % D], kb + 32 * i, uc);
+              if (i + D < nsteps) load_step(buf[u % D], kb + 32 * (i + D));
+            }
+          });
+        });
+      };
+      int base0 = 0;
+      if (nsteps >= U + D) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_step(buf[d], kb + 32 * (d < nsteps ? d : nsteps - 1));
-    const int nfull = nsteps - nsteps % U;
-    for (int base = 0; base < nfull; base += U) {
-      static_for<0, U>([&](auto uc) {
-        constexpr int u = decltype(uc)::value;
-        const int i = base + u;
-        compute(buf[u % D], kb + 32 * i, uc);
-        const int nx = i + D < nsteps ? i + D : nsteps - 1;
-        load_step(buf[u % D], kb + 32 * nx);
-      });
-    }
-    static_for<0, U - 1>([&](auto uc) {
-      constexpr int u = decltype(uc)::value;
-      const int i = nfull + u;
-      if (i < nsteps) {
-        compute(buf[u % D], kb + 32 * i, uc);
-        if constexpr (U > D) {
+        for (int d = 0; d < D; ++d) load_step(buf[d], kb + 32 * d);
+        base0 = ((nsteps - U - D) / U + 1) * U;  // chunks whose loads are all in range
+        for (int base = 0; base < base0; base += U) {
+          static_for<0, U>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            const int i = base + u;
+            compute(buf[u % D], kb + 32 * i, uc);
+            load_step(buf[u % D], kb + 32 * (i + D));
+          });
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+          if (d < nsteps) load_step(buf[d], kb + 32 * d);
+      }
+      tail(base0);
+    } else {
+      // every load issued unconditionally, the step index clamped to the last step
+#pragma unroll
+      for (int d = 0; d < D; ++d) load_step(buf[d], kb + 32 * (d < nsteps ? d : nsteps - 1));
+      const int nfull = nsteps - nsteps % U;
+      for (int base = 0; base < nfull; base += U) {
+        static_for<0, U>([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          const int i = base + u;
+          compute(buf[u % D], kb + 32 * i, uc);
           const int nx = i + D < nsteps ? i + D : nsteps - 1;
           load_step(buf[u % D], kb + 32 * nx);
-        }
+        });
       }
-    });
+      static_for<0, U - 1>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        const int i = nfull + u;
+        if (i < nsteps) {
+          compute(buf[u % D], kb + 32 * i, uc);
+          if constexpr (U > D) {
+            const int nx = i + D < nsteps ? i + D : nsteps - 1;
+            load_step(buf[u % D], kb + 32 * nx);
+          }
+        }
+      });
+    }
   };
 
   if constexpr (F16) {
