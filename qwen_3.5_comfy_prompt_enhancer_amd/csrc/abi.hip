@@ -40,6 +40,10 @@ constexpr int kWideTiles = 512;          // 256-column tiles at which no K split
 constexpr long long kTargetWavesW8 = 2048;
 constexpr long long kTargetWavesW4 = 1024;
 constexpr int kMinWaveKW8 = 64;
+// fp16-activation W8 launches of at most this many (column tile x 32-row) units run
+// one 32-row step per wave (measured: 2048x2048 and 2048x512 gain 0.4-0.9 us per
+// launch; larger launches lose with that many workgroups)
+constexpr long long kOneStepUnits = 1024;
 constexpr int kMinWaveKW4 = 128;
 // largest one-pass tile (weight bytes per set; measured with the weights streaming
 // from HBM: 64 KB tiles win, 128 KB tiles lose to split-K)
@@ -158,7 +162,8 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   } else {
     // narrow N: spread K over up to kTargetWaves waves, each at least kMinWaveK deep
     const long long target = (P.wk == WK_W4) ? kTargetWavesW4 : kTargetWavesW8;
-    const int min_k = (P.wk == WK_W4) ? kMinWaveKW4 : kMinWaveKW8;
+    int min_k = (P.wk == WK_W4) ? kMinWaveKW4 : kMinWaveKW8;
+    if (P.act == ACT_F16 && P.wk == WK_W8 && (long long)ntiles * nunits <= kOneStepUnits) min_k = 32;
     const int min_upw = (min_k + kalign - 1) / kalign;
     if (upw == 0) {
       upw = (int)(((long long)ntiles * nunits + target - 1) / target);
