@@ -19,8 +19,9 @@
 //   * MFMA: v_mfma_i32_16x16x64_i8, one instruction per 64-wide block, started from
 //     an inline zero.  Lane (g, j) holds K bytes 16g..16g+15 of activation row j and
 //     of weight column 4j + t for instruction t.  Weight bytes are N-contiguous in
-//     LDS (as in HBM); each lane reads 4 adjacent columns of its 16 K rows (one dword
-//     per row) and 4x4 byte transposes turn them into the 4 B operands.  W4: the
+//     LDS (as in HBM, rows padded per lane group); each lane reads 4 adjacent columns
+//     of its 16 K rows (one dword per row) and 4x4 byte transposes turn them into the
+//     4 B operands.  W4: the
 //     nibbles become int8 16 * (n - 8) (even K then odd K), the activation operand
 //     is permuted to the same order, and the dot is shifted right by 4 (exact);
 //     explicit zeros add (8 - z) * sum(a) from one more MFMA against all-ones.
@@ -45,7 +46,14 @@ struct Gi8 {
   static constexpr bool W4 = WK == WK_W4;
   static constexpr int A_BLK = BM * 64;                 // activation bytes of one block
   static constexpr int B_ROWS = W4 ? 32 : 64;           // weight rows of one block
-  static constexpr int B_BLK = B_ROWS * BN;             // weight bytes of one block of one set
+  // Weight rows are N-contiguous (128 bytes), with 64 bytes of padding after every
+  // group of RG rows, RG = the rows of one MFMA lane group (16 int8, 8 packed).  The
+  // four lane groups of a ds_read_b32 then start 16 dwords apart modulo the 64 banks
+  // and read without bank conflicts (unpadded they all hit the same 16 banks).
+  static constexpr int RG = W4 ? 8 : 16;
+  static constexpr int B_PAD = 64;
+  static constexpr int B_BLK = B_ROWS * BN + (B_ROWS / RG) * B_PAD;  // one block of one set
+  static __device__ __forceinline__ int b_row(int r) { return r * BN + (r / RG) * B_PAD; }
   static constexpr int B_OFF = 2 * A_BLK;               // weights: [set][2 blocks]
   static constexpr int AS_OFF = B_OFF + NS * 2 * B_BLK;  // activation scales: [2][128] fp32
   static constexpr int BS_OFF = AS_OFF + 2 * BM * 4;    // W4 group scales: [set][2][128] fp32
@@ -174,13 +182,13 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
       uint8_t* sb = base + G::B_OFF + s * 2 * G::B_BLK;
       if constexpr (W4) {
         const int k2 = tid >> 8, r = (tid & 255) >> 3, c = tid & 7;
-        *(u32x4*)(sb + k2 * G::B_BLK + r * BN + 16 * c) = rg.bv[s][0];
+        *(u32x4*)(sb + k2 * G::B_BLK + G::b_row(r) + 16 * c) = rg.bv[s][0];
       } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int q = tid + THREADS * i;
           const int k2 = q >> 9, r = (q & 511) >> 3, c = q & 7;
-          *(u32x4*)(sb + k2 * G::B_BLK + r * BN + 16 * c) = rg.bv[s][i];
+          *(u32x4*)(sb + k2 * G::B_BLK + G::b_row(r) + 16 * c) = rg.bv[s][i];
         }
       }
     }
@@ -246,7 +254,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
       if constexpr (W4) {
         uint32_t lo[8], hi[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w4_split_i8x16(*(const uint32_t*)(sb + (8 * g + i) * BN + cb), lo[i], hi[i]);
+        for (int i = 0; i < 8; ++i) w4_split_i8x16(*(const uint32_t*)(sb + G::b_row(8 * g + i) + cb), lo[i], hi[i]);
         uint32_t e0[4], e1[4], o0[4], o1[4];
         tr4(lo[0], lo[1], lo[2], lo[3], e0);
         tr4(lo[4], lo[5], lo[6], lo[7], e1);
@@ -272,7 +280,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
       } else {
         uint32_t d[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) d[i] = *(const uint32_t*)(sb + (16 * g + i) * BN + cb);
+        for (int i = 0; i < 16; ++i) d[i] = *(const uint32_t*)(sb + G::b_row(16 * g + i) + cb);
         uint32_t x0[4], x1[4], x2[4], x3[4];
         tr4(d[0], d[1], d[2], d[3], x0);
         tr4(d[4], d[5], d[6], d[7], x1);
