@@ -217,6 +217,25 @@ def test_decode_forced_plans(plan, K, N, monkeypatch):
             assert torch.equal(_run_w4(x[3:4], packed, s4, z)[0], y4[3])
 
 
+@pytest.mark.parametrize("upw", [1, 2, 3, 5, 8, 9, 12, 13])
+@pytest.mark.parametrize("K,N", [(2048, 1024), (6144, 512)])
+def test_decode_w8_wave_depths(upw, K, N, monkeypatch):
+    """fp16 W8 waves issue each 32-row step's loads once: short K ranges test every
+    load, long ones run a straight-line main loop and test only their last steps.
+    Forced K depths of 1-13 steps per wave (the last wave of a tile shorter, some
+    waves empty) cover both paths and the boundary between them, split-K or not;
+    oracle parity with a residual at M = 1, 4, 16, rows independent of M."""
+    monkeypatch.setenv("QLIN_SKINNY_PLAN", f"8,8,{upw}")
+    x = H.act_f16(16, K, seed=94)
+    w, s = H.w8(K, N, seed=95)
+    res = torch.randn((16, N), generator=H.gen(96)).to(torch.float16)
+    for M in (1, 4, 16):
+        y = _run_w8(x[:M], w, s, residual=res[:M])
+        H.assert_out_close(y, H.linear_w8_ref_cols(x[:M], w, s, np.arange(N), residual=res[:M]))
+        if M == 16:
+            assert torch.equal(_run_w8(x[5:6], w, s, residual=res[5:6])[0], y[5])
+
+
 def test_repeat_calls_are_deterministic():
     """Split-K partials are summed in a fixed order, so repeated calls agree bit for bit."""
     K, N = 6144, 2048
