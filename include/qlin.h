@@ -174,6 +174,23 @@ int qlin_w4_dequant_f32(const uint8_t* packed, const void* scale, int s_dtype,
 int qlin_w8_dequant_f32(const int8_t* w, const void* scale, int s_dtype, int K, int N,
                         float* out, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Load-time producers of the packed layouts (GPU requantization of fp32 weights)
+ * ------------------------------------------------------------------------- */
+
+/* Symmetric W4 per (group, column), replacing requant_w4_sym
+ * (quant_formats.py:253-267): sc = max(amax over the group's K rows, 1e-8) / 7 in
+ * fp32, code = clamp(round_half_even(w / sc), -8, 7) + 8, packed[K/2,N] with even K
+ * in the low nibble (quant_formats.py:246-250), scale_bf16[K/group,N] = bf16(sc).
+ * w is fp32 [K,N] (N contiguous); group is 32 or 64 and divides K. */
+int qlin_requant_w4_sym(const float* w, int K, int N, int group, uint8_t* packed,
+                        uint16_t* scale_bf16, void* stream);
+
+/* Per-column W8, replacing requant_w8_row (quant_formats.py:270-275): sc[n] =
+ * max(amax over K, 1e-8) / 127 in fp32, q = clamp(round_half_even(w / sc), -127, 127).
+ * w is fp32 [K,N]; q int8 [K,N]; scale fp32 [N]. */
+int qlin_requant_w8_row(const float* w, int K, int N, int8_t* q, float* scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

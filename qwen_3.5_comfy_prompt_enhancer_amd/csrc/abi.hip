@@ -651,4 +651,26 @@ int qlin_w8_dequant_f32(const int8_t* w, const void* scale, int s_dtype, int K, 
   return hip_status("qlin_w8_dequant_f32", launch_w8_dequant(w, scale, s_dtype, K, N, out, (hipStream_t)stream));
 }
 
+int qlin_requant_w4_sym(const float* w, int K, int N, int group, uint8_t* packed, uint16_t* scale_bf16,
+                        void* stream) {
+  g_err[0] = 0;
+  if (K < 0 || N < 0) return fail(QLIN_ERR_INVALID, "qlin_requant_w4_sym: bad sizes K=%d N=%d", K, N);
+  if ((group != 32 && group != 64) || K % group != 0)
+    return fail(QLIN_ERR_INVALID, "qlin_requant_w4_sym: group %d must be 32 or 64 and divide K=%d", group, K);
+  if (K / group > 65535) return fail(QLIN_ERR_UNSUPPORTED, "qlin_requant_w4_sym: K=%d too large", K);
+  if ((long long)K * N == 0) return QLIN_OK;
+  if (!w || !packed || !scale_bf16) return fail(QLIN_ERR_INVALID, "qlin_requant_w4_sym: null pointer");
+  return hip_status("qlin_requant_w4_sym",
+                    launch_requant_w4(w, K, N, group, packed, scale_bf16, (hipStream_t)stream));
+}
+
+int qlin_requant_w8_row(const float* w, int K, int N, int8_t* q, float* scale, void* stream) {
+  g_err[0] = 0;
+  if (K < 0 || N < 0) return fail(QLIN_ERR_INVALID, "qlin_requant_w8_row: bad sizes K=%d N=%d", K, N);
+  if ((K + 63) / 64 > 65535) return fail(QLIN_ERR_UNSUPPORTED, "qlin_requant_w8_row: K=%d too large", K);
+  if ((long long)K * N == 0) return QLIN_OK;
+  if (!w || !q || !scale) return fail(QLIN_ERR_INVALID, "qlin_requant_w8_row: null pointer");
+  return hip_status("qlin_requant_w8_row", launch_requant_w8(w, K, N, q, scale, (hipStream_t)stream));
+}
+
 }  // extern "C"

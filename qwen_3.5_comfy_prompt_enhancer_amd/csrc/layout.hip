@@ -1,7 +1,10 @@
-// Element-wise layout kernels: W4 unpack and W4 / W8 dequantization to fp32.
-// They expose the exact integer / fp32 values the GEMM kernels consume so the
-// unpack and dequant can be checked bit for bit (quant_formats.py:6-9,
-// kernels/w4.py:51-61, 103-104).
+// Layout kernels.  W4 unpack and W4 / W8 dequantization to fp32 expose the exact
+// integer / fp32 values the GEMM kernels consume, so the unpack and dequant can be
+// checked bit for bit (quant_formats.py:6-9, kernels/w4.py:51-61, 103-104).  The
+// load-time producers of the packed layouts, symmetric W4 per (group, column) and
+// W8 per column (quant_formats.py:253-275), requantize fp32 weights on the GPU with
+// the same arithmetic: fp32 amax, clamp at 1e-8, one correctly rounded division for
+// the scale and one per weight, round half to even.
 #include "qlin_dev.h"
 #include "qlin_internal.h"
 
@@ -47,6 +50,68 @@ __global__ void w8_dequant_kernel(const int8_t* __restrict__ w, const void* s, i
   }
 }
 
+// ---------------------------------------------------------------------------
+// Requantization (quant_formats.py:253-275).  Byte and fp32 element work, bound
+// by HBM: every weight is read from HBM once (the second pass of a column's group
+// or of the per-column quantization hits the caches) and its code written once.
+// ---------------------------------------------------------------------------
+
+// W4: thread = (group g, column n).  sc = max(amax, 1e-8) / 7 over the group's rows;
+// code = clamp(rint(w / sc), -8, 7) + 8; even K in the low nibble (quant_formats.py:
+// 223-229, 246-250); the scale is stored as bf16 (round to nearest even).
+__global__ void requant_w4_kernel(const float* __restrict__ w, int K, int N, int group,
+                                  uint8_t* __restrict__ packed, uint16_t* __restrict__ sbf) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int gi = blockIdx.y;
+  if (n >= N) return;
+  const float* col = w + (long long)gi * group * N + n;
+  float amax = 0.0f;
+  for (int r = 0; r < group; ++r) amax = fmaxf(amax, fabsf(col[(long long)r * N]));
+  const float sc = fmaxf(amax, 1e-8f) / 7.0f;
+  uint8_t* prow = packed + (long long)gi * (group / 2) * N + n;
+  for (int r = 0; r < group; r += 2) {
+    const float q0 = fminf(fmaxf(rintf(col[(long long)r * N] / sc), -8.0f), 7.0f) + 8.0f;
+    const float q1 = fminf(fmaxf(rintf(col[(long long)(r + 1) * N] / sc), -8.0f), 7.0f) + 8.0f;
+    prow[(long long)(r / 2) * N] = (uint8_t)((int)q0 | ((int)q1 << 4));
+  }
+  sbf[(long long)gi * N + n] = f32_to_bf16(sc);
+}
+
+// W8, pass 1: the bits of max |w| over a block of rows of each column, merged with an
+// unsigned atomic max (the order of non-negative floats is that of their bits) into
+// `bits`, which starts at zero.
+__global__ void w8_amax_kernel(const float* __restrict__ w, int K, int N, int rows, unsigned* __restrict__ bits) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int r0 = blockIdx.y * rows, r1 = min(K, r0 + rows);
+  float amax = 0.0f;
+  for (int r = r0; r < r1; ++r) amax = fmaxf(amax, fabsf(w[(long long)r * N + n]));
+  atomicMax(bits + n, bitcast<unsigned>(amax));
+}
+
+__global__ void fill_u32_kernel(unsigned* __restrict__ p, int n, unsigned v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// W8, pass 2: code = clamp(rint(w / sc), -127, 127) with sc = max(amax, 1e-8) / 127.
+__global__ void w8_quant_kernel(const float* __restrict__ w, int K, int N, const unsigned* __restrict__ bits,
+                                int8_t* __restrict__ q) {
+  const long long total = (long long)K * N;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int n = (int)(i % N);
+    const float sc = fmaxf(bitcast<float>(bits[n]), 1e-8f) / 127.0f;
+    q[i] = (int8_t)(int)fminf(fmaxf(rintf(w[i] / sc), -127.0f), 127.0f);
+  }
+}
+
+// W8, pass 3: the amax bits become the fp32 scale, in place.
+__global__ void w8_scale_kernel(int N, unsigned* __restrict__ bits) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n < N) bits[n] = bitcast<unsigned>(fmaxf(bitcast<float>(bits[n]), 1e-8f) / 127.0f);
+}
+
 static dim3 grid_for(long long total) {
   long long blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
@@ -69,6 +134,25 @@ hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uin
 hipError_t launch_w8_dequant(const int8_t* w, const void* s, int sdt, int K, int N, float* out,
                              hipStream_t st) {
   hipLaunchKernelGGL(w8_dequant_kernel, grid_for((long long)K * N), dim3(256), 0, st, w, s, sdt, K, N, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_requant_w4(const float* w, int K, int N, int group, uint8_t* packed, uint16_t* sbf,
+                             hipStream_t st) {
+  hipLaunchKernelGGL(requant_w4_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)(K / group)), dim3(256), 0, st,
+                     w, K, N, group, packed, sbf);
+  return hipGetLastError();
+}
+
+hipError_t launch_requant_w8(const float* w, int K, int N, int8_t* q, float* scale, hipStream_t st) {
+  unsigned* bits = (unsigned*)scale;  // amax bits first, the scale at the end
+  const unsigned cb = (unsigned)((N + 255) / 256);
+  constexpr int kRows = 64;  // rows per amax block: enough blocks to fill the chip
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(cb), dim3(256), 0, st, bits, N, 0u);
+  hipLaunchKernelGGL(w8_amax_kernel, dim3(cb, (unsigned)((K + kRows - 1) / kRows)), dim3(256), 0, st, w, K, N,
+                     kRows, bits);
+  hipLaunchKernelGGL(w8_quant_kernel, grid_for((long long)K * N), dim3(256), 0, st, w, K, N, bits, q);
+  hipLaunchKernelGGL(w8_scale_kernel, dim3(cb), dim3(256), 0, st, N, bits);
   return hipGetLastError();
 }
 

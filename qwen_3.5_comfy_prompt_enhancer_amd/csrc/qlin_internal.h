@@ -97,5 +97,8 @@ hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uin
                              int group, int K, int N, float* out, hipStream_t st);
 hipError_t launch_w8_dequant(const int8_t* w, const void* s, int sdt, int K, int N, float* out,
                              hipStream_t st);
+hipError_t launch_requant_w4(const float* w, int K, int N, int group, uint8_t* packed, uint16_t* sbf,
+                             hipStream_t st);
+hipError_t launch_requant_w8(const float* w, int K, int N, int8_t* q, float* scale, hipStream_t st);
 
 }  // namespace qlin

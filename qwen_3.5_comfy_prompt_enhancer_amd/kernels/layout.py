@@ -6,6 +6,13 @@ These expose the exact values the GEMM kernels consume:
 * `w4_dequant_f32(packed, scale, zero=None)` -> fp32 `(nibble - z) * scale[k // G, n]`
   (quant_formats.py:6-8, kernels/w4.py:103-104);
 * `w8_dequant_f32(w, scale)` -> fp32 `w * scale[None, :]` (quant_formats.py:9).
+
+and, on the GPU, the load-time producers of those layouts with the reference's
+arithmetic and return types:
+
+* `requant_w4_sym(w, group=32)` -> (packed uint8 [K//2, N], bf16 scale [K//group, N])
+  (quant_formats.py:253-267);
+* `requant_w8_row(w)` -> (int8 [K, N], fp32 scale [N]) (quant_formats.py:270-275).
 """
 from __future__ import annotations
 
@@ -13,7 +20,7 @@ import torch
 
 from . import qlin as C
 
-__all__ = ["w4_unpack", "w4_dequant_f32", "w8_dequant_f32"]
+__all__ = ["w4_unpack", "w4_dequant_f32", "w8_dequant_f32", "requant_w4_sym", "requant_w8_row"]
 
 
 def w4_unpack(packed: torch.Tensor) -> torch.Tensor:
@@ -56,3 +63,33 @@ def w8_dequant_f32(w: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     C.call("qlin_w8_dequant_f32", C.ptr(w), C.ptr(scale), C.dtype_code(scale), K, N, C.ptr(out),
            C.stream_of(w))
     return out
+
+
+def _f32_weights(w: torch.Tensor) -> torch.Tensor:
+    if w.dim() != 2 or not w.is_floating_point():
+        raise ValueError("w must be a float [K, N] tensor")
+    C.require_cuda(w)
+    return w.to(torch.float32).contiguous()
+
+
+def requant_w4_sym(w: torch.Tensor, group: int = 32):
+    """float [K, N] -> (packed [K//2, N] uint8, scales [K//group, N] bf16): symmetric
+    int4 per (group, column) on the grid [-8, 7] + 8 (quant_formats.py:253-267)."""
+    K, N = w.shape
+    assert group in (32, 64) and K % group == 0, (K, group)
+    w = _f32_weights(w)
+    packed = torch.empty((K // 2, N), dtype=torch.uint8, device=w.device)
+    scale = torch.empty((K // group, N), dtype=torch.bfloat16, device=w.device)
+    C.call("qlin_requant_w4_sym", C.ptr(w), K, N, group, C.ptr(packed), C.ptr(scale), C.stream_of(w))
+    return packed, scale
+
+
+def requant_w8_row(w: torch.Tensor):
+    """float [K, N] -> (int8 [K, N], fp32 scale [N]) per-column symmetric
+    (quant_formats.py:270-275)."""
+    w = _f32_weights(w)
+    K, N = w.shape
+    q = torch.empty((K, N), dtype=torch.int8, device=w.device)
+    scale = torch.empty((N,), dtype=torch.float32, device=w.device)
+    C.call("qlin_requant_w8_row", C.ptr(w), K, N, C.ptr(q), C.ptr(scale), C.stream_of(w))
+    return q, scale

@@ -63,6 +63,8 @@ _SIGS = {
     "qlin_w4_unpack": [_P, _I, _I, _P, _P],
     "qlin_w4_dequant_f32": [_P, _P, _I, _P, _I, _I, _I, _P, _P],
     "qlin_w8_dequant_f32": [_P, _P, _I, _I, _I, _P, _P],
+    "qlin_requant_w4_sym": [_P, _I, _I, _I, _P, _P, _P],
+    "qlin_requant_w8_row": [_P, _I, _I, _P, _P, _P],
 }
 
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_workspace_bytes", *_SIGS)

@@ -61,6 +61,64 @@ def test_w8_dequant_bit_exact(sdt):
     assert np.array_equal(d, R.dequant_w8_f32(w.numpy(), H.np_(s)))
 
 
+def _requant_input(K, N, seed, grid_amax, group):
+    """Normal weights plus the edge cases of the producers: an all-zero column block
+    (amax clamped at 1e-8), a column holding -0.0, and a column whose blocks hit an
+    exact scale (amax = grid_amax * 2^-4, so sc = 2^-4) with every half-step tie."""
+    w = (torch.randn((K, N), generator=H.gen(seed)) * 0.02).numpy()
+    w[:group, 0] = 0.0
+    w[:, 1] = -0.0
+    rows = np.arange(K)
+    ties = ((rows % (2 * grid_amax + 1)) - grid_amax + 0.5) / 16.0
+    w[:, 2] = np.clip(ties, -grid_amax / 16.0, grid_amax / 16.0)
+    w[::group, 2] = grid_amax / 16.0  # every block reaches the exact amax
+    return torch.from_numpy(w.astype(np.float32))
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("K,N", [(256, 40), (2048, 1040)])
+def test_requant_w4_sym_bit_exact(group, K, N):
+    """GPU requant_w4_sym (quant_formats.py:253-267) equals the oracle bit for bit:
+    packed codes and bf16 scales, ties rounded half to even."""
+    layout, _ = _k()
+    w = _requant_input(K, N, seed=14, grid_amax=7, group=group)
+    packed, scale = layout.requant_w4_sym(w.cuda(), group)
+    assert packed.dtype == torch.uint8 and scale.dtype == torch.bfloat16
+    ref_p, ref_s = R.requant_w4_sym(w.numpy(), group)
+    assert np.array_equal(packed.cpu().numpy(), ref_p)
+    assert np.array_equal(scale.cpu().view(torch.int16).numpy().view(np.uint16), ref_s)
+
+
+@pytest.mark.parametrize("K,N", [(64, 24), (2048, 1040), (6144, 2048)])
+def test_requant_w8_row_bit_exact(K, N):
+    """GPU requant_w8_row (quant_formats.py:270-275) equals the oracle bit for bit."""
+    layout, _ = _k()
+    w = _requant_input(K, N, seed=15, grid_amax=127, group=K)
+    q, sc = layout.requant_w8_row(w.cuda())
+    assert q.dtype == torch.int8 and sc.dtype == torch.float32
+    ref_q, ref_sc = R.requant_w8_row(w.numpy())
+    assert np.array_equal(q.cpu().numpy(), ref_q)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), ref_sc.view(np.uint32))
+
+
+def test_requant_round_trip_full_size():
+    """At a full layer size: requantize on the GPU, dequantize with the GEMM layout
+    kernels, and every weight is back within half a step of its scale (the codes'
+    rounding bound), for W8 per column and W4 g32."""
+    layout, _ = _k()
+    K, N = 4096, 6144
+    w = (torch.randn((K, N), generator=H.gen(16)) * 0.02).cuda()
+    q, sc = layout.requant_w8_row(w)
+    err = (layout.w8_dequant_f32(q, sc) - w).abs()
+    assert bool((err <= sc[None, :] * 0.5 + w.abs() * 2.0 ** -22).all())
+    packed, s4 = layout.requant_w4_sym(w, 32)
+    d4 = layout.w4_dequant_f32(packed, s4)
+    s_rows = s4.float().repeat_interleave(32, dim=0)
+    # the codes were rounded with the fp32 scale; bf16 storage of the scale adds up to
+    # 2^-9 relative per step of 8
+    assert bool(((d4 - w).abs() <= s_rows * (0.5 + 8 * 2.0 ** -8) + w.abs() * 2.0 ** -22).all())
+
+
 # ---------------------------------------------------------------- A16 linears
 
 def _run_w8(x, w, s, out_dtype=torch.float16, residual=None):
