@@ -191,6 +191,22 @@ int qlin_requant_w4_sym(const float* w, int K, int N, int group, uint8_t* packed
  * w is fp32 [K,N]; q int8 [K,N]; scale fp32 [N]. */
 int qlin_requant_w8_row(const float* w, int K, int N, int8_t* q, float* scale, void* stream);
 
+/* GPTQ int4 qweight int32 [K/8, N] (8 K-nibbles per word, nibble j = row 8w + j) ->
+ * engine packed[K/2, N]: the nibble decode and pair packing of decode_gptq
+ * (quant_formats.py:199-208, 369-372, 411-412, 428-429).  K % 8 == 0. */
+int qlin_w4_repack_gptq(const int32_t* qweight, int K, int N, uint8_t* packed, void* stream);
+
+/* AWQ int4 qweight int32 [K, N/8] (8 N-nibbles per word in AWQ order) -> engine
+ * packed[K/2, N]: decode_awq's nibble decode, de-interleave and pair packing
+ * (quant_formats.py:211-220, 442-444, 466).  K even, N % 8 == 0, packed 8-byte aligned. */
+int qlin_w4_repack_awq(const int32_t* qweight, int K, int N, uint8_t* packed, void* stream);
+
+/* qzeros int32 [G, N/8] (8 N-nibbles per word; AWQ order if awq_order) -> uint8
+ * zeros[G, N] = nibble + add: GPTQ's effective zero is nibble + 1
+ * (quant_formats.py:396-400, 418-424), AWQ's the nibble (quant_formats.py:445-446). */
+int qlin_w4_zeros_unpack(const int32_t* qzeros, int G, int N, int awq_order, int add, uint8_t* zeros,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

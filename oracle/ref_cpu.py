@@ -16,7 +16,8 @@ file:line it follows (paths relative to the reference checkout):
   `silu(g) * u`, bf16 round trip, per-64-column int8 re-quantization with
   round-half-away-from-zero;
 * the load-time producers of the packed layouts (symmetric W4 / per-row W8
-  requantization).
+  requantization) and the external int4 formats' nibble decode into them (GPTQ
+  K-packed words, AWQ N-packed words in AWQ order, their packed zeros).
 
 Pinning (see tests/test_oracle.py): brute force over all 256 byte values, known-answer
 bytes, pack/unpack round trips, closed forms (one-hot activations, unit scales,
@@ -271,6 +272,56 @@ def requant_w8_row(w):
     sc = (amax / np.float32(127.0)).astype(np.float32)
     q = np.clip(np.rint(w / sc[None, :]), -127, 127).astype(np.int8)
     return q, sc
+
+
+def nibbles_i32(qw, bits: int = 4) -> np.ndarray:
+    """int32 packed [R, W] -> uint8 nibbles [R, W * 32/bits] in straight bit order:
+    element j of word w is bits j*bits .. j*bits+bits-1 (quant_formats.py:199-208)."""
+    q = np.asarray(qw).astype(np.int64) & 0xFFFFFFFF
+    epf = 32 // bits
+    shifts = np.arange(epf, dtype=np.int64) * bits
+    n = ((q[..., None] >> shifts) & ((1 << bits) - 1)).astype(np.uint8)
+    return n.reshape(n.shape[0], -1)
+
+
+AWQ_ORDER = np.array([0, 4, 1, 5, 2, 6, 3, 7])
+
+
+def deinterleave_awq(nib) -> np.ndarray:
+    """Restore AutoAWQ's nibble order along the last axis: out[:, c] = in[:, REV[c]]
+    per group of 8 with REV = [0, 4, 1, 5, 2, 6, 3, 7] (quant_formats.py:211-220)."""
+    nib = np.asarray(nib)
+    g = nib.reshape(*nib.shape[:-1], -1, 8)
+    return g[..., AWQ_ORDER].reshape(nib.shape)
+
+
+def gptq_w4_to_engine(qweight) -> np.ndarray:
+    """GPTQ int4 qweight int32 [K/8, N] (8 K-nibbles per word, one column) -> engine
+    packed [K/2, N] (quant_formats.py:369-372 then 246-250)."""
+    qw = np.asarray(qweight)
+    R, N = qw.shape
+    nib = nibbles_i32(qw).reshape(R, N, 8).transpose(0, 2, 1).reshape(R * 8, N)
+    return pack_pairs(nib)
+
+
+def awq_w4_to_engine(qweight) -> np.ndarray:
+    """AWQ int4 qweight int32 [K, N/8] (8 N-nibbles per word in AWQ order) -> engine
+    packed [K/2, N] (quant_formats.py:442-444 then 246-250)."""
+    nib = deinterleave_awq(nibbles_i32(qweight))
+    return pack_pairs(nib)
+
+
+def gptq_zeros(qzeros, plus_one: bool = True) -> np.ndarray:
+    """GPTQ qzeros int32 [G, N/8] -> uint8 zeros [G, N], N-packed straight order, with
+    the +1 of the effective zero (quant_formats.py:396-400, 418-424)."""
+    z = nibbles_i32(qzeros).astype(np.int32) + (1 if plus_one else 0)
+    return z.astype(np.uint8)
+
+
+def awq_zeros(qzeros) -> np.ndarray:
+    """AWQ qzeros int32 [G, N/8] -> uint8 zeros [G, N] in natural order, used as is
+    (quant_formats.py:445-446, 455)."""
+    return deinterleave_awq(nibbles_i32(qzeros)).astype(np.uint8)
 
 
 # ----------------------------------------------------------------------------

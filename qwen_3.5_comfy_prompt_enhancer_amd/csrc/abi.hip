@@ -673,4 +673,35 @@ int qlin_requant_w8_row(const float* w, int K, int N, int8_t* q, float* scale, v
   return hip_status("qlin_requant_w8_row", launch_requant_w8(w, K, N, q, scale, (hipStream_t)stream));
 }
 
+int qlin_w4_repack_gptq(const int32_t* qweight, int K, int N, uint8_t* packed, void* stream) {
+  g_err[0] = 0;
+  if (K < 0 || N < 0 || K % 8 != 0)
+    return fail(QLIN_ERR_INVALID, "qlin_w4_repack_gptq: K=%d must be a multiple of 8, N=%d", K, N);
+  if ((long long)K * N == 0) return QLIN_OK;
+  if (!qweight || !packed) return fail(QLIN_ERR_INVALID, "qlin_w4_repack_gptq: null pointer");
+  return hip_status("qlin_w4_repack_gptq", launch_repack_gptq(qweight, K, N, packed, (hipStream_t)stream));
+}
+
+int qlin_w4_repack_awq(const int32_t* qweight, int K, int N, uint8_t* packed, void* stream) {
+  g_err[0] = 0;
+  if (K < 0 || N < 0 || K % 2 != 0 || N % 8 != 0)
+    return fail(QLIN_ERR_INVALID, "qlin_w4_repack_awq: K=%d must be even and N=%d a multiple of 8", K, N);
+  if ((long long)K * N == 0) return QLIN_OK;
+  if (!qweight || !packed) return fail(QLIN_ERR_INVALID, "qlin_w4_repack_awq: null pointer");
+  if (!aligned(packed, 8)) return fail(QLIN_ERR_UNSUPPORTED, "qlin_w4_repack_awq: packed must be 8-byte aligned");
+  return hip_status("qlin_w4_repack_awq", launch_repack_awq(qweight, K, N, packed, (hipStream_t)stream));
+}
+
+int qlin_w4_zeros_unpack(const int32_t* qzeros, int G, int N, int awq_order, int add, uint8_t* zeros,
+                         void* stream) {
+  g_err[0] = 0;
+  if (G < 0 || N < 0 || N % 8 != 0)
+    return fail(QLIN_ERR_INVALID, "qlin_w4_zeros_unpack: N=%d must be a multiple of 8 (G=%d)", N, G);
+  if (add < 0 || add > 240) return fail(QLIN_ERR_INVALID, "qlin_w4_zeros_unpack: add=%d out of range", add);
+  if ((long long)G * N == 0) return QLIN_OK;
+  if (!qzeros || !zeros) return fail(QLIN_ERR_INVALID, "qlin_w4_zeros_unpack: null pointer");
+  return hip_status("qlin_w4_zeros_unpack",
+                    launch_zeros_unpack(qzeros, G, N, awq_order ? 1 : 0, add, zeros, (hipStream_t)stream));
+}
+
 }  // extern "C"

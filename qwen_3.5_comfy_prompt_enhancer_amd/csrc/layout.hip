@@ -112,6 +112,61 @@ __global__ void w8_scale_kernel(int N, unsigned* __restrict__ bits) {
   if (n < N) bits[n] = bitcast<unsigned>(fmaxf(bitcast<float>(bits[n]), 1e-8f) / 127.0f);
 }
 
+// ---------------------------------------------------------------------------
+// External int4 formats -> the engine layout (quant_formats.py:199-229, 355-466).
+// GPTQ packs 8 K-nibbles of one column per int32 word (nibble j = bits 4j..4j+3 =
+// row 8w + j), so the engine's pair bytes (even K low, odd K high) are the word's
+// little-endian bytes: packed[4w + t][n] = byte t of qweight[w][n].  AWQ packs 8
+// N-nibbles of one row per word in the order [0, 2, 4, 6, 1, 3, 5, 7]; column 8c + j
+// sits at nibble kAwqRev[j] = [0, 4, 1, 5, 2, 6, 3, 7][j] of word c.
+// ---------------------------------------------------------------------------
+
+__constant__ int kAwqRev[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+// thread = (word row w, column n): one word in, its 4 bytes to 4 packed rows
+__global__ void repack_gptq_kernel(const uint32_t* __restrict__ qw, int K, int N, uint8_t* __restrict__ packed) {
+  const long long total = (long long)(K / 8) * N;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long w = i / N, n = i - w * N;
+    const uint32_t v = qw[i];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) packed[(4 * w + t) * N + n] = (uint8_t)(v >> (8 * t));
+  }
+}
+
+// thread = (packed row r, word c): rows 2r and 2r+1 of word column c -> 8 pair bytes
+__global__ void repack_awq_kernel(const uint32_t* __restrict__ qw, int K, int N, uint8_t* __restrict__ packed) {
+  const int W = N / 8;
+  const long long total = (long long)(K / 2) * W;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long r = i / W, c = i - r * W;
+    const uint32_t lo = qw[(2 * r) * W + c], hi = qw[(2 * r + 1) * W + c];
+    uint32_t b[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int sh = 4 * kAwqRev[j];
+      const uint32_t byte = ((lo >> sh) & 0xFu) | (((hi >> sh) & 0xFu) << 4);
+      b[j >> 2] |= byte << (8 * (j & 3));
+    }
+    *(u32x2*)(packed + r * N + 8 * c) = u32x2{b[0], b[1]};
+  }
+}
+
+// z[g][8c + j] = nibble (awq ? kAwqRev[j] : j) of qzeros[g][c], plus `add`
+__global__ void zeros_unpack_kernel(const uint32_t* __restrict__ qz, int G, int N, int awq, int add,
+                                    uint8_t* __restrict__ z) {
+  const long long total = (long long)G * N;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long g = i / N;
+    const int n = (int)(i - g * N), c = n >> 3, j = n & 7;
+    const int pos = awq ? kAwqRev[j] : j;
+    z[i] = (uint8_t)(((qz[g * (N / 8) + c] >> (4 * pos)) & 0xFu) + (uint32_t)add);
+  }
+}
+
 static dim3 grid_for(long long total) {
   long long blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
@@ -153,6 +208,24 @@ hipError_t launch_requant_w8(const float* w, int K, int N, int8_t* q, float* sca
                      kRows, bits);
   hipLaunchKernelGGL(w8_quant_kernel, grid_for((long long)K * N), dim3(256), 0, st, w, K, N, bits, q);
   hipLaunchKernelGGL(w8_scale_kernel, dim3(cb), dim3(256), 0, st, N, bits);
+  return hipGetLastError();
+}
+
+hipError_t launch_repack_gptq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st) {
+  hipLaunchKernelGGL(repack_gptq_kernel, grid_for((long long)(K / 8) * N), dim3(256), 0, st, (const uint32_t*)qw,
+                     K, N, packed);
+  return hipGetLastError();
+}
+
+hipError_t launch_repack_awq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st) {
+  hipLaunchKernelGGL(repack_awq_kernel, grid_for((long long)(K / 2) * (N / 8)), dim3(256), 0, st,
+                     (const uint32_t*)qw, K, N, packed);
+  return hipGetLastError();
+}
+
+hipError_t launch_zeros_unpack(const int32_t* qz, int G, int N, int awq, int add, uint8_t* z, hipStream_t st) {
+  hipLaunchKernelGGL(zeros_unpack_kernel, grid_for((long long)G * N), dim3(256), 0, st, (const uint32_t*)qz, G, N,
+                     awq, add, z);
   return hipGetLastError();
 }
 

@@ -100,5 +100,8 @@ hipError_t launch_w8_dequant(const int8_t* w, const void* s, int sdt, int K, int
 hipError_t launch_requant_w4(const float* w, int K, int N, int group, uint8_t* packed, uint16_t* sbf,
                              hipStream_t st);
 hipError_t launch_requant_w8(const float* w, int K, int N, int8_t* q, float* scale, hipStream_t st);
+hipError_t launch_repack_gptq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st);
+hipError_t launch_repack_awq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st);
+hipError_t launch_zeros_unpack(const int32_t* qz, int G, int N, int awq, int add, uint8_t* z, hipStream_t st);
 
 }  // namespace qlin

@@ -12,7 +12,16 @@ arithmetic and return types:
 
 * `requant_w4_sym(w, group=32)` -> (packed uint8 [K//2, N], bf16 scale [K//group, N])
   (quant_formats.py:253-267);
-* `requant_w8_row(w)` -> (int8 [K, N], fp32 scale [N]) (quant_formats.py:270-275).
+* `requant_w8_row(w)` -> (int8 [K, N], fp32 scale [N]) (quant_formats.py:270-275);
+
+and the external int4 formats' nibble decode into the engine layout:
+
+* `gptq_w4_to_engine(qweight)`: int32 [K/8, N] -> packed [K/2, N] (quant_formats.py:
+  369-372, 411-412);
+* `awq_w4_to_engine(qweight)`: int32 [K, N/8] in AWQ order -> packed [K/2, N]
+  (quant_formats.py:442-444, 466);
+* `gptq_zeros(qzeros, plus_one=True)` / `awq_zeros(qzeros)`: int32 [G, N/8] -> uint8
+  [G, N] (quant_formats.py:396-400, 445-446).
 """
 from __future__ import annotations
 
@@ -20,7 +29,8 @@ import torch
 
 from . import qlin as C
 
-__all__ = ["w4_unpack", "w4_dequant_f32", "w8_dequant_f32", "requant_w4_sym", "requant_w8_row"]
+__all__ = ["w4_unpack", "w4_dequant_f32", "w8_dequant_f32", "requant_w4_sym", "requant_w8_row",
+           "gptq_w4_to_engine", "awq_w4_to_engine", "gptq_zeros", "awq_zeros"]
 
 
 def w4_unpack(packed: torch.Tensor) -> torch.Tensor:
@@ -93,3 +103,47 @@ def requant_w8_row(w: torch.Tensor):
     scale = torch.empty((N,), dtype=torch.float32, device=w.device)
     C.call("qlin_requant_w8_row", C.ptr(w), K, N, C.ptr(q), C.ptr(scale), C.stream_of(w))
     return q, scale
+
+
+def _i32_words(name: str, t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.int32 or t.dim() != 2:
+        raise ValueError(f"{name} must be an int32 [rows, words] tensor")
+    C.require_contig(name, t)
+    C.require_cuda(t)
+    return t
+
+
+def gptq_w4_to_engine(qweight: torch.Tensor) -> torch.Tensor:
+    """GPTQ int4 qweight int32 [K/8, N] -> engine packed uint8 [K/2, N]."""
+    qweight = _i32_words("qweight", qweight)
+    K, N = qweight.shape[0] * 8, qweight.shape[1]
+    packed = torch.empty((K // 2, N), dtype=torch.uint8, device=qweight.device)
+    C.call("qlin_w4_repack_gptq", C.ptr(qweight), K, N, C.ptr(packed), C.stream_of(qweight))
+    return packed
+
+
+def awq_w4_to_engine(qweight: torch.Tensor) -> torch.Tensor:
+    """AWQ int4 qweight int32 [K, N/8] (AWQ nibble order) -> engine packed uint8 [K/2, N]."""
+    qweight = _i32_words("qweight", qweight)
+    K, N = qweight.shape[0], qweight.shape[1] * 8
+    packed = torch.empty((K // 2, N), dtype=torch.uint8, device=qweight.device)
+    C.call("qlin_w4_repack_awq", C.ptr(qweight), K, N, C.ptr(packed), C.stream_of(qweight))
+    return packed
+
+
+def _zeros(qzeros: torch.Tensor, awq: int, add: int) -> torch.Tensor:
+    qzeros = _i32_words("qzeros", qzeros)
+    G, N = qzeros.shape[0], qzeros.shape[1] * 8
+    z = torch.empty((G, N), dtype=torch.uint8, device=qzeros.device)
+    C.call("qlin_w4_zeros_unpack", C.ptr(qzeros), G, N, awq, add, C.ptr(z), C.stream_of(qzeros))
+    return z
+
+
+def gptq_zeros(qzeros: torch.Tensor, plus_one: bool = True) -> torch.Tensor:
+    """GPTQ qzeros int32 [G, N/8] -> uint8 zeros [G, N] (+1: the effective zero)."""
+    return _zeros(qzeros, 0, 1 if plus_one else 0)
+
+
+def awq_zeros(qzeros: torch.Tensor) -> torch.Tensor:
+    """AWQ qzeros int32 [G, N/8] (AWQ nibble order) -> uint8 zeros [G, N]."""
+    return _zeros(qzeros, 1, 0)

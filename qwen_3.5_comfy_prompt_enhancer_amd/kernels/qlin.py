@@ -65,6 +65,9 @@ _SIGS = {
     "qlin_w8_dequant_f32": [_P, _P, _I, _I, _I, _P, _P],
     "qlin_requant_w4_sym": [_P, _I, _I, _I, _P, _P, _P],
     "qlin_requant_w8_row": [_P, _I, _I, _P, _P, _P],
+    "qlin_w4_repack_gptq": [_P, _I, _I, _P, _P],
+    "qlin_w4_repack_awq": [_P, _I, _I, _P, _P],
+    "qlin_w4_zeros_unpack": [_P, _I, _I, _I, _I, _P, _P],
 }
 
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_workspace_bytes", *_SIGS)

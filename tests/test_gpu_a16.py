@@ -119,6 +119,62 @@ def test_requant_round_trip_full_size():
     assert bool(((d4 - w).abs() <= s_rows * (0.5 + 8 * 2.0 ** -8) + w.abs() * 2.0 ** -22).all())
 
 
+def _rand_words(rows, cols, seed):
+    g = np.random.default_rng(seed)
+    return torch.from_numpy(g.integers(-2 ** 31, 2 ** 31, size=(rows, cols), dtype=np.int64).astype(np.int32))
+
+
+@pytest.mark.parametrize("K,N", [(64, 24), (4096, 1040), (12288, 4096)])
+def test_w4_repack_gptq_bit_exact(K, N):
+    """GPTQ qweight int32 [K/8, N] -> engine packed [K/2, N] equals the oracle bit for bit."""
+    layout, _ = _k()
+    qw = _rand_words(K // 8, N, seed=17)
+    p = layout.gptq_w4_to_engine(qw.cuda())
+    assert p.shape == (K // 2, N) and p.dtype == torch.uint8
+    assert np.array_equal(p.cpu().numpy(), R.gptq_w4_to_engine(qw.numpy()))
+
+
+@pytest.mark.parametrize("K,N", [(2, 8), (4096, 1040), (4096, 12288)])
+def test_w4_repack_awq_bit_exact(K, N):
+    """AWQ qweight int32 [K, N/8] (AWQ nibble order) -> engine packed [K/2, N]."""
+    layout, _ = _k()
+    qw = _rand_words(K, N // 8, seed=18)
+    p = layout.awq_w4_to_engine(qw.cuda())
+    assert p.shape == (K // 2, N) and p.dtype == torch.uint8
+    assert np.array_equal(p.cpu().numpy(), R.awq_w4_to_engine(qw.numpy()))
+
+
+def test_w4_zeros_unpack_bit_exact():
+    layout, _ = _k()
+    qz = _rand_words(32, 128, seed=19)
+    assert np.array_equal(layout.gptq_zeros(qz.cuda()).cpu().numpy(), R.gptq_zeros(qz.numpy()))
+    assert np.array_equal(layout.gptq_zeros(qz.cuda(), plus_one=False).cpu().numpy(),
+                          R.gptq_zeros(qz.numpy(), plus_one=False))
+    assert np.array_equal(layout.awq_zeros(qz.cuda()).cpu().numpy(), R.awq_zeros(qz.numpy()))
+
+
+def test_repacked_gptq_feeds_the_gemm():
+    """A GPTQ-packed symmetric checkpoint, repacked on the GPU, runs through the W4
+    decode GEMM and matches the oracle's dequantize + fp32 matmul of the same codes."""
+    layout, _ = _k()
+    K, N = 2048, 1024
+    qw = _rand_words(K // 8, N, seed=20)
+    packed = layout.gptq_w4_to_engine(qw.cuda())
+    s = (torch.rand((K // 128, N), generator=H.gen(21)) * 1e-3).to(torch.float16)
+    x = H.act_f16(4, K, seed=22)
+    y = _run_w4(x, packed.cpu(), s, None)
+    ref = H.linear_w4_ref_cols(x, torch.from_numpy(R.gptq_w4_to_engine(qw.numpy())), s, None, np.arange(N))
+    H.assert_out_close(y, ref)
+
+
+def test_repack_bad_arguments_raise():
+    layout, _ = _k()
+    with pytest.raises(ValueError):
+        layout.awq_w4_to_engine(torch.zeros((3, 2), dtype=torch.int32, device="cuda"))  # odd K
+    with pytest.raises(ValueError):
+        layout.gptq_w4_to_engine(torch.zeros((4, 8), dtype=torch.int64, device="cuda"))  # not int32
+
+
 # ---------------------------------------------------------------- A16 linears
 
 def _run_w8(x, w, s, out_dtype=torch.float16, residual=None):

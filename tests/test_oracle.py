@@ -304,3 +304,68 @@ def test_requant_rounding_matches_torch_round():
     q, sc = R.requant_w8_row(w)
     ref = torch.clamp(torch.round(torch.from_numpy(w) / torch.from_numpy(sc)[None, :]), -127, 127)
     assert np.array_equal(q.astype(np.float32), ref.numpy())
+
+
+# ---------------------------------------------------------------- external int4 formats
+#
+# Anchors: the bit layout the reference's decoders state (quant_formats.py:199-220:
+# straight nibble order inside an int32 word, AWQ's reverse order [0, 4, 1, 5, 2, 6,
+# 3, 7]) and the pack order of AutoAWQ's published packer, [0, 2, 4, 6, 1, 3, 5, 7]
+# (AutoAWQ is not part of the reference checkout; its order is the inverse of the
+# reference's REV, which the round trips below check).
+
+AWQ_PACK_ORDER = [0, 2, 4, 6, 1, 3, 5, 7]
+
+
+def _words_from_nibbles(nib8):
+    """[..., 8] nibbles -> int32 words, nibble p at bits 4p..4p+3."""
+    w = np.zeros(nib8.shape[:-1], dtype=np.int64)
+    for p in range(8):
+        w |= nib8[..., p].astype(np.int64) << (4 * p)
+    return w.astype(np.uint32).view(np.int32)
+
+
+def _gptq_words(nib):
+    """natural nibbles [K, N] -> GPTQ qweight [K/8, N]: word w holds rows 8w..8w+7."""
+    K, N = nib.shape
+    return _words_from_nibbles(nib.reshape(K // 8, 8, N).transpose(0, 2, 1))
+
+
+def _awq_words(nib, order=AWQ_PACK_ORDER):
+    """natural nibbles [R, N] -> AWQ words [R, N/8]: nibble p of word c = column 8c + order[p]."""
+    R_, N = nib.shape
+    g = nib.reshape(R_, N // 8, 8)
+    return _words_from_nibbles(g[..., order])
+
+
+def test_nibbles_known_answers():
+    words = np.array([[0x76543210, np.uint32(0xFEDCBA98).view(np.int32), -1, 0]], dtype=np.int32)
+    n = R.nibbles_i32(words)
+    assert n.tolist() == [list(range(8)) + list(range(8, 16)) + [15] * 8 + [0] * 8]
+
+
+def test_gptq_repack_is_the_words_bytes():
+    qw = RNG.integers(-2 ** 31, 2 ** 31, size=(16, 24), dtype=np.int64).astype(np.int32)
+    p = R.gptq_w4_to_engine(qw)
+    u = qw.view(np.uint32)
+    for t in range(4):
+        assert np.array_equal(p[t::4], ((u >> (8 * t)) & 0xFF).astype(np.uint8))
+
+
+def test_gptq_repack_round_trip():
+    nib = RNG.integers(0, 16, size=(64, 40), dtype=np.uint8)
+    assert np.array_equal(R.unpack_w4(R.gptq_w4_to_engine(_gptq_words(nib))), nib)
+
+
+def test_awq_repack_round_trip_with_published_pack_order():
+    nib = RNG.integers(0, 16, size=(32, 64), dtype=np.uint8)
+    assert np.array_equal(R.unpack_w4(R.awq_w4_to_engine(_awq_words(nib))), nib)
+    # the order is an inverse pair: words packed in straight order do not round-trip
+    assert not np.array_equal(R.unpack_w4(R.awq_w4_to_engine(_awq_words(nib, list(range(8))))), nib)
+
+
+def test_zero_unpack_orders():
+    z = RNG.integers(0, 16, size=(4, 32), dtype=np.uint8)
+    assert np.array_equal(R.gptq_zeros(_awq_words(z, list(range(8)))), z + 1)
+    assert np.array_equal(R.gptq_zeros(_awq_words(z, list(range(8))), plus_one=False), z)
+    assert np.array_equal(R.awq_zeros(_awq_words(z)), z)
