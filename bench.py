@@ -17,7 +17,8 @@ dominant kernel's live per-launch time for the roofline object.
 Other workloads (`--workload`): decode-w4 (same shapes, W4 group 128), prefill
 (M in 128/512/2048, TFLOP/s), chain-w4 (9B-class 32-layer W4 decode chain), single
 (one 2048x6144 int8 linear, M=1), engine-w8 / engine-w4 (the engine-signature calls
-of one layer at decode rows and a 512-row prefill chunk).
+of one layer at decode rows and a 512-row prefill chunk), layout (the load-time layout
+producers: GPU requantization and GPTQ / AWQ repacks, HBM GB/s).
 
 Prints ONE JSON line (rank 0).  Synthetic data; weights are random in the engine
 layouts.
@@ -511,6 +512,48 @@ def prefill_pmc(args):
     return 0
 
 
+def layout_bench(args):
+    """The load-time layout producers at a 9B-class projection (K=4096, N=12288):
+    GPU requantization of fp32 weights (W8 per column, W4 g32) and the GPTQ / AWQ int4
+    repacks.  HBM-bound byte work: algorithmic bytes = one read of the input and one
+    write of the outputs; time per launch from HIP events on the launching stream."""
+    import torch
+    dev = torch.device("cuda", 0)
+    lay = importlib.import_module(f"{ALIAS}.kernels.layout")
+    gen = torch.Generator().manual_seed(9)
+    K, N = 4096, 12288
+    w = (torch.randn((K, N), generator=gen) * 0.02).to(dev)
+    qg = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), generator=gen, dtype=torch.int32).to(dev)
+    qa = torch.randint(-2 ** 31, 2 ** 31 - 1, (K, N // 8), generator=gen, dtype=torch.int32).to(dev)
+    cases = {
+        "requant_w8_row": (lambda: lay.requant_w8_row(w), 4 * K * N + K * N + 4 * N),
+        "requant_w4_sym_g32": (lambda: lay.requant_w4_sym(w, 32), 4 * K * N + K * N // 2 + 2 * (K // 32) * N),
+        "w4_repack_gptq": (lambda: lay.gptq_w4_to_engine(qg), K * N // 2 + K * N // 2),
+        "w4_repack_awq": (lambda: lay.awq_w4_to_engine(qa), K * N // 2 + K * N // 2),
+    }
+    res = {}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(args.warmup):
+            fn()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(args.steps):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / args.steps
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "GB/s": round(nbytes / us / 1e3, 1),
+                     "frac_of_8TB/s": round(nbytes / us / 1e3 / 8000.0, 3)}
+    line = {"metric": "layout producers, HBM GB/s", "value": res["requant_w8_row"]["GB/s"], "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "data": "synthetic (seeded random fp32 weights and int32 words)", "dtype": "f32 / u8 / i32",
+            "config": {"workload": "layout producers at K=4096, N=12288", "kernels": res}}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 # ------------------------------------------------------------------ main
 
 def read_traffic(kernel_tag):
@@ -536,7 +579,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode-w8",
                     choices=["decode-w8", "decode-w4", "prefill", "chain-w4", "single", "head-pmc",
-                             "prefill-pmc", "engine-w8", "engine-w4"])
+                             "prefill-pmc", "engine-w8", "engine-w4", "layout"])
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -562,6 +605,8 @@ def main() -> int:
         return head_pmc(args)
     if wl == "prefill-pmc":
         return prefill_pmc(args)
+    if wl == "layout":
+        return layout_bench(args)
     ms = [1, 2, 4]
     roof = None
     if wl in ("decode-w8", "decode-w4", "chain-w4", "single"):

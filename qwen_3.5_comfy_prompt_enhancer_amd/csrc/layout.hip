@@ -56,6 +56,40 @@ __global__ void w8_dequant_kernel(const int8_t* __restrict__ w, const void* s, i
 // or of the per-column quantization hits the caches) and its code written once.
 // ---------------------------------------------------------------------------
 
+__device__ __forceinline__ uint32_t code_w4(float w, float sc) {
+  return (uint32_t)(int)(fminf(fmaxf(rintf(w / sc), -8.0f), 7.0f) + 8.0f);
+}
+
+// W4, 4 columns per thread (N % 4 == 0): 16-byte loads, one 4-byte store per row pair.
+__global__ void requant_w4_x4_kernel(const float* __restrict__ w, int K, int N, int group,
+                                     uint8_t* __restrict__ packed, uint16_t* __restrict__ sbf) {
+  const int n = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+  const int gi = blockIdx.y;
+  if (n >= N) return;
+  const float* col = w + (long long)gi * group * N + n;
+  f32x4 amax = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < group; ++r) {
+    const f32x4 v = *(const f32x4*)(col + (long long)r * N);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) amax[c] = fmaxf(amax[c], fabsf(v[c]));
+  }
+  float sc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) sc[c] = fmaxf(amax[c], 1e-8f) / 7.0f;
+  uint8_t* prow = packed + (long long)gi * (group / 2) * N + n;
+  for (int r = 0; r < group; r += 2) {
+    const f32x4 v0 = *(const f32x4*)(col + (long long)r * N);
+    const f32x4 v1 = *(const f32x4*)(col + (long long)(r + 1) * N);
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) word |= (code_w4(v0[c], sc[c]) | (code_w4(v1[c], sc[c]) << 4)) << (8 * c);
+    *(uint32_t*)(prow + (long long)(r / 2) * N) = word;
+  }
+  *(u32x2*)(sbf + (long long)gi * N + n) =
+      u32x2{(uint32_t)f32_to_bf16(sc[0]) | ((uint32_t)f32_to_bf16(sc[1]) << 16),
+            (uint32_t)f32_to_bf16(sc[2]) | ((uint32_t)f32_to_bf16(sc[3]) << 16)};
+}
+
 // W4: thread = (group g, column n).  sc = max(amax, 1e-8) / 7 over the group's rows;
 // code = clamp(rint(w / sc), -8, 7) + 8; even K in the low nibble (quant_formats.py:
 // 223-229, 246-250); the scale is stored as bf16 (round to nearest even).
@@ -89,6 +123,21 @@ __global__ void w8_amax_kernel(const float* __restrict__ w, int K, int N, int ro
   atomicMax(bits + n, bitcast<unsigned>(amax));
 }
 
+// the same, 4 columns per thread (N % 4 == 0)
+__global__ void w8_amax_x4_kernel(const float* __restrict__ w, int K, int N, int rows, unsigned* __restrict__ bits) {
+  const int n = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (n >= N) return;
+  const int r0 = blockIdx.y * rows, r1 = min(K, r0 + rows);
+  f32x4 amax = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int r = r0; r < r1; ++r) {
+    const f32x4 v = *(const f32x4*)(w + (long long)r * N + n);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) amax[c] = fmaxf(amax[c], fabsf(v[c]));
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) atomicMax(bits + n + c, bitcast<unsigned>(amax[c]));
+}
+
 __global__ void fill_u32_kernel(unsigned* __restrict__ p, int n, unsigned v) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -103,6 +152,26 @@ __global__ void w8_quant_kernel(const float* __restrict__ w, int K, int N, const
     const int n = (int)(i % N);
     const float sc = fmaxf(bitcast<float>(bits[n]), 1e-8f) / 127.0f;
     q[i] = (int8_t)(int)fminf(fmaxf(rintf(w[i] / sc), -127.0f), 127.0f);
+  }
+}
+
+__device__ __forceinline__ uint32_t code_w8(float w, float sc) {
+  return (uint32_t)(int)fminf(fmaxf(rintf(w / sc), -127.0f), 127.0f) & 0xFFu;
+}
+
+// the same, 4 consecutive elements per thread (N % 4 == 0, so they share a row)
+__global__ void w8_quant_x4_kernel(const float* __restrict__ w, int K, int N, const unsigned* __restrict__ bits,
+                                   int8_t* __restrict__ q) {
+  const long long total4 = (long long)K * N / 4;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total4;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int n = (int)((4 * i) % N);
+    const f32x4 v = *(const f32x4*)(w + 4 * i);
+    const u32x4 b = *(const u32x4*)(bits + n);
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) word |= code_w8(v[c], fmaxf(bitcast<float>(b[c]), 1e-8f) / 127.0f) << (8 * c);
+    *(uint32_t*)(q + 4 * i) = word;
   }
 }
 
@@ -132,6 +201,21 @@ __global__ void repack_gptq_kernel(const uint32_t* __restrict__ qw, int K, int N
     const uint32_t v = qw[i];
 #pragma unroll
     for (int t = 0; t < 4; ++t) packed[(4 * w + t) * N + n] = (uint8_t)(v >> (8 * t));
+  }
+}
+
+// 4 columns per thread (N % 4 == 0): one 16-byte load, a 4x4 byte transpose, four
+// 4-byte stores (row 4w + t gets byte t of the four words)
+__global__ void repack_gptq_x4_kernel(const uint32_t* __restrict__ qw, int K, int N, uint8_t* __restrict__ packed) {
+  const long long total4 = (long long)(K / 8) * N / 4;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total4;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long e = 4 * i, w = e / N, n = e - w * N;
+    const u32x4 v = *(const u32x4*)(qw + e);
+    uint32_t t4[4];
+    tr4(v.x, v.y, v.z, v.w, t4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) *(uint32_t*)(packed + (4 * w + t) * N + n) = t4[t];
   }
 }
 
@@ -167,6 +251,8 @@ __global__ void zeros_unpack_kernel(const uint32_t* __restrict__ qz, int G, int 
   }
 }
 
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 static dim3 grid_for(long long total) {
   long long blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
@@ -194,8 +280,12 @@ hipError_t launch_w8_dequant(const int8_t* w, const void* s, int sdt, int K, int
 
 hipError_t launch_requant_w4(const float* w, int K, int N, int group, uint8_t* packed, uint16_t* sbf,
                              hipStream_t st) {
-  hipLaunchKernelGGL(requant_w4_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)(K / group)), dim3(256), 0, st,
-                     w, K, N, group, packed, sbf);
+  if (N % 4 == 0 && aligned16(w) && aligned16(packed) && aligned16(sbf))
+    hipLaunchKernelGGL(requant_w4_x4_kernel, dim3((unsigned)((N / 4 + 255) / 256), (unsigned)(K / group)), dim3(256),
+                       0, st, w, K, N, group, packed, sbf);
+  else
+    hipLaunchKernelGGL(requant_w4_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)(K / group)), dim3(256), 0,
+                       st, w, K, N, group, packed, sbf);
   return hipGetLastError();
 }
 
@@ -204,16 +294,26 @@ hipError_t launch_requant_w8(const float* w, int K, int N, int8_t* q, float* sca
   const unsigned cb = (unsigned)((N + 255) / 256);
   constexpr int kRows = 64;  // rows per amax block: enough blocks to fill the chip
   hipLaunchKernelGGL(fill_u32_kernel, dim3(cb), dim3(256), 0, st, bits, N, 0u);
-  hipLaunchKernelGGL(w8_amax_kernel, dim3(cb, (unsigned)((K + kRows - 1) / kRows)), dim3(256), 0, st, w, K, N,
-                     kRows, bits);
-  hipLaunchKernelGGL(w8_quant_kernel, grid_for((long long)K * N), dim3(256), 0, st, w, K, N, bits, q);
+  if (N % 4 == 0 && aligned16(w) && aligned16(q) && aligned16(scale)) {
+    hipLaunchKernelGGL(w8_amax_x4_kernel, dim3((unsigned)((N / 4 + 255) / 256), (unsigned)((K + kRows - 1) / kRows)),
+                       dim3(256), 0, st, w, K, N, kRows, bits);
+    hipLaunchKernelGGL(w8_quant_x4_kernel, grid_for((long long)K * N / 4), dim3(256), 0, st, w, K, N, bits, q);
+  } else {
+    hipLaunchKernelGGL(w8_amax_kernel, dim3(cb, (unsigned)((K + kRows - 1) / kRows)), dim3(256), 0, st, w, K, N,
+                       kRows, bits);
+    hipLaunchKernelGGL(w8_quant_kernel, grid_for((long long)K * N), dim3(256), 0, st, w, K, N, bits, q);
+  }
   hipLaunchKernelGGL(w8_scale_kernel, dim3(cb), dim3(256), 0, st, N, bits);
   return hipGetLastError();
 }
 
 hipError_t launch_repack_gptq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st) {
-  hipLaunchKernelGGL(repack_gptq_kernel, grid_for((long long)(K / 8) * N), dim3(256), 0, st, (const uint32_t*)qw,
-                     K, N, packed);
+  if (N % 4 == 0 && aligned16(qw) && aligned16(packed))
+    hipLaunchKernelGGL(repack_gptq_x4_kernel, grid_for((long long)(K / 8) * N / 4), dim3(256), 0, st,
+                       (const uint32_t*)qw, K, N, packed);
+  else
+    hipLaunchKernelGGL(repack_gptq_kernel, grid_for((long long)(K / 8) * N), dim3(256), 0, st, (const uint32_t*)qw,
+                       K, N, packed);
   return hipGetLastError();
 }
 
