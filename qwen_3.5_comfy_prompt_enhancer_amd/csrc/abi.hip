@@ -402,16 +402,27 @@ struct PfPlan {
 };
 
 PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
+  // Time model fitted to MI355X measurements with the weights streaming from HBM
+  // (M = 128 / 512 / 2048 on the 2048x6144, 6144x2048 and 2048x2048 shapes):
+  //   tiled:  5 us + rounds x (K tiles per split) x t_tile  (x 1.3 for W4)
+  //           + split-K exchange: 1.45 us per split (the last workgroup reads the
+  //             splits one round trip each) + 12 ns per workgroup + 0.1 us per MB of
+  //             partial tiles; a split level is tried only while the level below it
+  //             leaves CUs idle (split-K exists to fill the chip)
+  //   rows:   16-row tiles, 4 waves over the whole K per 128 columns:
+  //           7.1 us (W4 5.8) + max(1, workgroups / 256) x 3.4 ns (W4 2.7) per K row
   struct Cand {
     int shape;
     int per_cu;        // workgroups one CU can hold
     double t_tile[2];  // seconds per 64-wide K tile of a workgroup, 1 or 2 per CU
   };
-  const double w4f = (wk == WK_W4) ? 1.3 : 1.0;
-  const Cand cands[2] = {{PF_128x128_K2, 2, {0.66e-6, 1.35e-6}}, {PF_256x256, 1, {1.96e-6, 1.96e-6}}};
+  const bool w4 = wk == WK_W4;
+  const double w4f = w4 ? 1.3 : 1.0;
+  const Cand cands[2] = {{PF_128x128_K2, 2, {0.48e-6, 1.35e-6}}, {PF_256x256, 1, {1.96e-6, 1.96e-6}}};
   const int nk = K / 64;
   PfPlan best{false, PF_128x128_K2, 1};
-  double best_t = 9.8e-6 + 6.3e-9 * M * ((double)K * N / 1e6);
+  const double row_wgs = (double)((M + 15) / 16) * ((N + 127) / 128);
+  double best_t = (w4 ? 5.8e-6 : 7.1e-6) + (row_wgs > 256 ? row_wgs / 256 : 1.0) * (w4 ? 2.7e-9 : 3.4e-9) * K;
   for (const Cand& c : cands) {
     int bm, bn, waves;
     prefill_geometry(c.shape, &bm, &bn, &waves);
@@ -421,9 +432,12 @@ PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
       const double part_bytes = (double)tiles * S * waves * 128 * 64 * sizeof(float);
       if (S > 1 && (part_bytes > (double)part_cap || tiles > (long long)(kCounterBytes / sizeof(unsigned)))) break;
       const long long wgs = tiles * S;
+      if (S > 1 && tiles * (S / 2) >= 256LL * c.per_cu) break;
       const int occ = (wgs > 256 && c.per_cu > 1) ? 2 : 1;
       const double rounds = (double)((wgs + 256LL * occ - 1) / (256LL * occ));
-      const double t = 5e-6 + rounds * (nk / S) * c.t_tile[occ - 1] * w4f + (S > 1 ? 3e-6 + part_bytes * 0.5e-12 : 0.0);
+      const double tile_bytes = (double)wgs * bm * bn * sizeof(float);  // one partial tile per workgroup
+      const double t = 5e-6 + rounds * (nk / S) * c.t_tile[occ - 1] * w4f +
+                       (S > 1 ? 1.45e-6 * S + 12e-9 * wgs + 0.1e-12 * tile_bytes : 0.0);
       if (t < best_t) {
         best_t = t;
         best = PfPlan{true, c.shape, S};
