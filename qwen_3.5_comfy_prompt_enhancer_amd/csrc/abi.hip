@@ -399,6 +399,7 @@ struct PfPlan {
   bool tiled;
   int shape;
   int splits;
+  int sk;  // balanced schedule: K tiles per workgroup (0 = off)
 };
 
 PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
@@ -409,6 +410,8 @@ PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
   //             splits one round trip each) + 12 ns per workgroup + 0.1 us per MB of
   //             partial tiles; a split level is tried only while the level below it
   //             leaves CUs idle (split-K exists to fill the chip)
+  //   balanced: 5 us + (K tiles per workgroup) x t_tile + the exchange of the
+  //             tiles shared by two workgroups (below)
   //   rows:   16-row tiles, 4 waves over the whole K per 128 columns:
   //           7.1 us (W4 5.8) + max(1, workgroups / 256) x 3.4 ns (W4 2.7) per K row
   struct Cand {
@@ -420,7 +423,7 @@ PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
   const double w4f = w4 ? 1.3 : 1.0;
   const Cand cands[2] = {{PF_128x128_K2, 2, {0.48e-6, 1.35e-6}}, {PF_256x256, 1, {1.96e-6, 1.96e-6}}};
   const int nk = K / 64;
-  PfPlan best{false, PF_128x128_K2, 1};
+  PfPlan best{false, PF_128x128_K2, 1, 0};
   const double row_wgs = (double)((M + 15) / 16) * ((N + 127) / 128);
   double best_t = (w4 ? 5.8e-6 : 7.1e-6) + (row_wgs > 256 ? row_wgs / 256 : 1.0) * (w4 ? 2.7e-9 : 3.4e-9) * K;
   for (const Cand& c : cands) {
@@ -440,7 +443,30 @@ PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
                        (S > 1 ? 1.45e-6 * S + 12e-9 * wgs + 0.1e-12 * tile_bytes : 0.0);
       if (t < best_t) {
         best_t = t;
-        best = PfPlan{true, c.shape, S};
+        best = PfPlan{true, c.shape, S, 0};
+      }
+    }
+    // Balanced schedule: every CU slot gets the same run of (tile, K tile) units,
+    // crossing tile boundaries.  A tile split over two workgroups moves about 1.8
+    // fp32 partial tiles (one store, two when both pieces end together, and one
+    // load), at about 0.22 us per MB, plus about 2 us for the second piece's
+    // pipeline start (measured, W8 and W4, M = 2048: 2048x6144 in 192 tiles, where
+    // this loses to one tile per workgroup, and 4096x12288 in 384 tiles, where it
+    // wins by 9 %).
+    const long long slots = 256LL * c.per_cu;
+    const long long units = tiles * nk;
+    if (tiles % slots != 0 && tiles > slots / 2 &&
+        tiles <= (long long)(kCounterBytes / sizeof(unsigned)) &&
+        (double)tiles * 2 * waves * 128 * 64 * sizeof(float) <= (double)part_cap) {
+      const int sk = (int)((units + slots - 1) / slots);
+      if (prefill_balanced_ok(tiles, nk, sk)) {
+        const int occ = c.per_cu > 1 ? 2 : 1;
+        const double xbytes = 1.8 * (double)tiles * bm * bn * sizeof(float);
+        const double t = 5e-6 + sk * c.t_tile[occ - 1] * w4f + 2e-6 + 0.22e-12 * xbytes;
+        if (t < best_t) {
+          best_t = t;
+          best = PfPlan{true, c.shape, 1, sk};
+        }
       }
     }
   }
@@ -494,17 +520,20 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
     t.splits = 1;
     t.part = nullptr;
     t.cnt = nullptr;
+    t.sk = 0;
     if (fits32) {
       PfPlan p = plan_prefill(wk, M, K, N, part_cap);
       if (getenv("QLIN_PREFILL_VERBOSE"))
-        fprintf(stderr, "qlin prefill plan M=%d K=%d N=%d: %s shape=%d splits=%d\n", M, K, N,
-                p.tiled ? "tiled" : "skinny", p.shape, p.splits);
+        fprintf(stderr, "qlin prefill plan M=%d K=%d N=%d: %s shape=%d splits=%d sk=%d\n", M, K, N,
+                p.tiled ? "tiled" : "skinny", p.shape, p.splits, p.sk);
       const char* e = getenv("QLIN_PREFILL_SHAPE");
       const char* e2 = getenv("QLIN_PREFILL_SPLITS");
-      if ((e && *e) || (e2 && *e2)) {
+      const char* e3 = getenv("QLIN_PREFILL_SK");
+      if ((e && *e) || (e2 && *e2) || (e3 && *e3)) {
         p.tiled = true;
         if (e && *e) p.shape = atoi(e);
         p.splits = (e2 && *e2) ? atoi(e2) : 1;
+        p.sk = (e3 && *e3) ? atoi(e3) : 0;
         int bm, bn, waves;
         prefill_geometry(p.shape, &bm, &bn, &waves);
         const size_t tiles = (size_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
@@ -514,10 +543,15 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
             (p.splits > 1 && (tiles * p.splits * waves * 128 * 64 * sizeof(float) > part_cap ||
                               tiles > kCounterBytes / sizeof(unsigned))))
           return fail(QLIN_ERR_UNSUPPORTED, "%s: QLIN_PREFILL_SPLITS=%d unusable here", fn, p.splits);
+        if (p.sk != 0 && (p.sk < 0 || p.splits != 1 || !prefill_balanced_ok((long long)tiles, K / 64, p.sk) ||
+                          tiles * 2 * waves * 128 * 64 * sizeof(float) > part_cap ||
+                          tiles > kCounterBytes / sizeof(unsigned)))
+          return fail(QLIN_ERR_UNSUPPORTED, "%s: QLIN_PREFILL_SK=%d unusable here", fn, p.sk);
       }
       if (p.tiled || force_tiled) {
         t.splits = p.splits;
-        if (p.splits > 1) {
+        t.sk = p.sk;
+        if (p.splits > 1 || p.sk > 0) {
           t.cnt = (unsigned*)ws;
           t.part = (float*)((char*)ws + kCounterBytes);
         }

@@ -115,25 +115,35 @@ void prefill_kernel(const TlArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
 
-  const int tid = threadIdx.x;
+  const int M = a.M, N = a.N, K = a.K;
+  const int tiles_m = (M + G::BM - 1) / G::BM, tiles_n = (N + BN - 1) / BN;
+  __shared__ int s_last;
+
+  // One piece of work: K tiles kb .. kb + nk - 1 of output tile `tile`, shared by xs
+  // workgroups (1: no exchange).  Split-K (pair = false): xs splits, partial slot
+  // xslot, the last to arrive sums every slot in split order.  Balanced schedule
+  // (pair = true): xs <= 2, slot 0 holds the piece that starts at K = 0, and the last
+  // to arrive adds the other piece's partial to its own accumulators.
+  auto run = [&](const int tile, const int kb, const int nk, const int xs, const int xslot, const bool pair) {
+  // The thread index goes through an empty asm so that nothing derived from it is
+  // hoisted out of the balanced schedule's loop over pieces (which would keep those
+  // values live across every piece and spill).
+  int tid = (int)threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int wave = (int)rfl((uint32_t)tid >> 6), lane = tid & 63;  // wave index in an SGPR
   const int j = lane & 15, g = lane >> 4;
   const int kg = wave / (WM * WN);  // K group: with KG = 2, group kg computes substep kg
   const int wl = wave % (WM * WN);  // wave within its group
   const int wm = wl / WN, wn = wl % WN;
-  const int M = a.M, N = a.N, K = a.K;
-
   // grouped tile order: consecutive workgroups share weight column tiles in L2
-  const int tiles_m = (M + G::BM - 1) / G::BM, tiles_n = (N + BN - 1) / BN;
-  const int S = a.splits;
-  const int split = blockIdx.x % S;
-  const int tile = blockIdx.x / S;
+  // (the balanced schedule numbers tiles row by row: its workgroups already run
+  // consecutive tiles on one XCD)
   const int pid = tile;
   const int per_group = GROUP_M * tiles_n;
   const int first_m = (pid / per_group) * GROUP_M;
   const int gsize = min(tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (pid % per_group) % gsize;
-  const int tn = (pid % per_group) / gsize;
+  const int tm = pair ? pid / tiles_n : first_m + (pid % per_group) % gsize;
+  const int tn = pair ? pid % tiles_n : (pid % per_group) / gsize;
   const int m0 = tm * G::BM, n0 = tn * BN;
 
   // activation copies: block q of this wave = rows 8 * blk .. +7; lane -> row
@@ -290,9 +300,7 @@ void prefill_kernel(const TlArgs a) {
     }
   };
 
-  // this workgroup's K tiles: kb .. kb + nk - 1
-  const int nk = K / BK / S;
-  const int kb = split * nk;
+  // this piece's K tiles: kb .. kb + nk - 1
 #pragma unroll
   for (int u = 0; u < NSTAGE - 1; ++u) issue(kb + min(u, nk - 1), u);
   // With one wave per SIMD (registers to spare) the loops below are unrolled by
@@ -388,46 +396,79 @@ void prefill_kernel(const TlArgs a) {
     }
   }
 
-  if (S > 1) {
+  if (xs > 1) {
     // Partial tile of this wave: the float4 (rb, t) of every lane at byte
     // ((rb * 4 + t) * 64 + lane) * 16 of the wave's slot, so each store or load
     // instruction moves 1 KiB contiguous.  Device-coherent (SC1) stores and loads;
-    // each workgroup's stores complete before it counts its arrival.
-    __shared__ int s_last;
+    // each workgroup's stores complete before it signals.
     constexpr unsigned kSlot = 128u * 64u * 4u;  // bytes of one wave's partial tile
     const __amdgpu_buffer_rsrc_t rs =
-        part_rsrc(a.part + (long long)tile * S * G::WAVES * (128 * 64), (unsigned)(S * G::WAVES) * kSlot);
+        part_rsrc(a.part + (long long)tile * xs * G::WAVES * (128 * 64), (unsigned)(xs * G::WAVES) * kSlot);
     const unsigned lane_off = (unsigned)lane * 16u;
-    if (kg == 0) {
-      const unsigned base = (unsigned)(split * G::WAVES + wl) * kSlot + lane_off;
+    auto store_partial = [&]() {
+      if (kg == 0) {
+        const unsigned base = (unsigned)(xslot * G::WAVES + wl) * kSlot + lane_off;
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) st_coherent(acc[rb][t], rs, base + (unsigned)(rb * 4 + t) * 1024u);
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __syncthreads();
+    };
+    if (!pair) {
+      store_partial();
+      if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (unsigned)(xs - 1);
+        if (last) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+      __syncthreads();
+      if (!s_last || kg != 0) return;  // uniform over each wave
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      // the last workgroup sums the partials in split order: 32 independent loads per split
+      for (int sp = 0; sp < xs; ++sp) {
+        const unsigned base = (unsigned)(sp * G::WAVES + wl) * kSlot + lane_off;
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const f32x4 v = ld_coherent(rs, base + (unsigned)(rb * 4 + t) * 1024u);
+            acc[rb][t] = (sp == 0) ? v : acc[rb][t] + v;
+          }
+      }
+    } else {
+      // Two pieces, one bit each in the tile's word: bit p = piece p's partial is
+      // stored.  A piece that finds the other's bit set finishes the tile at once,
+      // with no store of its own; otherwise it stores its partial, sets its bit and
+      // finishes the tile only if the other's bit was set meanwhile.  The atomics on
+      // the word are ordered, so exactly one piece finishes, and nothing waits.  The
+      // finisher adds the other's partial to its own accumulators (the fp32 sum of
+      // two values does not depend on their order, so neither does the result on
+      // which piece finishes) and clears the word.
+      const unsigned mine = 1u << xslot, other = 1u << (1 - xslot);
+      if (tid == 0)
+        s_last = (__hip_atomic_fetch_or(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & other) ? 1 : 0;
+      __syncthreads();
+      if (!s_last) {  // uniform
+        store_partial();
+        if (tid == 0)
+          s_last =
+              (__hip_atomic_fetch_or(a.cnt + tile, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & other) ? 1 : 0;
+        __syncthreads();
+        if (!s_last) return;
+      }
+      if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (kg != 0) return;
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      const unsigned base = (unsigned)((1 - xslot) * G::WAVES + wl) * kSlot + lane_off;
 #pragma unroll
       for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) st_coherent(acc[rb][t], rs, base + (unsigned)(rb * 4 + t) * 1024u);
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = prev == (unsigned)(S - 1);
-      if (last) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
-    }
-    __syncthreads();
-    if (!s_last || kg != 0) return;  // uniform over each wave
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    // the last workgroup sums the partials in split order: 32 independent loads per split
-    for (int sp = 0; sp < S; ++sp) {
-      const unsigned base = (unsigned)(sp * G::WAVES + wl) * kSlot + lane_off;
-#pragma unroll
-      for (int rb = 0; rb < 8; ++rb)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f32x4 v = ld_coherent(rs, base + (unsigned)(rb * 4 + t) * 1024u);
-          acc[rb][t] = (sp == 0) ? v : acc[rb][t] + v;
-        }
+        for (int t = 0; t < 4; ++t) acc[rb][t] = acc[rb][t] + ld_coherent(rs, base + (unsigned)(rb * 4 + t) * 1024u);
     }
   }
 
@@ -486,12 +527,43 @@ void prefill_kernel(const TlArgs a) {
     if (a.res) store_all(F{}, T{});
     else store_all(F{}, F{});
   }
+  };
+
+  const int nkt = K / BK;  // K tiles of one output tile
+  if (a.sk == 0) {
+    // one tile per workgroup, or `splits` workgroups per tile over equal K ranges
+    const int S = a.splits;
+    const int nk = nkt / S;
+    run((int)blockIdx.x / S, ((int)blockIdx.x % S) * nk, nk, S, (int)blockIdx.x % S, false);
+    return;
+  }
+  // Balanced schedule: the (tile, K tile) units in order, a.sk consecutive units per
+  // workgroup, so every workgroup does the same work when the tiles alone would leave
+  // CUs idle.  The host only picks it when no tile spans more than two workgroups.
+  // Workgroups go to the 8 XCDs in turn; with a multiple of 8 of them, workgroup b
+  // takes range (b % 8) * (W / 8) + b / 8, so each XCD runs one contiguous eighth of
+  // the units (whole rows of tiles when there are 8 row tiles: one activation block
+  // per XCD L2), and the two pieces of a tile run on the same XCD.
+  const int total = tiles_m * tiles_n * nkt;
+  const int W = (int)gridDim.x;
+  const int v = (W % 8 == 0) ? ((int)blockIdx.x % 8) * (W / 8) + (int)blockIdx.x / 8 : (int)blockIdx.x;
+  const int beg = v * a.sk, end = min(beg + a.sk, total);
+  for (int pos = beg; pos < end;) {
+    const int tile = pos / nkt, kb = pos - tile * nkt;
+    const int ke = min(nkt, end - tile * nkt);
+    const int c0 = tile * nkt / a.sk, c1 = (tile * nkt + nkt - 1) / a.sk;  // workgroups on the tile
+    if (pos != beg) __syncthreads();  // the previous piece's LDS reads are done before new copies
+    run(tile, kb, ke - kb, c1 - c0 + 1, kb == 0 ? 0 : 1, true);
+    pos = tile * nkt + ke;
+  }
 }
 
 template <int WK, bool HZ, int WM, int WN, int KG, int NS>
 static hipError_t launch_prefill_t(const TlArgs& a, hipStream_t st) {
   using G = Geo<WK, WM, WN, KG, NS>;
-  const int tiles = ((a.M + G::BM - 1) / G::BM) * ((a.N + G::BN - 1) / G::BN) * a.splits;
+  const long long tiles = (long long)((a.M + G::BM - 1) / G::BM) * ((a.N + G::BN - 1) / G::BN);
+  const long long units = tiles * (a.K / BK);
+  const int wgs = (int)(a.sk > 0 ? (units + a.sk - 1) / a.sk : tiles * a.splits);
   const size_t lds = (size_t)G::NSTAGE * G::STAGE;
   static bool attr_set = false;  // benign race: every caller sets the same value
   if (!attr_set) {
@@ -500,7 +572,7 @@ static hipError_t launch_prefill_t(const TlArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((prefill_kernel<WK, HZ, WM, WN, KG, NS>), dim3(tiles), dim3(G::THREADS), lds, st, a);
+  hipLaunchKernelGGL((prefill_kernel<WK, HZ, WM, WN, KG, NS>), dim3(wgs), dim3(G::THREADS), lds, st, a);
   return hipGetLastError();
 }
 
@@ -521,6 +593,15 @@ void prefill_geometry(int shape, int* bm, int* bn, int* waves) {
 }
 
 bool prefill_shape_ok(int shape) { return shape >= 0 && shape < PF_SHAPES; }
+
+bool prefill_balanced_ok(long long tiles, int nkt, int sk) {
+  if (sk < 2 || nkt < 1) return false;
+  for (long long t = 0; t < tiles; ++t) {
+    const long long u0 = t * nkt, u1 = u0 + nkt - 1;
+    if (u1 / sk - u0 / sk > 1) return false;  // three or more workgroups on the tile
+  }
+  return true;
+}
 
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t st) {
   switch (shape) {

@@ -81,6 +81,8 @@ struct TlArgs {
   int splits;         // workgroups per output tile along K
   float* part;        // split-K partials [tiles][splits][waves][128 * 64], or nullptr
   unsigned* cnt;      // split-K arrival counters [tiles], zero between calls
+  int sk;             // balanced schedule: K tiles per workgroup over all tiles (0 = off);
+                      // partials [tiles][2][waves][128 * 64]
 };
 
 // LDS-DMA prefill kernel; `shape` picks the workgroup tile (rows x columns):
@@ -88,6 +90,9 @@ struct TlArgs {
 // wave groups split every K tile's substeps: 4 waves).
 enum PrefillShape { PF_128x128 = 0, PF_256x256 = 1, PF_128x128_K2 = 2, PF_SHAPES = 3 };
 hipError_t launch_prefill(const TlArgs& a, int wk, bool hz, int shape, hipStream_t stream);
+// whether the balanced schedule with sk K tiles per workgroup gives every output tile
+// at most two workgroups
+bool prefill_balanced_ok(long long tiles, int nkt, int sk);
 // rows, columns and waves of a prefill workgroup tile
 void prefill_geometry(int shape, int* bm, int* bn, int* waves);
 bool prefill_shape_ok(int shape);

@@ -442,6 +442,42 @@ def test_prefill_split_k(shape, splits, monkeypatch):
     assert torch.equal(_run_w4(x, packed, s4, z, out_dtype=torch.bfloat16), y4)
 
 
+@pytest.mark.parametrize("shape,sk", [(1, 16), (1, 24), (1, 31), (1, 37), (1, 40), (0, 24), (2, 31), (2, 37)])
+def test_prefill_balanced(shape, sk, monkeypatch):
+    """Balanced schedule: workgroup i covers the (tile, K tile) units
+    [i*sk, (i+1)*sk) in order, so it may finish one tile and go on to the next; a
+    tile shared by two workgroups is finished by the last to arrive, which adds the
+    other's partial.  With 32 K tiles per tile: sk=16 halves every tile, sk=31 leaves
+    one-K-tile pieces, sk=37 gives some workgroups three pieces, and sk=40 (8
+    workgroups) and the 128x128 case (40) take the XCD-ordered ranges.  Checked against the
+    oracle (W8 with residual, W4 with zeros and bf16 out) and for bit-identical
+    repeat calls."""
+    _force_tiled(monkeypatch, shape)
+    monkeypatch.setenv("QLIN_PREFILL_SK", str(sk))
+    M, K, N = 300, 2048, 1280
+    x = H.act_f16(M, K, seed=370 + sk)
+    w, s = H.w8(K, N, seed=371)
+    res = torch.randn((M, N), generator=H.gen(372)).to(torch.float16)
+    y = _run_w8(x, w, s, residual=res)
+    H.assert_out_close(y, H.linear_w8_ref_cols(x, w, s, np.arange(N), residual=res))
+    for _ in range(2):
+        assert torch.equal(_run_w8(x, w, s, residual=res), y)
+    packed, s4, z = H.w4(K, N, seed=373, group=128, zeros="random")
+    y4 = _run_w4(x, packed, s4, z, out_dtype=torch.bfloat16)
+    H.assert_out_close(y4, H.linear_w4_ref_cols(x, packed, s4, z, np.arange(N)))
+    assert torch.equal(_run_w4(x, packed, s4, z, out_dtype=torch.bfloat16), y4)
+
+
+def test_prefill_balanced_rejects_three_way_tiles(monkeypatch):
+    """sk=12 would spread a 32-K-tile output tile over three workgroups: refused."""
+    _force_tiled(monkeypatch, 1)
+    monkeypatch.setenv("QLIN_PREFILL_SK", "12")
+    x = H.act_f16(300, 2048, seed=380)
+    w, s = H.w8(2048, 1280, seed=381)
+    with pytest.raises(ValueError, match="QLIN_PREFILL_SK"):
+        _run_w8(x, w, s)
+
+
 @pytest.mark.parametrize("shape", [0, 1, 2])
 def test_prefill_rows_independent_of_chunking(shape, monkeypatch):
     """Rows computed in one M=300 call equal the same rows computed as an M=100
@@ -503,6 +539,28 @@ def test_config3_prefill_full_size(kind, K, N):
         packed, s, z = H.w4(K, N, seed=502)
         y = _run_w4(x, packed, s, z)
         y2 = _run_w4((x * 2).to(torch.float16), packed, s, z)
+        ref = H.linear_w4_ref_cols(x, packed, s, z, cols)
+    H.assert_out_close(y.cpu()[:, cols], ref)
+    _assert_doubled(y, y2)
+
+
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+def test_prefill_balanced_default_plan_full_size(kind):
+    """M = 2048 on the 9B-class gate shape (4096 x 12288): 384 tiles of 256x256 would
+    take one and a half rounds of the chip, so the planner picks the balanced
+    schedule (96 K tiles per workgroup, every other tile shared by two workgroups).
+    Sampled columns against the oracle, and the activation-doubling property over the
+    whole output."""
+    M, K, N = 2048, 4096, 12288
+    x = H.act_f16(M, K, seed=520)
+    cols = H.sample_cols(N, 256, seed=521)
+    if kind == "w8":
+        w, s = H.w8(K, N, seed=522)
+        y, y2 = _run_w8(x, w, s), _run_w8((x * 2).to(torch.float16), w, s)
+        ref = H.linear_w8_ref_cols(x, w, s, cols)
+    else:
+        packed, s, z = H.w4(K, N, seed=522)
+        y, y2 = _run_w4(x, packed, s, z), _run_w4((x * 2).to(torch.float16), packed, s, z)
         ref = H.linear_w4_ref_cols(x, packed, s, z, cols)
     H.assert_out_close(y.cpu()[:, cols], ref)
     _assert_doubled(y, y2)
