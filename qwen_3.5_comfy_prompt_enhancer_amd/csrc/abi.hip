@@ -83,11 +83,16 @@ void plan_override(const Problem& P, int& cols, int& waves, int& upw) {
 int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
                     hipStream_t stream) {
   // Engine-signature stores with more than 16 rows (prefill chunks): the tiled int8
-  // kernel where it applies and a time model fitted to MI355X measurements prefers it
-  // to the 16-row tiles:
-  //   tiled:  4 us + rounds of 256 workgroups x 128-wide K stages x 1.5 us
-  //   rows:   10 us + 7 ns per row per MB of int8-sized weights
-  // QLIN_ENGINE_PREFILL ("tiled" or "skinny") overrides the choice (tests, tuning).
+  // kernel where it applies and a time model fitted to MI355X measurements (M = 512,
+  // W8 and W4, K x N = 2048 x 2048, 6144 x 2048, 2048 x 8192, every plan forced)
+  // prefers it to the 16-row tiles:
+  //   tiled:  7 us + rounds of 256 workgroups x 128-wide K stages x 1.1 us (x 1.4 W4)
+  //           x weight sets + split-K exchange (store epilogue): 1.45 us per split
+  //           + 12 ns per workgroup + 0.1 us per MB of partial tiles; a split level
+  //           is tried only while the level below it leaves CUs idle
+  //   rows:   5 us + 6.9 ns per row per MB of int8-sized weights (W4: 4.3 us, 6.5 ns)
+  // QLIN_ENGINE_PREFILL ("tiled" or "skinny") and QLIN_ENGINE_SPLITS override the
+  // choice (tests, tuning).
   if (P.act == ACT_I8 && prefill_i8_ok(a, P.wk, P.epi)) {
     const char* e = getenv("QLIN_ENGINE_PREFILL");
     const bool force_rows = e && strcmp(e, "skinny") == 0;
@@ -95,11 +100,39 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
     long long tiles_n = 0;
     for (int s = 0; s < (P.epi == EPI_STORE ? a.nseg : 1); ++s) tiles_n += a.seg[s].n / 128;
     const long long tiles = (long long)((P.M + 127) / 128) * tiles_n;
-    // gate/up computes two weight sets per tile
-    const double t_tiled = 4e-6 + (double)((tiles + 255) / 256) * ((P.K / 64 + 1) / 2) * 1.5e-6 * P.nsets;
-    const double t_rows = 10e-6 + 7e-9 * P.M * ((double)P.K * P.ncols * P.nsets / 1e6);
-    if (force_tiled || (!force_rows && t_tiled < t_rows))
+    const int nb = P.K / 64;
+    const size_t part_cap = (workspace && ws_bytes > kCounterBytes) ? ws_bytes - kCounterBytes : 0;
+    auto split_fits = [&](int S) {
+      return P.epi == EPI_STORE && S >= 1 && nb % S == 0 &&
+             (S == 1 || ((size_t)tiles * S * 128 * 128 * sizeof(float) <= part_cap &&
+                         (size_t)tiles <= kCounterBytes / sizeof(unsigned)));
+    };
+    const double t_stage = (P.wk == WK_W4 ? 1.4 : 1.0) * 1.1e-6 * P.nsets;  // gate/up: two weight sets
+    double t_tiled = 7e-6 + (double)((tiles + 255) / 256) * ((nb + 1) / 2) * t_stage;
+    int splits = 1;
+    for (int S = 2; S <= 8; S *= 2) {
+      if (!split_fits(S) || nb / S < 2 || tiles * (S / 2) >= 256) break;
+      const long long wgs = tiles * S;
+      const double t = 7e-6 + (double)((wgs + 255) / 256) * ((nb / S + 1) / 2) * t_stage + 1.45e-6 * S +
+                       12e-9 * wgs + 0.1e-12 * (double)wgs * 128 * 128 * sizeof(float);
+      if (t < t_tiled) {
+        t_tiled = t;
+        splits = S;
+      }
+    }
+    const char* es = getenv("QLIN_ENGINE_SPLITS");  // store epilogue only
+    if (es && *es && P.epi == EPI_STORE) {
+      splits = atoi(es);
+      if (!split_fits(splits)) return fail(QLIN_ERR_UNSUPPORTED, "%s: QLIN_ENGINE_SPLITS=%d unusable here", fn, splits);
+    }
+    const double t_rows = (P.wk == WK_W4 ? 4.3e-6 : 5e-6) +
+                          (P.wk == WK_W4 ? 6.5e-9 : 6.9e-9) * P.M * ((double)P.K * P.ncols * P.nsets / 1e6);
+    if (force_tiled || (!force_rows && t_tiled < t_rows)) {
+      a.splits = splits;
+      a.cnt = splits > 1 ? (unsigned*)workspace : nullptr;
+      a.part = splits > 1 ? (float*)((char*)workspace + kCounterBytes) : nullptr;
       return hip_status(fn, launch_prefill_i8(a, P.wk, P.hz, P.epi, stream));
+    }
   }
   SkLaunch L;
   L.act = P.act;

@@ -83,11 +83,15 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   const int j = lane & 15, g = lane >> 4;
   const int kg = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
   const int M = a.M, K = a.K;
-  const int nk = K / 64;
+  // split-K (store epilogue): `S` workgroups per output tile, each over nk
+  // consecutive 64-wide blocks from kb0
+  const int S = (EPI == EPI_STORE) ? a.splits : 1;
+  const int tile = (int)blockIdx.x / S, split = (int)blockIdx.x % S;
+  const int nk = K / 64 / S;
+  const int kb0 = split * nk;
 
   // grouped tile order
   const int tiles_m = (M + BM - 1) / BM, tiles_n = a.ntiles;
-  const int tile = blockIdx.x;
   const int per_group = GROUP_M * tiles_n;
   const int grp = tile / per_group;
   const int first_m = grp * GROUP_M;
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
     for (int i = 0; i < 2; ++i) {
       const int q = tid + THREADS * i;
       const int k2 = q >> 9, r = (q & 511) >> 2, c = q & 3;
-      const int blk = min(2 * st + k2, nk - 1);
+      const int blk = kb0 + min(2 * st + k2, nk - 1);
       const int row = min(m0 + r, M - 1);
       rg.av[i] = *(const u32x4*)(xq + (long long)row * K + blk * 64 + 16 * c);
     }
@@ -139,21 +143,21 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
     for (int s = 0; s < NS; ++s) {
       if constexpr (W4) {
         const int k2 = tid >> 8, r = (tid & 255) >> 3, c = tid & 7;
-        const int blk = min(2 * st + k2, nk - 1);
+        const int blk = kb0 + min(2 * st + k2, nk - 1);
         rg.bv[s][0] = *(const u32x4*)(wset[s] + (long long)(blk * 32 + r) * n + ncol0 + 16 * c);
       } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int q = tid + THREADS * i;
           const int k2 = q >> 9, r = (q & 511) >> 3, c = q & 7;
-          const int blk = min(2 * st + k2, nk - 1);
+          const int blk = kb0 + min(2 * st + k2, nk - 1);
           rg.bv[s][i] = *(const u32x4*)(wset[s] + (long long)(blk * 64 + r) * n + ncol0 + 16 * c);
         }
       }
     }
     if (tid < 256) {
       const int k2 = tid >> 7, r = tid & 127;
-      const int blk = min(2 * st + k2, nk - 1);
+      const int blk = kb0 + min(2 * st + k2, nk - 1);
       rg.as_ = a.xs[(long long)min(m0 + r, M - 1) * NG + blk];
     }
     if constexpr (W4) {
@@ -162,7 +166,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
       const int s = tid >> 8;
       if (s < NS) {
         const int t2 = tid & 255, k2 = t2 >> 7, c = t2 & 127;
-        const int blk = min(2 * st + k2, nk - 1);
+        const int blk = kb0 + min(2 * st + k2, nk - 1);
         const long long gi = (long long)(blk * 64 / a.group) * n + ncol0 + c;
         rg.bs = ld_scale1_raw(sset[s], a.sdt, gi);  // converted at the LDS store
         if constexpr (HZ) rg.bz = zset[s][gi];
@@ -365,6 +369,49 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
           for (int r = 0; r < 4; ++r) acc[s][rb][t][r] += red[((rb * 4 + t) * 4 + r) * 64];
     }
   }
+  if constexpr (EPI == EPI_STORE) {
+    if (S > 1) {
+      // Split-K: group 0's partial tile (wave w: the float4 (rb, t) of every lane at
+      // byte ((rb * 4 + t) * 64 + lane) * 16 of its 16 KB slot) goes out through
+      // device-coherent stores; each workgroup's stores complete before it counts its
+      // arrival, and the last to arrive sums the partials in split order.
+      __shared__ int s_last;
+      constexpr unsigned kSlot = 64u * 64u * 4u;
+      const __amdgpu_buffer_rsrc_t rs =
+          part_rsrc(a.part + (long long)tile * S * 4 * (64 * 64), (unsigned)(S * 4) * kSlot);
+      const unsigned lane_off = (unsigned)lane * 16u;
+      if (kg == 0) {
+        const unsigned base = (unsigned)(split * 4 + (wave & 3)) * kSlot + lane_off;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) st_coherent(acc[0][rb][t], rs, base + (unsigned)(rb * 4 + t) * 1024u);
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __syncthreads();
+      if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (unsigned)(S - 1);
+        if (last) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+      __syncthreads();
+      if (!s_last || kg != 0) return;  // uniform over each wave
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      for (int sp = 0; sp < S; ++sp) {
+        const unsigned base = (unsigned)(sp * 4 + (wave & 3)) * kSlot + lane_off;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const f32x4 v = ld_coherent(rs, base + (unsigned)(rb * 4 + t) * 1024u);
+            acc[0][rb][t] = (sp == 0) ? v : acc[0][rb][t] + v;
+          }
+      }
+    }
+  }
   if (kg != 0) return;
 
   // ---------------- epilogue ----------------
@@ -511,7 +558,8 @@ hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t st)
     tn = a.seg[0].n / BN;
   }
   a.ntiles = tn;
-  const int tiles = ((a.M + BM - 1) / BM) * tn;
+  if (epi != EPI_STORE || a.splits < 1) a.splits = 1;  // split-K: store epilogue only
+  const int tiles = ((a.M + BM - 1) / BM) * tn * a.splits;
   switch (epi) {
     case EPI_STORE: return launch_i8_e<EPI_STORE>(a, wk, hz, tiles, st);
     case EPI_GATEUP: return launch_i8_e<EPI_GATEUP>(a, wk, hz, tiles, st);

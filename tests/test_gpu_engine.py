@@ -350,10 +350,76 @@ def test_prefill_outside_tiled_kernel(N, group, tiled):
     H.assert_out_close(out, ref)
 
 
-@pytest.mark.parametrize("M,K,N", [(512, 2048, 6144), (512, 6144, 2048)])
+@pytest.mark.parametrize("splits", [2, 4, 8])
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+def test_gemm_prefill_tiled_split_k(kind, splits, tiled):
+    """Split-K on the tiled int8 kernel (store epilogue): each of `splits` workgroups
+    per tile covers K/splits, and the last to arrive sums the fp32 partials in split
+    order.  W8 with the residual in place, W4 with zeros; against the oracle and
+    bit-identical on repeat calls (the arrival order must not matter)."""
+    gemm, _ = _g()
+    tiled.setenv("QLIN_ENGINE_SPLITS", str(splits))
+    M, K, N = 300, 2048, 1024
+    a, as_ = H.engine_act(M, K, seed=480 + splits)
+    hid = torch.randn((M, N), generator=H.gen(481)).to(torch.bfloat16)
+    if kind == "w8":
+        b, bs = H.engine_w8(K, N, seed=482)
+        bz = None
+        ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy(), bs.numpy(), residual=_bf16(hid))
+    else:
+        b, bs, bz = _w4_engine(K, N, seed=482, zeros="random")
+        ref = R.gemm_w4_ref(a.numpy(), as_.numpy(), b.numpy(), _bf16(bs), bz.numpy(), residual=_bf16(hid))
+    cu = lambda t: None if t is None else t.cuda()
+    outs = []
+    for _ in range(3):
+        h = hid.cuda()
+        gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), h, residual=h, b_z=cu(bz))
+        outs.append(h)
+    H.assert_out_close(outs[0], ref)
+    assert torch.equal(outs[1], outs[0]) and torch.equal(outs[2], outs[0])
+
+
+def test_proj3_prefill_tiled_split_k(tiled):
+    """proj3 (three column segments in one launch) with split-K on the tiled kernel."""
+    gemm, _ = _g()
+    tiled.setenv("QLIN_ENGINE_SPLITS", "4")
+    M, K = 200, 1024
+    a, as_ = H.engine_act(M, K, seed=485)
+    ws = [H.engine_w8(K, n, seed=486 + i) for i, n in enumerate((1024, 256, 256))]
+    out = torch.empty((M, 1536), dtype=torch.bfloat16, device="cuda")
+    gemm.proj3(a.cuda(), as_.cuda(), *(t.cuda() for w in ws for t in w), out)
+    ref = R.proj3_ref(a.numpy(), as_.numpy(), *(t.numpy() for w in ws for t in w))
+    H.assert_out_close(out, ref)
+
+
+def test_prefill_tiled_split_k_rows_independent_of_chunking(tiled):
+    """With a fixed split count the K order of a row does not depend on M either."""
+    gemm, _ = _g()
+    tiled.setenv("QLIN_ENGINE_SPLITS", "4")
+    K, N = 2048, 1024
+    a, as_ = H.engine_act(300, K, seed=487)
+    b, bs = H.engine_w8(K, N, seed=488)
+    y = torch.empty((300, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y)
+    yc = torch.empty((100, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a[100:200].contiguous().cuda(), as_[100:200].contiguous().cuda(), b.cuda(), bs.cuda(), yc)
+    assert torch.equal(y[100:200], yc)
+
+
+def test_prefill_tiled_bad_split_raises(tiled):
+    gemm, _ = _g()
+    tiled.setenv("QLIN_ENGINE_SPLITS", "3")  # 32 blocks of 64 do not split three ways
+    a, as_ = H.engine_act(64, 2048, seed=489)
+    b, bs = H.engine_w8(2048, 1024, seed=489)
+    out = torch.empty((64, 1024), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="QLIN_ENGINE_SPLITS"):
+        gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 6144), (512, 6144, 2048), (512, 2048, 2048)])
 def test_engine_prefill_default_dispatch(M, K, N):
-    """Engine prefill chunk sizes with the library's own choice of kernel (tiled int8
-    for the wide shape, 16-row tiles for the deep one), sampled columns."""
+    """Engine prefill chunk sizes with the library's own choice of kernel (tiled int8,
+    split over K for the narrow shapes), sampled columns."""
     gemm, _ = _g()
     a, as_ = H.engine_act(M, K, seed=460)
     b, bs = H.engine_w8(K, N, seed=461)
@@ -390,13 +456,12 @@ def test_mlp_gate_up_quant_w4_prefill_tiled(zeros, group, tiled):
     _fused_vs_unfused(96, w4_=True, zeros=zeros, group=group)
 
 
-@pytest.mark.parametrize("M", [1, 4, 512])
-def test_engine_scale_property_full_size(M):
+@pytest.mark.parametrize("M,K,N", [(1, 2048, 6144), (4, 2048, 6144), (512, 2048, 6144), (512, 6144, 2048)])
+def test_engine_scale_property_full_size(M, K, N):
     """Doubling the per-64 activation scales doubles every bf16 output exactly (the
-    int32 dots are unchanged and the fp32 fold and the rounding commute with 2), over
-    the whole 2048 x 6144 output at decode and prefill-chunk sizes."""
+    int32 dots are unchanged and the fp32 fold, the split-K sum and the rounding
+    commute with 2), over the whole output at decode and prefill-chunk sizes."""
     gemm, _ = _g()
-    K, N = 2048, 6144
     a, as_ = H.engine_act(M, K, seed=490 + M)
     b, bs = H.engine_w8(K, N, seed=491)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
