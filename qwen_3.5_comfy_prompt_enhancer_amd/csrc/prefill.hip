@@ -105,7 +105,7 @@ __device__ __forceinline__ _Float16 scale_f16(uint32_t bits, int dt) {
 
 }  // namespace
 
-template <int WK, bool HZ, int WM, int WN, int KG, int NS>
+template <int WK, bool HZ, int WM, int WN, int KG, int NS, bool BAL>
 __global__ __launch_bounds__(64 * WM * WN * KG)
 __attribute__((amdgpu_waves_per_eu(Geo<WK, WM, WN, KG, NS>::OCC, Geo<WK, WM, WN, KG, NS>::OCC)))
 void prefill_kernel(const TlArgs a) {
@@ -125,11 +125,11 @@ void prefill_kernel(const TlArgs a) {
   // (pair = true): xs <= 2, slot 0 holds the piece that starts at K = 0, and the last
   // to arrive adds the other piece's partial to its own accumulators.
   auto run = [&](const int tile, const int kb, const int nk, const int xs, const int xslot, const bool pair) {
-  // The thread index goes through an empty asm so that nothing derived from it is
-  // hoisted out of the balanced schedule's loop over pieces (which would keep those
-  // values live across every piece and spill).
+  // In the balanced schedule (BAL) the thread index goes through an empty asm so that
+  // nothing derived from it is hoisted out of the loop over pieces (which would keep
+  // those values live across every piece and spill).
   int tid = (int)threadIdx.x;
-  asm volatile("" : "+v"(tid));
+  if constexpr (BAL) asm volatile("" : "+v"(tid));
   const int wave = (int)rfl((uint32_t)tid >> 6), lane = tid & 63;  // wave index in an SGPR
   const int j = lane & 15, g = lane >> 4;
   const int kg = wave / (WM * WN);  // K group: with KG = 2, group kg computes substep kg
@@ -530,7 +530,7 @@ void prefill_kernel(const TlArgs a) {
   };
 
   const int nkt = K / BK;  // K tiles of one output tile
-  if (a.sk == 0) {
+  if constexpr (!BAL) {
     // one tile per workgroup, or `splits` workgroups per tile over equal K ranges
     const int S = a.splits;
     const int nk = nkt / S;
@@ -558,7 +558,7 @@ void prefill_kernel(const TlArgs a) {
   }
 }
 
-template <int WK, bool HZ, int WM, int WN, int KG, int NS>
+template <int WK, bool HZ, int WM, int WN, int KG, int NS, bool BAL>
 static hipError_t launch_prefill_t(const TlArgs& a, hipStream_t st) {
   using G = Geo<WK, WM, WN, KG, NS>;
   const long long tiles = (long long)((a.M + G::BM - 1) / G::BM) * ((a.N + G::BN - 1) / G::BN);
@@ -567,20 +567,28 @@ static hipError_t launch_prefill_t(const TlArgs& a, hipStream_t st) {
   const size_t lds = (size_t)G::NSTAGE * G::STAGE;
   static bool attr_set = false;  // benign race: every caller sets the same value
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<WK, HZ, WM, WN, KG, NS>,
+    const hipError_t e = hipFuncSetAttribute((const void*)prefill_kernel<WK, HZ, WM, WN, KG, NS, BAL>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((prefill_kernel<WK, HZ, WM, WN, KG, NS>), dim3(wgs), dim3(G::THREADS), lds, st, a);
+  hipLaunchKernelGGL((prefill_kernel<WK, HZ, WM, WN, KG, NS, BAL>), dim3(wgs), dim3(G::THREADS), lds, st, a);
   return hipGetLastError();
 }
 
+template <int WM, int WN, int KG, int NS, bool BAL>
+static hipError_t launch_prefill_b(const TlArgs& a, int wk, bool hz, hipStream_t st) {
+  if (wk == WK_W8) return launch_prefill_t<WK_W8, false, WM, WN, KG, NS, BAL>(a, st);
+  if (hz) return launch_prefill_t<WK_W4, true, WM, WN, KG, NS, BAL>(a, st);
+  return launch_prefill_t<WK_W4, false, WM, WN, KG, NS, BAL>(a, st);
+}
+
+// the balanced schedule is its own instantiation, so the other plans compile as
+// they would without it
 template <int WM, int WN, int KG, int NS>
 static hipError_t launch_prefill_g(const TlArgs& a, int wk, bool hz, hipStream_t st) {
-  if (wk == WK_W8) return launch_prefill_t<WK_W8, false, WM, WN, KG, NS>(a, st);
-  if (hz) return launch_prefill_t<WK_W4, true, WM, WN, KG, NS>(a, st);
-  return launch_prefill_t<WK_W4, false, WM, WN, KG, NS>(a, st);
+  if (a.sk > 0) return launch_prefill_b<WM, WN, KG, NS, true>(a, wk, hz, st);
+  return launch_prefill_b<WM, WN, KG, NS, false>(a, wk, hz, st);
 }
 
 void prefill_geometry(int shape, int* bm, int* bn, int* waves) {
