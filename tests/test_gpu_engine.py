@@ -416,10 +416,12 @@ def test_prefill_tiled_bad_split_raises(tiled):
         gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)
 
 
-@pytest.mark.parametrize("M,K,N", [(512, 2048, 6144), (512, 6144, 2048), (512, 2048, 2048)])
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 6144), (512, 6144, 2048), (512, 2048, 2048), (384, 6144, 2048),
+                                   (100, 6144, 2048)])
 def test_engine_prefill_default_dispatch(M, K, N):
     """Engine prefill chunk sizes with the library's own choice of kernel (tiled int8,
-    split over K for the narrow shapes), sampled columns."""
+    split over K for the narrow shapes at M = 384 and 512; row tiles at M = 100),
+    sampled columns."""
     gemm, _ = _g()
     a, as_ = H.engine_act(M, K, seed=460)
     b, bs = H.engine_w8(K, N, seed=461)
