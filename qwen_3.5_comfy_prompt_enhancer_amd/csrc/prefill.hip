@@ -38,6 +38,10 @@
 //     arrival counter; the last to arrive sums the partials in split order (all
 //     loads of one split in flight together), resets the counter and runs the
 //     epilogue.  The sum order is fixed, so results are deterministic.
+//   * Balanced schedule (its own instantiation): when the tiles would leave CUs idle
+//     for a whole round, each workgroup takes the same run of (tile, K tile) units,
+//     crossing tile boundaries; a tile shared by two workgroups is finished by one of
+//     them, which adds the other's fp32 partial (one flag bit per piece, no waiting).
 //   * The K order of every output element is fixed (tiles in order, two 32-wide
 //     substeps each, partials summed in split order), so a row's result depends on
 //     the split count and the number of wave groups but not on M or the tile size.
@@ -122,8 +126,9 @@ void prefill_kernel(const TlArgs a) {
   // One piece of work: K tiles kb .. kb + nk - 1 of output tile `tile`, shared by xs
   // workgroups (1: no exchange).  Split-K (pair = false): xs splits, partial slot
   // xslot, the last to arrive sums every slot in split order.  Balanced schedule
-  // (pair = true): xs <= 2, slot 0 holds the piece that starts at K = 0, and the last
-  // to arrive adds the other piece's partial to its own accumulators.
+  // (pair = true): xs <= 2, slot 0 holds the piece that starts at K = 0, and one of
+  // the two pieces finishes the tile, adding the other's partial to its own
+  // accumulators.
   auto run = [&](const int tile, const int kb, const int nk, const int xs, const int xslot, const bool pair) {
   // In the balanced schedule (BAL) the thread index goes through an empty asm so that
   // nothing derived from it is hoisted out of the loop over pieces (which would keep
