@@ -27,8 +27,12 @@
 //     explicit zeros add (8 - z) * sum(a) from one more MFMA against all-ones.
 //   * Copies: global -> registers (three stages ahead, two for gate/up) -> LDS (one
 //     stage ahead), one barrier per stage.
+//   * Split-K (store epilogue): `splits` workgroups per tile over equal ranges of
+//     64-wide blocks; each stores its fp32 partial (device-coherent) and counts its
+//     arrival, and the last to arrive sums the partials in split order.
 //   * The K order of every output element is fixed (blocks in order within each K
-//     group, then group 0 + group 1), so rows do not depend on M or on the chunking.
+//     group, then group 0 + group 1, then splits in order), so rows do not depend on M
+//     or on the chunking for a given split count.
 #include "qlin_dev.h"
 #include "qlin_internal.h"
 
