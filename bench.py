@@ -15,7 +15,8 @@ launch stays eager with HIP events around it on its launch stream, which gives t
 dominant kernel's live per-launch time for the roofline object.
 
 Other workloads (`--workload`): decode-w4 (same shapes, W4 group 128), prefill
-(M in 128/512/2048, TFLOP/s), chain-w4 (9B-class 32-layer W4 decode chain), single
+(M in 128/512/2048, TFLOP/s), prefill-9b (the same over 9B-class layer shapes, where
+M = 2048 takes the balanced schedule), chain-w4 (9B-class 32-layer W4 decode chain), single
 (one 2048x6144 int8 linear, M=1), engine-w8 / engine-w4 (the engine-signature calls
 of one layer at decode rows and a 512-row prefill chunk), layout (the load-time layout
 producers: GPU requantization and GPTQ / AWQ repacks, HBM GB/s).
@@ -54,6 +55,9 @@ CHAIN_SHAPES = [  # 9B-class layer
 ]
 CHAIN_HEAD = ("lm_head", 4096, 248320)
 PREFILL_SHAPES = [("gate", 2048, 6144), ("down", 6144, 2048), ("q", 2048, 2048)]
+# 9B-class layer (hidden 4096, intermediate 12288): at M = 2048 the gate shape has 384
+# tiles of 256x256, one and a half rounds of the chip, and takes the balanced schedule
+PREFILL_SHAPES_9B = [("gate", 4096, 12288), ("down", 12288, 4096), ("q", 4096, 4096)]
 
 
 def _load_package():
@@ -223,7 +227,7 @@ def detail_table(ctx, kind, shapes, head, ms, reps=40):
 
 # ------------------------------------------------------------------ prefill
 
-def prefill_bench(args):
+def prefill_bench(args, shapes=PREFILL_SHAPES):
     import torch
     dev = torch.device("cuda", 0)
     lin = importlib.import_module(f"{ALIAS}.kernels.linear")
@@ -232,11 +236,11 @@ def prefill_bench(args):
     # The weights exist in several copy sets (about 45 MB each, > 512 MB in all) and
     # consecutive steps use different sets, so every step streams its weights from
     # HBM rather than the 256 MB last-level cache, as consecutive layers would.
-    set_bytes = sum(bytes_w8(0, K, N) + bytes_w4(0, K, N) for (_, K, N) in PREFILL_SHAPES)
+    set_bytes = sum(bytes_w8(0, K, N) + bytes_w4(0, K, N) for (_, K, N) in shapes)
     nsets = max(1, -(-600_000_000 // set_bytes))
     xs = {}
     outs = {}
-    for (name, K, N) in PREFILL_SHAPES:
+    for (name, K, N) in shapes:
         for M in ms:
             if (K, M) not in xs:
                 xs[(K, M)] = torch.randn((M, K), generator=gen).to(torch.float16).to(dev)
@@ -246,7 +250,7 @@ def prefill_bench(args):
     for _ in range(nsets):
         items = []
         for kind in ("w4", "w8"):  # W4 first: graph A below then holds most of the step
-            for (name, K, N) in PREFILL_SHAPES:
+            for (name, K, N) in shapes:
                 w = Weights(kind, K, N, dev, gen)
                 for M in ms:
                     items.append((kind, name, M, K, N, w, xs[(K, M)], outs[(N, M)]))
@@ -579,7 +583,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode-w8",
                     choices=["decode-w8", "decode-w4", "prefill", "chain-w4", "single", "head-pmc",
-                             "prefill-pmc", "engine-w8", "engine-w4", "layout"])
+                             "prefill-pmc", "engine-w8", "engine-w4", "layout", "prefill-9b"])
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -661,11 +665,13 @@ def main() -> int:
                   "launch": "hipgraph of all layers per M"}
         dtype = "i8 x int8" if kind == "w8" else "i8 x int4"
     else:
-        flops, t, roof, nsets = prefill_bench(args)
+        shapes = PREFILL_SHAPES_9B if wl == "prefill-9b" else PREFILL_SHAPES
+        flops, t, roof, nsets = prefill_bench(args, shapes)
         value = flops / t / 1e12
         unit = "TFLOP/s"
-        config = {"workload": "prefill GEMM, int8 and W4 g128, M in 128/512/2048",
-                  "shapes_KN": [[K, N] for (_, K, N) in PREFILL_SHAPES], "flops_per_step": flops,
+        config = {"workload": "prefill GEMM, int8 and W4 g128, M in 128/512/2048" +
+                              (", 9B-class layer shapes" if wl == "prefill-9b" else ""),
+                  "shapes_KN": [[K, N] for (_, K, N) in shapes], "flops_per_step": flops,
                   "weight_copy_sets": nsets,
                   "launch": "hipgraph per copy set for 17 cases, eager dominant case"}
         dtype = "f16 x int8/int4"
