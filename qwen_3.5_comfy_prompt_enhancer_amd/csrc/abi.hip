@@ -8,6 +8,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "../../include/qlin.h"
 #include "qlin_dev.h"
 #include "qlin_internal.h"
@@ -77,63 +79,166 @@ void plan_override(const Problem& P, int& cols, int& waves, int& upw) {
   if (u >= 1) upw = u;
 }
 
+// ---------------------------------------------------------------------------
+// Engine-signature calls with at least kRowsM rows (prefill chunks, chunk remainders)
+//
+// One K order for every M: the result of a row depends on (K, N) and the call kind,
+// never on M, on the chunking of a prompt or on which kernel family runs, so a
+// chunked prefill equals an unchunked one bit for bit.  The order is the tiled int8
+// kernel's: K/64 blocks in S contiguous splits; within a split, lane 0 folds the
+// blocks at even offsets and lane 1 those at odd offsets (acc = fma(float(dot),
+// scale, acc) from zero, in increasing K); split value = lane 0 + lane 1; total =
+// ((v0 + v1) + v2) + ...; then the W8 column scale (and residual, one rounding).
+// The 16-row skinny tiles reproduce it with two waves per split (lanes == 2).
+// S is chosen for the engine's 512-row chunk and then held for every M.
+// Calls with fewer rows (decode: one sequence or up to four best-of rows) keep the
+// decode plans, whose results depend on (K, N) only, so batch rows equal single rows.
+constexpr int kRowsM = 5;
+constexpr int kRefChunkM = 512;
+
+// Column tiles of 128 over the call's column ranges.
+long long tiles128(const Problem& P, const SkArgs& a) {
+  long long t = 0;
+  for (int s = 0; s < (P.epi == EPI_STORE ? a.nseg : 1); ++s) t += (a.seg[s].n + 127) / 128;
+  return t;
+}
+
+// Split count of the K order (store calls; gate/up calls are never split).  Time
+// model of the tiled int8 kernel, fitted to MI355X measurements (M = 512, W8 and W4,
+// K x N = 2048 x 2048, 6144 x 2048, 2048 x 8192, every plan forced), evaluated at the
+// engine's 512-row chunk:
+//   7 us + rounds of 256 workgroups x 128-wide K stages x 1.1 us (x 1.4 W4)
+//   + split-K exchange: 1.45 us per split + 12 ns per workgroup + 0.1 us per MB of
+//     partial tiles; a split level is tried only while the level below leaves CUs idle
+// QLIN_ENGINE_SPLITS overrides it (tuning; it changes the K order).
+int engine_splits(const Problem& P, const SkArgs& a) {
+  if (P.epi != EPI_STORE) return 1;
+  const int nb = P.K / 64;
+  const char* es = getenv("QLIN_ENGINE_SPLITS");
+  if (es && *es) return atoi(es);
+  const long long tiles = (long long)((kRefChunkM + 127) / 128) * tiles128(P, a);
+  const double t_stage = (P.wk == WK_W4 ? 1.4 : 1.0) * 1.1e-6;
+  double best = 7e-6 + (double)((tiles + 255) / 256) * ((nb + 1) / 2) * t_stage;
+  int S = 1;
+  for (int s = 2; s <= 8; s *= 2) {
+    if (nb % s != 0 || nb / s < 2 || tiles * (s / 2) >= 256) break;
+    const long long wgs = tiles * s;
+    const double t = 7e-6 + (double)((wgs + 255) / 256) * ((nb / s + 1) / 2) * t_stage + 1.45e-6 * s +
+                     12e-9 * wgs + 0.1e-12 * (double)wgs * 128 * 128 * sizeof(float);
+    if (t < best) best = t, S = s;
+  }
+  return S;
+}
+
+// The rows [m0, m0 + rows) of a call as a call of its own (rows are independent).
+SkArgs row_block(const SkArgs& a, int m0, int rows) {
+  SkArgs b = a;
+  b.M = rows;
+  b.x = (const int8_t*)a.x + (long long)m0 * a.K;
+  b.xs = a.xs + (long long)m0 * (a.K / 64);
+  if (a.out) b.out = (uint16_t*)a.out + (long long)m0 * a.ldo;
+  if (a.res) b.res = (const uint16_t*)a.res + (long long)m0 * a.ldr;
+  if (a.oq) b.oq = a.oq + (long long)m0 * a.ncols;
+  if (a.os) b.os = a.os + (long long)m0 * (a.ncols / 64);
+  return b;
+}
+
+int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
+                hipStream_t stream) {
+  const int S = engine_splits(P, a);
+  const int nb = P.K / 64;
+  if (S < 1 || S > 64 || nb % S != 0 || (S > 1 && nb / S < 2))
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: %d K splits do not divide K=%d into ranges of at least 128", fn, S, P.K);
+  if (P.epi != EPI_STORE && S != 1) return fail(QLIN_ERR_UNSUPPORTED, "%s: gate/up calls are not split", fn);
+  // family: the tiled int8 kernel where it applies and a time model prefers it to the
+  // 16-row tiles; both give the same bits.  QLIN_ENGINE_PREFILL=tiled|skinny forces one.
+  const char* e = getenv("QLIN_ENGINE_PREFILL");
+  const bool force_rows = e && strcmp(e, "skinny") == 0;
+  const bool force_tiled = e && strcmp(e, "tiled") == 0;
+  // Time models fitted to MI355X measurements (both families forced, M = 17-512, W8
+  // and W4-g128, the layer shapes 2048x2048, 6144x2048, 2048x8192 and gate/up
+  // 2048x6144, weights rotated over 600 MB so they stream from HBM):
+  //   tiled: 7 us + rounds of 256 workgroups x 128-wide K stages x weight sets x
+  //          t_stage, t_stage = 1.05 us + 2.5 ns per workgroup in the round (W4:
+  //          1.8 us + 1.6 ns), + the split-K exchange (1.45 us per split, 12 ns per
+  //          workgroup, 0.1 us per MB of partial tiles)
+  //   rows:  5 us + 0.125 us (W4 0.17) per 16-row tile per million weight elements,
+  //          + 1.45 us per split
+  bool tiled = false;
+  if (prefill_i8_ok(a, P.wk, P.epi) && !force_rows) {
+    const long long tiles = (long long)((P.M + 127) / 128) * tiles128(P, a);
+    const long long wgs = tiles * S;
+    const double occ = (double)std::min<long long>(wgs, 256);
+    const double t_stage = (P.wk == WK_W4 ? 1.8e-6 + 1.6e-9 * occ : 1.05e-6 + 2.5e-9 * occ) * P.nsets;
+    double t_tiled = 7e-6 + (double)((wgs + 255) / 256) * ((nb / S + 1) / 2) * t_stage;
+    if (S > 1) t_tiled += 1.45e-6 * S + 12e-9 * wgs + 0.1e-12 * (double)wgs * 128 * 128 * sizeof(float);
+    const double elems = (double)P.K * P.ncols * P.nsets / 1e6;
+    const double t_rows = 5e-6 + (P.wk == WK_W4 ? 0.17e-6 : 0.125e-6) * ((P.M + 15) / 16) * elems +
+                          (S > 1 ? 1.45e-6 * S : 0.0);
+    tiled = force_tiled || t_tiled < t_rows;
+  }
+  const int TN = tiled ? 128 : (S == 1 ? 64 : 128);
+  long long ntiles = 0;
+  for (int s = 0; s < (P.epi == EPI_STORE ? a.nseg : 1); ++s) ntiles += (a.seg[s].n + TN - 1) / TN;
+  // rows per launch: the split-K partials and arrival counters of a launch must fit
+  // the workspace (rows are independent, so blocks of rows give the same bits)
+  const size_t part_cap = (workspace && ws_bytes > kCounterBytes) ? ws_bytes - kCounterBytes : 0;
+  const int rstep = tiled ? 128 : 16;
+  long long mb_rows = P.M;
+  if (S > 1) {
+    const double row_bytes = (double)S * P.nsets * ntiles * TN * sizeof(float);  // per row of partials
+    const long long cap_rows = (long long)((double)part_cap / row_bytes) / rstep * rstep;
+    const long long cnt_rows = (long long)(kCounterBytes / sizeof(unsigned)) / ntiles * rstep;
+    mb_rows = std::min<long long>(P.M, std::min(cap_rows, cnt_rows));
+    if (mb_rows < std::min(P.M, rstep))
+      return fail(QLIN_ERR_WORKSPACE, "%s: the workspace (%zu bytes) cannot hold %d K splits of %lld columns", fn,
+                  ws_bytes, S, (long long)ntiles * TN);
+  }
+  for (long long m0 = 0; m0 < P.M; m0 += mb_rows) {
+    const int rows = (int)std::min<long long>(mb_rows, P.M - m0);
+    SkArgs b = row_block(a, (int)m0, rows);
+    b.splits = S;
+    b.cnt = S > 1 ? (unsigned*)workspace : nullptr;
+    b.part = S > 1 ? (float*)((char*)workspace + kCounterBytes) : nullptr;
+    hipError_t err;
+    if (tiled) {
+      err = launch_prefill_i8(b, P.wk, P.hz, P.epi, stream);
+    } else {
+      SkLaunch L;
+      L.act = P.act;
+      L.wk = P.wk;
+      L.hz = P.hz ? 1 : 0;
+      L.epi = P.epi;
+      L.cols = TN / 16;
+      L.waves = 2;
+      int acc = 0;
+      for (int s = 0; s < b.nseg; ++s) {
+        b.seg[s].tile0 = (P.epi == EPI_STORE) ? acc : 0;
+        if (P.epi == EPI_STORE) acc += (b.seg[s].n + TN - 1) / TN;
+      }
+      b.ntiles = (int)ntiles;
+      b.kchunk = P.K / S;
+      b.lanes = 2;
+      const int rtiles = (rows + 15) / 16;
+      if (ntiles * S > 0x7FFFFFFFLL || rtiles > 65535)
+        return fail(QLIN_ERR_UNSUPPORTED, "%s: grid too large (M=%d, N=%d)", fn, P.M, P.ncols);
+      L.grid = dim3((unsigned)(ntiles * S), (unsigned)rtiles, 1);
+      const int rg0 = ((rows < 16 ? rows : 16) + 3) / 4;
+      L.lds = ((size_t)L.waves * P.nsets * rg0 * 4 * (TN + 4) + (size_t)P.nsets * TN) * sizeof(float);
+      err = launch_skinny(L, b, stream);
+    }
+    if (err != hipSuccess) return hip_status(fn, err);
+  }
+  return QLIN_OK;
+}
+
 // Chooses the kernel variant, column tile, waves per workgroup and split-K, then launches.
 // Every choice depends on K, N (and whether M > 16), never on M itself, so an output row
-// is computed the same way for every M <= 16.
+// is computed the same way for every M <= 16.  Engine-signature calls with kRowsM rows
+// or more take engine_rows (one K order for every M).
 int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
                     hipStream_t stream) {
-  // Engine-signature stores with more than 16 rows (prefill chunks): the tiled int8
-  // kernel where it applies and a time model fitted to MI355X measurements (M = 512,
-  // W8 and W4, K x N = 2048 x 2048, 6144 x 2048, 2048 x 8192, every plan forced)
-  // prefers it to the 16-row tiles:
-  //   tiled:  7 us + rounds of 256 workgroups x 128-wide K stages x 1.1 us (x 1.4 W4)
-  //           x weight sets + split-K exchange (store epilogue): 1.45 us per split
-  //           + 12 ns per workgroup + 0.1 us per MB of partial tiles; a split level
-  //           is tried only while the level below it leaves CUs idle
-  //   rows:   5 us + 6.9 ns per row per MB of int8-sized weights (W4: 4.3 us, 6.5 ns)
-  // QLIN_ENGINE_PREFILL ("tiled" or "skinny") and QLIN_ENGINE_SPLITS override the
-  // choice (tests, tuning).
-  if (P.act == ACT_I8 && prefill_i8_ok(a, P.wk, P.epi)) {
-    const char* e = getenv("QLIN_ENGINE_PREFILL");
-    const bool force_rows = e && strcmp(e, "skinny") == 0;
-    const bool force_tiled = e && strcmp(e, "tiled") == 0;
-    long long tiles_n = 0;
-    for (int s = 0; s < (P.epi == EPI_STORE ? a.nseg : 1); ++s) tiles_n += a.seg[s].n / 128;
-    const long long tiles = (long long)((P.M + 127) / 128) * tiles_n;
-    const int nb = P.K / 64;
-    const size_t part_cap = (workspace && ws_bytes > kCounterBytes) ? ws_bytes - kCounterBytes : 0;
-    auto split_fits = [&](int S) {
-      return P.epi == EPI_STORE && S >= 1 && nb % S == 0 &&
-             (S == 1 || ((size_t)tiles * S * 128 * 128 * sizeof(float) <= part_cap &&
-                         (size_t)tiles <= kCounterBytes / sizeof(unsigned)));
-    };
-    const double t_stage = (P.wk == WK_W4 ? 1.4 : 1.0) * 1.1e-6 * P.nsets;  // gate/up: two weight sets
-    double t_tiled = 7e-6 + (double)((tiles + 255) / 256) * ((nb + 1) / 2) * t_stage;
-    int splits = 1;
-    for (int S = 2; S <= 8; S *= 2) {
-      if (!split_fits(S) || nb / S < 2 || tiles * (S / 2) >= 256) break;
-      const long long wgs = tiles * S;
-      const double t = 7e-6 + (double)((wgs + 255) / 256) * ((nb / S + 1) / 2) * t_stage + 1.45e-6 * S +
-                       12e-9 * wgs + 0.1e-12 * (double)wgs * 128 * 128 * sizeof(float);
-      if (t < t_tiled) {
-        t_tiled = t;
-        splits = S;
-      }
-    }
-    const char* es = getenv("QLIN_ENGINE_SPLITS");  // store epilogue only
-    if (es && *es && P.epi == EPI_STORE) {
-      splits = atoi(es);
-      if (!split_fits(splits)) return fail(QLIN_ERR_UNSUPPORTED, "%s: QLIN_ENGINE_SPLITS=%d unusable here", fn, splits);
-    }
-    const double t_rows = (P.wk == WK_W4 ? 4.3e-6 : 5e-6) +
-                          (P.wk == WK_W4 ? 6.5e-9 : 6.9e-9) * P.M * ((double)P.K * P.ncols * P.nsets / 1e6);
-    if (force_tiled || (!force_rows && t_tiled < t_rows)) {
-      a.splits = splits;
-      a.cnt = splits > 1 ? (unsigned*)workspace : nullptr;
-      a.part = splits > 1 ? (float*)((char*)workspace + kCounterBytes) : nullptr;
-      return hip_status(fn, launch_prefill_i8(a, P.wk, P.hz, P.epi, stream));
-    }
-  }
+  if (P.act == ACT_I8 && P.M >= kRowsM) return engine_rows(fn, P, a, workspace, ws_bytes, stream);
   SkLaunch L;
   L.act = P.act;
   L.wk = P.wk;

@@ -452,17 +452,20 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
         for (int r = 0; r < 4; ++r) {
           if (rb * 16 + 4 * g + r >= nrows) continue;
           const int ur = rb * 16 + r;
+          // column scale and residual in one rounding (fmaf), the product alone
+          // without a residual: the skinny kernel's epilogue rounds the same way
           float y[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) y[t] = acc[0][rb][t][r] * cs[0][t];
           if constexpr (RES) {
             const u32x2 rv = *(const u32x2*)(rbase + (long long)ur * a.ldr + rofs);
             const uint32_t rw[2] = {rv.x, rv.y};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               const uint16_t hh = (uint16_t)(rw[t >> 1] >> (16 * (t & 1)));
-              y[t] += BF ? bf16_to_f32(hh) : (float)bitcast<_Float16>(hh);
+              y[t] = fmaf(acc[0][rb][t][r], cs[0][t], BF ? bf16_to_f32(hh) : (float)bitcast<_Float16>(hh));
             }
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) y[t] = acc[0][rb][t][r] * cs[0][t];
           }
           u32x2 o;
           o.x = cvt2(y[0], y[1]);

@@ -37,8 +37,12 @@ struct SkArgs {
   float* os;           // EPI_GATEUP_Q fp32 [M][ncols/64]
   float* part;         // split-K partials [splits][nsets][M][ncols]
   unsigned* cnt;       // split-K arrival counters [row tiles][ntiles], zero between calls
-  int kchunk;          // K range of one wave
+  int kchunk;          // K range of one wave (lanes == 0) or of one split (lanes == 2)
   int splits;          // workgroups per column tile along K
+  int lanes;           // int8 activations: 0 = wave w of split s folds the contiguous range
+                       // [(s*waves + w)*kchunk, +kchunk); 2 = the two waves of split s fold
+                       // the alternate 64-wide blocks of [s*kchunk, (s+1)*kchunk) (wave w:
+                       // block offsets w, w+2, ...), the K order of the tiled int8 kernel
 };
 
 struct SkLaunch {

@@ -272,8 +272,13 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
 
   const int arow = rt * 16 + j;  // activation row this lane feeds into the A operand
   const bool avalid = arow < M;
-  const int kb = (split * nw + wave) * a.kchunk;
+  // K range of this wave: contiguous kchunk-wide ranges (lanes == 0), or, for int8
+  // activations with lanes == 2, the alternate 64-wide blocks of the split's range
+  // (the K order of the tiled int8 kernel: see kof below)
+  const bool inter = ACT == ACT_I8 && a.lanes == 2;
+  const int kb = inter ? split * a.kchunk + 64 * wave : (split * nw + wave) * a.kchunk;
   const int ke = min(K, kb + a.kchunk);
+  const int kst = inter ? 128 : 64;  // K distance between this wave's consecutive 64-wide blocks
 
   f32x4 acc[NS][COLS];
 #pragma unroll
@@ -359,7 +364,12 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       }
     }
   };
-  const int nsteps = ke > kb ? (ke - kb) >> 5 : 0;
+  const int nsteps = inter ? 2 * (((a.kchunk >> 6) - wave + 1) >> 1) : (ke > kb ? (ke - kb) >> 5 : 0);
+  // K of step i: 32-wide steps, two per 64-wide block, blocks kst apart
+  auto kof = [&](int i) {
+    if constexpr (ACT == ACT_F16) return kb + 32 * i;
+    else return kb + kst * (i >> 1) + 32 * (i & 1);
+  };
   Step buf[D];
   // The loop is unrolled by U = 4 steps, and compute() receives the step's position
   // u = i % 4 as a compile-time constant.  Every wave's K range starts at a multiple
@@ -386,8 +396,8 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
             constexpr int u = decltype(uc)::value;
             const int i = base0 + c * U + u;
             if (i < nsteps) {
-              compute(buf[u % D], kb + 32 * i, uc);
-              if (i + D < nsteps) load_step(buf[u % D], kb + 32 * (i + D));
+              compute(buf[u % D], kof(i), uc);
+              if (i + D < nsteps) load_step(buf[u % D], kof(i + D));
             }
           });
         });
@@ -395,44 +405,44 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       int base0 = 0;
       if (nsteps >= U + D) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) load_step(buf[d], kb + 32 * d);
+        for (int d = 0; d < D; ++d) load_step(buf[d], kof(d));
         base0 = ((nsteps - U - D) / U + 1) * U;  // chunks whose loads are all in range
         for (int base = 0; base < base0; base += U) {
           static_for<0, U>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
             const int i = base + u;
-            compute(buf[u % D], kb + 32 * i, uc);
-            load_step(buf[u % D], kb + 32 * (i + D));
+            compute(buf[u % D], kof(i), uc);
+            load_step(buf[u % D], kof(i + D));
           });
         }
       } else {
 #pragma unroll
         for (int d = 0; d < D; ++d)
-          if (d < nsteps) load_step(buf[d], kb + 32 * d);
+          if (d < nsteps) load_step(buf[d], kof(d));
       }
       tail(base0);
     } else {
       // every load issued unconditionally, the step index clamped to the last step
 #pragma unroll
-      for (int d = 0; d < D; ++d) load_step(buf[d], kb + 32 * (d < nsteps ? d : nsteps - 1));
+      for (int d = 0; d < D; ++d) load_step(buf[d], kof(d < nsteps ? d : nsteps - 1));
       const int nfull = nsteps - nsteps % U;
       for (int base = 0; base < nfull; base += U) {
         static_for<0, U>([&](auto uc) {
           constexpr int u = decltype(uc)::value;
           const int i = base + u;
-          compute(buf[u % D], kb + 32 * i, uc);
+          compute(buf[u % D], kof(i), uc);
           const int nx = i + D < nsteps ? i + D : nsteps - 1;
-          load_step(buf[u % D], kb + 32 * nx);
+          load_step(buf[u % D], kof(nx));
         });
       }
       static_for<0, U - 1>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
         const int i = nfull + u;
         if (i < nsteps) {
-          compute(buf[u % D], kb + 32 * i, uc);
+          compute(buf[u % D], kof(i), uc);
           if constexpr (U > D) {
             const int nx = i + D < nsteps ? i + D : nsteps - 1;
-            load_step(buf[u % D], kb + 32 * nx);
+            load_step(buf[u % D], kof(nx));
           }
         }
       });
@@ -704,33 +714,39 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
     const bool cval = it < nitems && tcol0 + c < n;
     const int orow = rt * 16 + row;
     const long long oc = (long long)sg0.col0 + tcol0 + c;  // first output column
-    float v[NS][8];
+    // W8 column scale, then the residual: one rounding (fmaf) with a residual, the
+    // product alone without; the tiled int8 kernel rounds the same way, so both
+    // families give the same bits for the same K order.
+    float v[NS][8], cs[NS][8];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const f32x4 lo = *(const f32x4*)&red[(s * R4 + row) * TNP + c];
       const f32x4 hi = *(const f32x4*)&red[(s * R4 + row) * TNP + c + 4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[s][e] = lo[e], v[s][4 + e] = hi[e];
-      if constexpr (WK == WK_W8) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[s][e] *= scl[s * TN + c + e];
-      }
+      for (int e = 0; e < 8; ++e) cs[s][e] = (WK == WK_W8) ? scl[s * TN + c + e] : 1.0f;
     }
     if constexpr (EPI == EPI_STORE) {
       if (a.res != nullptr) {
-        const u32x4 rr = (base == 0) ? rpre : *(const u32x4*)((const uint16_t*)a.res + (long long)orow * a.ldr + oc);
+        // items past the row or the tile read a clamped, in-bounds chunk and store nothing
+        const long long rc = (long long)sg0.col0 + min(tcol0 + c, n - 8);
+        const u32x4 rr = (base == 0) ? rpre : *(const u32x4*)((const uint16_t*)a.res + (long long)orow * a.ldr + rc);
         const uint32_t rw[4] = {rr.x, rr.y, rr.z, rr.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint16_t h = (uint16_t)(rw[e >> 1] >> (16 * (e & 1)));
-          v[0][e] += (a.odt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+          v[0][e] = fmaf(v[0][e], cs[0][e], (a.odt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h));
         }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[0][e] *= cs[0][e];
       }
       if (cval) st_out16<8>(a.out, a.odt, (long long)orow * a.ldo + oc, v[0]);
     } else {
       float h[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = silu(v[0][e]) * v[1][e];
+      for (int e = 0; e < 8; ++e) h[e] = silu(v[0][e] * cs[0][e]) * (v[1][e] * cs[1][e]);
       if constexpr (EPI == EPI_GATEUP) {
         if (cval) st_out16<8>(a.out, DT_BF16, (long long)orow * a.ncols + oc, h);
       } else {

@@ -526,9 +526,11 @@ def _assert_doubled(y, y2):
 
 @pytest.mark.parametrize("kind", ["w8", "w4"])
 @pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048), (2048, 2048)])
-def test_config3_prefill_full_size(kind, K, N):
-    M = 2048
-    x = H.act_f16(M, K, seed=500 + K)
+@pytest.mark.parametrize("M", [128, 512, 2048])
+def test_config3_prefill_full_size(kind, K, N, M):
+    """Every config-3 case (M = 128, 512, 2048 on its three shapes, W8 and W4-g128)
+    under the planner's own choice of tile shape, split-K and schedule."""
+    x = H.act_f16(M, K, seed=500 + K + M)
     cols = H.sample_cols(N, 256, seed=501)
     if kind == "w8":
         w, s = H.w8(K, N, seed=502)

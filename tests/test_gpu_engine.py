@@ -193,11 +193,12 @@ def test_mlp_gate_up_quant_w4(M, zeros, group):
 
 
 @pytest.mark.parametrize("plan", ["4,8,0", "8,4,0"])
-@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("M", [1, 2, 4])
 def test_engine_decode_forced_plans(plan, M, monkeypatch):
     """One-pass 64-column tiles and split-K 128-column tiles for every engine call
     kind (store + residual, proj3, gate/up + quant; W8 and W4), whatever the
-    default plan is for the shape."""
+    default plan is for the shape (decode sizes: the plan override applies to calls
+    of at most 4 rows)."""
     monkeypatch.setenv("QLIN_SKINNY_PLAN", plan)
     gemm, w4 = _g()
     K, N = 2048, 2048
@@ -320,8 +321,8 @@ def test_prefill_tiled_rows_independent_of_chunking(kind, tiled):
 
 
 def test_prefill_tiled_matches_row_tiles(tiled):
-    """The tiled kernel and the 16-row skinny kernel compute the same products and
-    block scales in different fp32 orders: they agree to the GEMM tolerance."""
+    """The tiled kernel and the 16-row skinny kernel fold K in the same order (two
+    interleaved lanes per split, splits in order): identical bits."""
     gemm, _ = _g()
     M, K, N = 96, 2048, 2048
     a, as_ = H.engine_act(M, K, seed=440)
@@ -331,9 +332,7 @@ def test_prefill_tiled_matches_row_tiles(tiled):
     tiled.setenv("QLIN_ENGINE_PREFILL", "skinny")
     y1 = torch.empty_like(y0)
     gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y1)
-    f0, f1 = H.to_f32(y0).astype(np.float64), H.to_f32(y1).astype(np.float64)
-    # both are bf16-rounded: allow the tolerance plus one bf16 ulp
-    assert np.all(np.abs(f0 - f1) <= 2e-3 * np.abs(f1).max() + 2 * H.half_ulp(f1, torch.bfloat16))
+    assert torch.equal(y0, y1)
 
 
 @pytest.mark.parametrize("N,group", [(1040, 128), (1024, 32)])
@@ -412,7 +411,7 @@ def test_prefill_tiled_bad_split_raises(tiled):
     a, as_ = H.engine_act(64, 2048, seed=489)
     b, bs = H.engine_w8(2048, 1024, seed=489)
     out = torch.empty((64, 1024), dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(ValueError, match="QLIN_ENGINE_SPLITS"):
+    with pytest.raises(ValueError, match="K splits"):
         gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)
 
 
