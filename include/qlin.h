@@ -70,6 +70,22 @@ int qlin_gemm_i8(const int8_t* a_q, const float* a_s, int M, int K,
                  void* out, int64_t ldo, const void* residual, int64_t ldr,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* qlin_gemm_i8 without a workspace argument: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  Split-K partials and arrival
+ * counters go to a static device array of 9 MiB per GPU (1 MiB of counters, 8 MiB of
+ * partials), held until the process ends; nothing is allocated or freed per call.
+ * Each call first zeroes the arrival counters it can use with a fill kernel on
+ * `stream`.  Results equal qlin_gemm_i8's bit for bit: decode plans fit the scratch,
+ * and a prefill call whose partials exceed it runs in blocks of rows (rows are
+ * independent).  A call that cannot fit even one block of rows fails with
+ * QLIN_ERR_WORKSPACE before launching anything.  Calls that overlap in time on one
+ * GPU share the array and race: serialize them (one stream, or the engine's lock). */
+int qlin_gemm_i8_noalloc(const int8_t* a_q, const float* a_s, int M, int K,
+                         const int8_t* b, const void* b_s, int bs_dtype, int N,
+                         void* out, int64_t ldo, const void* residual, int64_t ldr,
+                         void* stream);
+
 /* W4 twin of qlin_gemm_i8: replaces gemm_w4 (kernels/w4.py:139-166, kernel
  * w4.py:107-136).  b uint8 [K/2,N]; b_s [K/group, N]; b_z uint8 [K/group, N] or NULL
  * (z = 8).  group: 32, 64 or a multiple of 64 (quant_formats.py:42-49). */

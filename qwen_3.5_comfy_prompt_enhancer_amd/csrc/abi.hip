@@ -33,6 +33,25 @@ int hip_status(const char* fn, hipError_t e) {
   return fail(QLIN_ERR_HIP, "%s: HIP error %d (%s)", fn, (int)e, hipGetErrorString(e));
 }
 
+#define QL_TRY(expr)              \
+  do {                            \
+    const int rc_ = (expr);       \
+    if (rc_ != QLIN_OK) return rc_; \
+  } while (0)
+
+__global__ void zero_u32(unsigned* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Zero the first n arrival counters of a scratch with a fill kernel on `stream` (a
+// kernel node, not a memset, so the call can be captured in a graph).
+hipError_t clear_counters(void* ws, long long n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_u32, dim3((unsigned)std::min<long long>(256, (n + 255) / 256)), dim3(256), 0, stream,
+                     (unsigned*)ws, (int)n);
+  return hipGetLastError();
+}
+
 // Workspace: [counters | partial sums].  Counters must be zero between calls.
 constexpr size_t kWorkspaceBytes = size_t(256) << 20;
 constexpr size_t kCounterBytes = size_t(1) << 20;
@@ -144,7 +163,7 @@ SkArgs row_block(const SkArgs& a, int m0, int rows) {
 }
 
 int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
-                hipStream_t stream) {
+                hipStream_t stream, bool clear) {
   const int S = engine_splits(P, a);
   const int nb = P.K / 64;
   if (S < 1 || S > 64 || nb % S != 0 || (S > 1 && nb / S < 2))
@@ -194,6 +213,11 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
       return fail(QLIN_ERR_WORKSPACE, "%s: the workspace (%zu bytes) cannot hold %d K splits of %lld columns", fn,
                   ws_bytes, S, (long long)ntiles * TN);
   }
+  if (clear && S > 1) {
+    // one counter per (16-row tile, column tile) at most, for the rows of one launch
+    const long long n = ((mb_rows + 15) / 16) * ntiles;
+    QL_TRY(hip_status(fn, clear_counters(workspace, std::min<long long>(n, kCounterBytes / sizeof(unsigned)), stream)));
+  }
   for (long long m0 = 0; m0 < P.M; m0 += mb_rows) {
     const int rows = (int)std::min<long long>(mb_rows, P.M - m0);
     SkArgs b = row_block(a, (int)m0, rows);
@@ -236,9 +260,11 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
 // Every choice depends on K, N (and whether M > 16), never on M itself, so an output row
 // is computed the same way for every M <= 16.  Engine-signature calls with kRowsM rows
 // or more take engine_rows (one K order for every M).
+// clear: zero the arrival counters the launch can use first (a scratch whose counters
+// are not known to be zero).
 int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
-                    hipStream_t stream) {
-  if (P.act == ACT_I8 && P.M >= kRowsM) return engine_rows(fn, P, a, workspace, ws_bytes, stream);
+                    hipStream_t stream, bool clear = false) {
+  if (P.act == ACT_I8 && P.M >= kRowsM) return engine_rows(fn, P, a, workspace, ws_bytes, stream, clear);
   SkLaunch L;
   L.act = P.act;
   L.wk = P.wk;
@@ -345,6 +371,7 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   L.lds = ((size_t)waves * P.nsets * rg0 * 4 * (TN + 4) + (size_t)P.nsets * TN) * sizeof(float);
   if ((long long)ntiles * splits > 0x7FFFFFFFLL || rtiles > 65535)
     return fail(QLIN_ERR_UNSUPPORTED, "%s: grid too large (M=%d, N=%d)", fn, P.M, P.ncols);
+  if (clear && splits > 1) QL_TRY(hip_status(fn, clear_counters(workspace, (long long)rtiles * ntiles, stream)));
   return hip_status(fn, launch_skinny(L, a, stream));
 }
 
@@ -386,11 +413,6 @@ int check_group(const char* fn, int group, int K) {
   return QLIN_OK;
 }
 
-#define QL_TRY(expr)              \
-  do {                            \
-    const int rc_ = (expr);       \
-    if (rc_ != QLIN_OK) return rc_; \
-  } while (0)
 
 Seg make_seg(const void* w, const void* s, const uint8_t* z, int n, int col0) {
   Seg g;
@@ -412,7 +434,7 @@ SkArgs base_args() {
 // Common body of gemm_i8 / gemm_w4.
 int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int M, int K, const void* b,
                 const void* b_s, int bs_dtype, const uint8_t* b_z, int group, int N, void* out, int64_t ldo,
-                const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream) {
+                const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream, bool clear = false) {
   QL_TRY(check_common(fn, M, K, N));
   if (M == 0 || N == 0) return QLIN_OK;
   QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
@@ -437,7 +459,8 @@ int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int
   a.res = residual;
   a.ldr = ldr;
   Problem P{ACT_I8, wk, EPI_STORE, b_z != nullptr, M, K, a.group, 1, N};
-  return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
+  if (clear && (!ws || wsb <= kCounterBytes)) return fail(QLIN_ERR_WORKSPACE, "%s: no scratch", fn);
+  return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream, clear);
 }
 
 int engine_proj3(const char* fn, int wk, const int8_t* a_q, const float* a_s, int M, int K, const void* w1,
@@ -717,6 +740,22 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
 }
 
 }  // namespace
+
+namespace qlin {
+
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
+int gemm_i8_scratch(const char* fn, const int8_t* a_q, const float* a_s, int M, int K, const int8_t* b,
+                    const void* b_s, int bs_dtype, int N, void* out, int64_t ldo, const void* residual,
+                    int64_t ldr, void* scratch, size_t scratch_bytes, void* stream) {
+  g_err[0] = 0;
+  return engine_gemm(fn, WK_W8, a_q, a_s, M, K, b, b_s, bs_dtype, nullptr, 64, N, out, ldo, residual, ldr,
+                     scratch, scratch_bytes, stream, true);
+}
+
+size_t counter_bytes() { return kCounterBytes; }
+
+}  // namespace qlin
 
 extern "C" {
 

@@ -101,6 +101,16 @@ bool prefill_balanced_ok(long long tiles, int nkt, int sk);
 void prefill_geometry(int shape, int* bm, int* bn, int* waves);
 bool prefill_shape_ok(int shape);
 
+// Sets the message qlin_last_error() returns on this thread; returns `code`.
+int set_error(int code, const char* msg);
+// qlin_gemm_i8 on a caller-owned scratch laid out like the workspace (counter_bytes()
+// of arrival counters, then partial sums): validates, clears the arrival counters the
+// call can use with a fill kernel on `stream`, then plans and launches.
+int gemm_i8_scratch(const char* fn, const int8_t* a_q, const float* a_s, int M, int K, const int8_t* b,
+                    const void* b_s, int bs_dtype, int N, void* out, int64_t ldo, const void* residual,
+                    int64_t ldr, void* scratch, size_t scratch_bytes, void* stream);
+size_t counter_bytes();
+
 hipError_t launch_w4_unpack(const uint8_t* p, int K, int N, uint8_t* out, hipStream_t st);
 hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uint8_t* z,
                              int group, int K, int N, float* out, hipStream_t st);

@@ -49,6 +49,7 @@ _S = ctypes.c_size_t
 # argument lists of the C ABI (include/qlin.h); every entry point returns int
 _SIGS = {
     "qlin_gemm_i8": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _L, _P, _L, _P, _S, _P],
+    "qlin_gemm_i8_noalloc": [_P, _P, _I, _I, _P, _P, _I, _I, _P, _L, _P, _L, _P],
     "qlin_gemm_w4": [_P, _P, _I, _I, _P, _P, _I, _P, _I, _I, _P, _L, _P, _L, _P, _S, _P],
     "qlin_proj3_i8": [_P, _P, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _P, _L, _P, _S, _P],
     "qlin_proj3_w4": [_P, _P, _I, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I,

@@ -27,8 +27,8 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 21
-    for n in ("qlin_gemm_i8", "qlin_gemm_w4", "qlin_proj3_i8", "qlin_proj3_w4",
+    assert len(names) == 22
+    for n in ("qlin_gemm_i8", "qlin_gemm_i8_noalloc", "qlin_gemm_w4", "qlin_proj3_i8", "qlin_proj3_w4",
               "qlin_mlp_gate_up_quant_i8", "qlin_mlp_gate_up_quant_w4", "qlin_linear_w8",
               "qlin_linear_w4", "qlin_w4_unpack", "qlin_w4_dequant_f32",
               "qlin_requant_w4_sym", "qlin_requant_w8_row", "qlin_w4_repack_gptq",
@@ -47,6 +47,8 @@ def test_version_and_workspace():
     _, L = _lib()
     assert L.qlin_version() == 1
     assert L.qlin_workspace_bytes() == 256 << 20
+    # every entry point clears the calling thread's message; an empty call succeeds
+    assert L.qlin_w4_unpack(None, 0, 0, None, None) == 0
     assert L.qlin_last_error() == b""
 
 
