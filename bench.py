@@ -54,6 +54,12 @@ CHAIN_SHAPES = [  # 9B-class layer
     ("gate", 4096, 12288), ("up", 4096, 12288), ("down", 12288, 4096),
 ]
 CHAIN_HEAD = ("lm_head", 4096, 248320)
+# Dependency level of each linear within a decode layer, as a real decode step orders
+# them: the projections that read the layer input, then the ones that read the
+# attention / linear-attention output, then gate/up (after the residual and norm),
+# then down; the next layer reads down's result, the vocabulary head the last layer's.
+LAYER_LEVEL = {"q": 0, "k": 0, "v": 0, "lin_in": 0, "o": 1, "lin_out": 1, "gate": 2, "up": 2, "down": 3}
+LEVELS_PER_LAYER = 4
 PREFILL_SHAPES = [("gate", 2048, 6144), ("down", 6144, 2048), ("q", 2048, 2048)]
 # 9B-class layer (hidden 4096, intermediate 12288): at M = 2048 the gate shape has 384
 # tiles of 256x256, one and a half rounds of the chip, and takes the balanced schedule
@@ -112,18 +118,22 @@ class Weights:
 
 # ------------------------------------------------------------------ decode sweep
 
-def decode_sweep(args, kind, shapes, head, ms, layers):
-    """Returns (total_bytes_per_step, step_fn, head_events, head_bytes_by_m)."""
+def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
+    """Returns (total_bytes_per_step, step_fn, head_events, head_bytes_by_m, record, ctx);
+    `reuse` = the ctx of an earlier call with the same shapes (its weights and buffers)."""
     import torch
     dev = torch.device("cuda", 0)
     lin = importlib.import_module(f"{ALIAS}.kernels.linear")
-    gen = torch.Generator().manual_seed(1234)
-    lw = [[Weights(kind, K, N, dev, gen) for (_, K, N) in shapes] for _ in range(layers)]
-    hw = Weights(kind, head[1], head[2], dev, gen)
-    kmax = max([K for _, K, _ in shapes] + [head[1]])
-    xs = {M: torch.randn((M, kmax), generator=gen).to(torch.float16).to(dev) for M in ms}
-    outs = {M: [torch.empty((M, N), dtype=torch.float16, device=dev) for (_, _, N) in shapes] for M in ms}
-    hout = {M: torch.empty((M, head[2]), dtype=torch.float16, device=dev) for M in ms}
+    if reuse is not None:
+        lw, hw, xs, outs, hout = reuse[:5]
+    else:
+        gen = torch.Generator().manual_seed(1234)
+        lw = [[Weights(kind, K, N, dev, gen) for (_, K, N) in shapes] for _ in range(layers)]
+        hw = Weights(kind, head[1], head[2], dev, gen)
+        kmax = max([K for _, K, _ in shapes] + [head[1]])
+        xs = {M: torch.randn((M, kmax), generator=gen).to(torch.float16).to(dev) for M in ms}
+        outs = {M: [torch.empty((M, N), dtype=torch.float16, device=dev) for (_, _, N) in shapes] for M in ms}
+        hout = {M: torch.empty((M, head[2]), dtype=torch.float16, device=dev) for M in ms}
 
     def xin(M, K):
         return xs[M][:, :K]
@@ -132,6 +142,48 @@ def decode_sweep(args, kind, shapes, head, ms, layers):
         for l in range(layers):
             for i, (_, K, _) in enumerate(shapes):
                 lw[l][i].run(lin, xin(M, K), outs[M][i])
+
+    total = sum((layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0) + hw.nbytes(M) for M in ms)
+    if args.launch == "chain":
+        # one persistent launch per M: every layer copy and the head, in dependency
+        # levels (args.levels == "layer") or all independent ("flat")
+        from qwen35_amd.kernels.chain import DecodeChain
+        order = sorted(range(len(shapes)), key=lambda i: LAYER_LEVEL.get(shapes[i][0], 0))
+        chains = {}
+        for M in ms:
+            ch = DecodeChain(M)
+            base = 0
+            for l in range(layers):
+                for i in order:
+                    _, K, _ = shapes[i]
+                    lvl = base + LAYER_LEVEL.get(shapes[i][0], 0) if args.levels == "layer" else 0
+                    ch.add(xin(M, K), lw[l][i].w, lw[l][i].s, outs[M][i], level=lvl)
+                if shapes and args.levels == "layer":
+                    base += LEVELS_PER_LAYER
+            ch.add(xin(M, head[1]), hw.w, hw.s, hout[M],
+                   level=(base if shapes and args.levels == "layer" else 0))
+            ch.build()
+            chains[M] = ch
+        for M in ms:
+            chains[M].run()
+        torch.cuda.synchronize()
+        ev = {M: [] for M in ms}
+        record = {"on": False}
+
+        def step():
+            for M in ms:
+                if record["on"]:
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    chains[M].run()
+                    e1.record()
+                    ev[M].append((e0, e1))
+                else:
+                    chains[M].run()
+
+        step_bytes = {M: (layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0) + hw.nbytes(M) for M in ms}
+        return total, step, ev, step_bytes, record, (lw, hw, xs, outs, hout, lin, chains)
 
     # eager warm-up (allocates the workspace outside capture), then capture per M
     for M in ms:
@@ -166,9 +218,8 @@ def decode_sweep(args, kind, shapes, head, ms, layers):
             else:
                 hw.run(lin, xin(M, head[1]), hout[M])
 
-    total = sum((layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0) + hw.nbytes(M) for M in ms)
     head_bytes = {M: hw.nbytes(M) for M in ms}
-    return total, step, head_ev, head_bytes, record, (lw, hw, xs, outs, hout, lin)
+    return total, step, head_ev, head_bytes, record, (lw, hw, xs, outs, hout, lin, None)
 
 
 def time_steps(step, steps, warmup, record=None):
@@ -192,7 +243,7 @@ def detail_table(ctx, kind, shapes, head, ms, reps=40):
     """Per-shape GPU time (stderr only): a HIP graph of `reps` launches of one shape,
     rotating over the layer copies, timed with events around its replay."""
     import torch
-    lw, hw, xs, outs, hout, lin = ctx
+    lw, hw, xs, outs, hout, lin, _ = ctx
     layers = max(1, len(lw))
     rows = []
     for M in ms:
@@ -409,58 +460,100 @@ def engine_bench(args, kind):
 
 # ------------------------------------------------------------------ CPU baseline
 
-def cpu_baseline(kind, shapes, head, budget_s=15.0):
-    """The oracle's CPU path (dequantize to fp32, then an fp32 matmul) on a bounded
-    sample of the decode workload: M = 1, every layer shape once, and 1/8 of the
-    vocabulary-head columns; GB/s over the same algorithmic bytes as the GPU."""
+def _cpu_model() -> str:
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def torch_dequant(kind, w, s):
+    """The reference's CPU path for one weight (quant_formats.py:6-9): dequantize to
+    fp32 with torch on the CPU.  W8: w[k, n] * s[n]; W4 g128: (nibble - 8) * s[k // 128, n]
+    with the low nibble of packed byte (j, n) at k = 2j (w4.py:5-11)."""
+    import torch
+    if kind == "w8":
+        return w.to(torch.float32) * s.to(torch.float32)[None, :]
+    K2, N = w.shape
+    nib = torch.stack((w & 15, w >> 4), dim=1).reshape(2 * K2, N)
+    sc = s.to(torch.float32).repeat_interleave(2 * K2 // s.shape[0], dim=0)
+    return (nib.to(torch.int16) - 8).to(torch.float32) * sc
+
+
+def cpu_baseline(kind, shapes, head, budget_s=30.0):
+    """The reference's CPU path on the decode workload at M = 1 (BASELINE's CPU
+    plan): for every layer shape and the whole vocabulary head, dequantize the
+    weight to fp32 with torch, then torch.matmul in fp32, on the host's cores
+    (torch.set_num_threads).  Dequantization and matmul are timed separately, each
+    the median of 10 runs after 2 warm-ups; GB/s over the same algorithmic bytes as
+    the GPU line.  The torch dequantization is first checked bit for bit against the
+    oracle."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    import torch
     if str(ROOT) not in sys.path:
         sys.path.insert(0, str(ROOT))
     from oracle import ref_cpu as R
 
-    cores = min(16, len(os.sched_getaffinity(0)))
-    rng = np.random.default_rng(5)
-    sample = list(shapes) + [(head[0] + "/8", head[1], head[2] // 8)]
-    tot_b = tot_t = t_deq = 0.0
-    with threadpool_limits(limits=cores):
-        deadline = time.perf_counter() + budget_s
-        reps = 0
-        while True:
-            for (_, K, N) in sample:
-                x = rng.standard_normal((1, K)).astype(np.float16)
-                if kind == "w8":
-                    w = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
-                    s = (np.abs(rng.normal(0, 0.02, N)) / 127).astype(np.float16)
-                    t0 = time.perf_counter()
-                    wd = R.dequant_w8_f32(w, s)
-                    t1 = time.perf_counter()
-                    R.linear_ref(x, wd)
-                    t2 = time.perf_counter()
-                    b = bytes_w8(1, K, N)
-                else:
-                    w = rng.integers(0, 256, size=(K // 2, N), dtype=np.uint8)
-                    s = (np.abs(rng.normal(0, 0.02, (K // 128, N))) / 7).astype(np.float16)
-                    t0 = time.perf_counter()
-                    wd = R.dequant_w4_f32(w, s)
-                    t1 = time.perf_counter()
-                    R.linear_ref(x, wd)
-                    t2 = time.perf_counter()
-                    b = bytes_w4(1, K, N)
-                tot_b += b
-                tot_t += t2 - t0
-                t_deq += t1 - t0
-            reps += 1
-            if time.perf_counter() > deadline:
-                break
+    affinity = len(os.sched_getaffinity(0))
+    threads = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity)))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(5)
+    sample = list(shapes) + [head]
+    t_deq = t_mm = 0.0
+    nbytes = 0
+    rows = []
+    t_start = time.perf_counter()
+    for i, (name, K, N) in enumerate(sample):
+        x = torch.randn((1, K), generator=gen).to(torch.float16)
+        if kind == "w8":
+            w = torch.randint(-127, 128, (K, N), generator=gen, dtype=torch.int8)
+            s = ((torch.randn(N, generator=gen) * 0.02).abs() / 127).to(torch.float16)
+            nbytes += bytes_w8(1, K, N)
+        else:
+            w = torch.randint(0, 256, (K // 2, N), generator=gen, dtype=torch.uint8)
+            s = ((torch.randn((K // 128, N), generator=gen) * 0.02).abs() / 7).to(torch.float16)
+            nbytes += bytes_w4(1, K, N)
+        if i == 0:  # the timed path is the oracle's dequantization, bit for bit
+            wd = torch_dequant(kind, w[:256], s if kind == "w8" else s[:4]).numpy()
+            ref = (R.dequant_w8_f32(w[:256].numpy(), s.numpy()) if kind == "w8"
+                   else R.dequant_w4_f32(w[:256].numpy(), s[:4].numpy()))
+            if not np.array_equal(wd, ref):
+                raise RuntimeError("cpu_baseline: torch dequantization differs from the oracle")
+        deq, mm = [], []
+        for rep in range(12):
+            t0 = time.perf_counter()
+            wd = torch_dequant(kind, w, s)
+            t1 = time.perf_counter()
+            y = torch.matmul(x.to(torch.float32), wd)
+            t2 = time.perf_counter()
+            if rep >= 2:
+                deq.append(t1 - t0)
+                mm.append(t2 - t1)
+            del wd, y
+        d, m = float(np.median(deq)), float(np.median(mm))
+        t_deq += d
+        t_mm += m
+        rows.append((name, K, N, d, m))
+        if time.perf_counter() - t_start > 4 * budget_s:
+            break
+    log("cpu baseline (" + kind + "): " + ", ".join(f"{n} {d * 1e3:.1f}+{m * 1e3:.1f} ms" for n, _, _, d, m in rows))
     return {
-        "value": round(tot_b / tot_t / 1e9, 3),
+        "value": round(nbytes / (t_deq + t_mm) / 1e9, 3),
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"M=1 decode of every layer shape plus 1/8 of the vocab-head columns, {kind}, "
-                   f"{reps} pass(es); numpy oracle: dequantize to fp32 (single thread, "
-                   f"{100 * t_deq / tot_t:.0f}% of the time) then fp32 matmul (BLAS, {cores} threads)"),
+        "cpu_model": _cpu_model(),
+        "affinity_cpus": affinity,
+        "dequant_s": round(t_deq, 5),
+        "matmul_s": round(t_mm, 5),
+        "sample": (f"M=1 decode of every layer shape and the whole vocab head ({kind}): torch on the CPU, "
+                   f"dequantize to fp32 then fp32 torch.matmul, {threads} threads; per shape the median "
+                   f"of 10 runs after 2 warm-ups, dequantization and matmul timed separately"),
     }
 
 
@@ -513,6 +606,26 @@ def prefill_pmc(args):
     print(json.dumps({"workload": "prefill-pmc", "flops_per_launch": 2 * M * K * N,
                       "algorithmic_bytes": K * N + 2 * N + 2 * M * K + 2 * M * N, "copy_bytes": 1 << 30}),
           flush=True)
+    return 0
+
+
+def decode_pmc(args):
+    """For `rocprofv3 --pmc` runs: `--steps` launches of the W8 decode chain (every
+    linear of 8 layer copies of the 2B-class layer plus the vocab head, M = 1,
+    dependency levels per `--levels`) and the same 1 GiB device copy as the
+    calibration of the byte counters."""
+    import torch
+    args.launch = "chain"
+    total, step, ev, step_bytes, record, ctx = decode_sweep(args, "w8", LAYER_SHAPES, HEAD, [1], args.layers)
+    for _ in range(args.steps):
+        step()
+    a = torch.empty(1 << 30, dtype=torch.uint8, device=torch.device("cuda", 0))
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "decode-pmc", "levels": args.levels, "bytes_per_launch": step_bytes[1],
+                      "copy_bytes": 1 << 30}), flush=True)
     return 0
 
 
@@ -583,9 +696,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode-w8",
                     choices=["decode-w8", "decode-w4", "prefill", "chain-w4", "single", "head-pmc",
-                             "prefill-pmc", "engine-w8", "engine-w4", "layout", "prefill-9b"])
+                             "prefill-pmc", "decode-pmc", "engine-w8", "engine-w4", "layout", "prefill-9b"])
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--launch", default="chain", choices=["chain", "graph"],
+                    help="decode workloads: one persistent chain launch per M, or one launch per GEMV "
+                         "replayed as a HIP graph")
+    ap.add_argument("--levels", default=None, choices=["layer", "flat"],
+                    help="chain dependency levels: per decode layer, or all independent (default: flat for "
+                         "the decode sweeps, whose shapes are independent; layer for the 9B-class decode chain)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--detail", action="store_true", help="per-shape table on stderr")
@@ -609,10 +728,16 @@ def main() -> int:
         return head_pmc(args)
     if wl == "prefill-pmc":
         return prefill_pmc(args)
+    if wl == "decode-pmc":
+        return decode_pmc(args)
     if wl == "layout":
         return layout_bench(args)
     ms = [1, 2, 4]
     roof = None
+    if args.no_graph:
+        args.launch = "graph"
+    if args.levels is None:
+        args.levels = "layer" if args.workload == "chain-w4" else "flat"
     if wl in ("decode-w8", "decode-w4", "chain-w4", "single"):
         kind = "w4" if wl in ("decode-w4", "chain-w4") else "w8"
         if wl == "chain-w4":
@@ -621,24 +746,49 @@ def main() -> int:
             shapes, head, layers, ms = [], ("gate", 2048, 6144), 0, [1]
         else:
             shapes, head, layers = LAYER_SHAPES, HEAD, args.layers
+        if wl == "single":
+            args.launch = "graph"
         total, step, head_ev, head_bytes, record, ctx = decode_sweep(args, kind, shapes, head, ms, layers)
         t = time_steps(step, args.steps, args.warmup, record)
         value = total / t / 1e9
-        # dominant kernel: the vocabulary-head GEMV, every launch of the timed steps
-        # (M = 1, 2, 4), timed live with HIP events on its launch stream
+        # dominant kernel, every launch of the timed steps timed live with HIP events on
+        # its launch stream: the chain kernel (one launch per M: the whole step's
+        # linears), or with per-GEMV launches the vocabulary-head GEMV
         durs = [(M, e0.elapsed_time(e1) * 1e-3) for M in ms for (e0, e1) in head_ev[M]]
         dur = sum(d for _, d in durs) / len(durs)
         hb = sum(head_bytes[M] for M, _ in durs) / len(durs)
         achieved = hb / dur / 1e9
-        tag = f"{kind}-{head[1]}x{head[2]}"
+        if args.launch == "chain":
+            tag = f"chain-{kind}-{wl}"
+            kname = (f"chain_kernel {kind}: {layers} layer copies x {len(shapes)} linears + vocab head "
+                     f"{head[1]}x{head[2]}, {args.levels} levels, M={'/'.join(map(str, ms))}")
+        else:
+            tag = f"{kind}-{head[1]}x{head[2]}"
+            kname = f"skinny_kernel {kind} vocab head {head[1]}x{head[2]}, M={'/'.join(map(str, ms))}"
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(tag),
-                "kernel": f"skinny_kernel {kind} vocab head {head[1]}x{head[2]}, M={'/'.join(map(str, ms))}",
-                "bytes_per_launch": int(hb), "avg_launch_us": round(dur * 1e6, 2)}
-        if args.detail:
+                "kernel": kname, "bytes_per_launch": int(hb), "avg_launch_us": round(dur * 1e6, 2)}
+        if args.detail and args.launch != "chain":
             detail_table(ctx, kind, shapes, head, ms)
         per_m = {M: sum(e0.elapsed_time(e1) for e0, e1 in head_ev[M]) / len(head_ev[M]) for M in ms}
-        log("vocab head per-launch us by M: " + ", ".join(f"M={M}: {v * 1e3:.1f}" for M, v in per_m.items()))
+        log(("chain" if args.launch == "chain" else "vocab head") + " per-launch us by M: " +
+            ", ".join(f"M={M}: {v * 1e3:.1f} ({head_bytes[M] / v / 1e6:.0f} GB/s)" for M, v in per_m.items()))
+        other = None
+        if args.launch == "chain":
+            for M, ch in ctx[6].items():
+                if ch.wait_error():
+                    log(f"chain M={M}: a dependency wait gave up")
+                    return 1
+            # the same step with the other dependency structure, for comparison
+            main_levels = args.levels
+            args.levels = "flat" if main_levels == "layer" else "layer"
+            tot2, step2, ev2, sb2, rec2, ctx2 = decode_sweep(args, kind, shapes, head, ms, layers, reuse=ctx)
+            t2 = time_steps(step2, max(3, args.steps // 2), 2, rec2)
+            other = {"levels": args.levels, "GB_per_s": round(tot2 / t2 / 1e9, 1),
+                     "ms_per_step": round(t2 * 1e3, 4)}
+            log(f"same step with {args.levels} levels: {tot2 / t2 / 1e9:.0f} GB/s")
+            args.levels = main_levels
+            del ctx2
         unit = "GB/s"
         config = {"workload": {"decode-w8": "int8 decode GEMV sweep, 2B-class layer shapes + vocab head",
                                "decode-w4": "W4 g128 decode GEMV sweep, 2B-class layer shapes + vocab head",
@@ -647,7 +797,11 @@ def main() -> int:
                   "rows_M": ms, "layer_copies": layers,
                   "shapes_KN": [[K, N] for (_, K, N) in shapes] + [[head[1], head[2]]],
                   "bytes_per_step": total,
-                  "launch": "hipgraph per M for layer shapes, eager vocab head" if not args.no_graph else "eager"}
+                  "launch": ({"chain": f"one persistent chain launch per M ({args.levels} dependency levels)",
+                              "graph": "hipgraph per M for layer shapes, eager vocab head"}[args.launch]
+                             if not args.no_graph else "eager")}
+        if other is not None:
+            config["other_levels"] = other
         dtype = "f16 x int8" if kind == "w8" else "f16 x int4"
     elif wl in ("engine-w8", "engine-w4"):
         kind = wl.split("-")[1]

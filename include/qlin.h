@@ -174,6 +174,54 @@ int qlin_linear_w4(const void* x, int x_dtype, int M, int K, int64_t ldx,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Decode chains: many A16 GEMVs in one persistent launch
+ *
+ * A chain is a list of jobs, each an A16 linear as qlin_linear_w8 / qlin_linear_w4
+ * computes it, for the same M (1-16 rows).  Jobs carry a dependency level: levels
+ * start at 0 and rise by at most 1 along the list, and the jobs of level L > 0 read
+ * their activations only after every job of level L-1 has written its output (so a
+ * job may read another's output, or add to a residual another job wrote).  One
+ * qlin_chain_run launch computes every job: the linears of a whole decode step with
+ * no kernel boundary between them.  No reference counterpart as a function: the
+ * reference launches one kernel per linear and names whole-step decode capture as its
+ * next step (ENGINEERING.md:383-399); each job replaces one such launch.
+ * ------------------------------------------------------------------------- */
+typedef struct qlin_chain_job {
+  const void* x;          /* fp16 activations [M][ldx] */
+  int64_t ldx;
+  const void* w;          /* W8: int8 [K][N]; W4: packed uint8 [K/2][N] */
+  const void* scale;      /* W8: [N]; W4: [K/group][N] */
+  int scale_dtype;        /* QLIN_F16, QLIN_BF16 or QLIN_F32 */
+  const uint8_t* zero;    /* W4 zeros [K/group][N] or NULL (z = 8); NULL for W8 */
+  int K, N;               /* W8: K % 32 == 0; W4: K % 128 == 0; N % 16 == 0 */
+  int group;              /* 0 = W8; 128 = W4 group 128 (the only W4 group chains take) */
+  void* out;              /* 16-bit [M][ldo] */
+  int out_dtype;          /* QLIN_F16 or QLIN_BF16 */
+  int64_t ldo;
+  const void* residual;   /* out_dtype [M][ldr] or NULL; may alias out */
+  int64_t ldr;
+  int level;              /* dependency level */
+} qlin_chain_job;
+
+/* Bytes of device memory a chain plan needs (0 if the jobs are invalid; the reason
+ * is in qlin_last_error()). */
+size_t qlin_chain_bytes(const qlin_chain_job* jobs, int njobs, int M);
+
+/* Validates the jobs and writes the plan (descriptors, work-unit table, zeroed
+ * counters; room for split-K partials) into `plan`, caller-owned device memory of
+ * at least qlin_chain_bytes() bytes, 16-byte aligned, kept for as long as the chain
+ * is run.  Synchronizes `stream` once (the host image is copied).  The pointers of
+ * the jobs are fixed in the plan: run it again after writing new inputs in place. */
+int qlin_chain_init(const qlin_chain_job* jobs, int njobs, int M, void* plan, size_t plan_bytes,
+                    void* stream);
+
+/* Runs every job of the plan in one launch on `stream`, asynchronously; capturable
+ * in a HIP graph.  The plan's counters return to zero when the launch ends.  Launches
+ * of one plan must not overlap in time.  The int at byte offset 20 of the plan
+ * becomes nonzero if a dependency wait gave up (it polls about 4 M times). */
+int qlin_chain_run(void* plan, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Layout entry points (bit-exactness checks of the unpack / dequant)
  * ------------------------------------------------------------------------- */
 

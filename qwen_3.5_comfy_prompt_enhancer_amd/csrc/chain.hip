@@ -1,0 +1,722 @@
+// Persistent multi-GEMV launch ("chain"): the decode-step linears of many layers in one
+// kernel, gfx950.
+//
+// A chain is a list of A16 GEMV jobs (fp16 activations x[M][K], M <= 16; W8 int8 [K][N]
+// with per-column scales, or W4 packed nibbles [K/2][N] with group-128 scales and
+// optional zeros -- the engine layouts of weights.py:297-309) with dependency levels:
+// the jobs of level L > 0 read their activations only after every job of level L-1
+// has written its output.  One launch runs the whole list: the decode step of a model
+// (per layer q/k/v, o, gate/up, down, then the vocabulary head) with no kernel
+// boundary between GEMVs.  This is the reference's own stated next step for a decode
+// that is dispatch-bound at one launch per linear (ENGINEERING.md:383-399).
+//
+//   * Work unit = (job, 128-column tile, K range of 4 waves x 128 rows): 64 KB of W8
+//     weights, 32 KB of packed W4 (one group of 128 per wave).  Workgroups of 4 waves
+//     take units from 8 queues (workgroup b from queue b % 8; queue q hands out units
+//     q, q + 8, ... in order; the next index is fetched while the current unit runs),
+//     so a unit only ever waits for units of lower levels, all taken before it: every
+//     wait ends whether or not all workgroups are resident.
+//   * A unit issues all of its weight (and scale, zero) loads first, then, above level
+//     0, waits for the level below (one thread polls the level's done flag with a
+//     bounded spin), then reads its activations with device-coherent loads (level 0:
+//     issued with the weights).  The next unit's loads go out as soon as this unit's
+//     partial stores have completed.
+//   * Each wave computes its 128-row K range for the tile's 128 columns on
+//     v_mfma_f32_16x16x32_f16 with exactly converted weights (the skinny decode
+//     kernel's operand construction: qlin_dev.h w8_pair_f16 / w4_pair_offset with the
+//     per-group offset correction); the 4 waves are summed in LDS in wave order.
+//   * A tile split over several units (K splits) exchanges fp32 partials through
+//     device-coherent stores and an arrival counter; the last unit to arrive sums the
+//     splits in split order (deterministic), applies the W8 column scale and the
+//     residual (one fmaf), and stores the 16-bit output with device-coherent stores.
+//     After those stores complete it counts the tile for its job; a job's last tile
+//     counts the job for its level, and a level's last job sets the level's flag.
+//   * The K order of an output depends on (K, N) only, so rows of an M = 4 step equal
+//     an M = 1 step bit for bit.
+//   * The last workgroup to leave resets the queues, the exit and level counters and
+//     the flags, so a plan can be launched again (and replayed in a HIP graph) without
+//     clearing.
+#include <stddef.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "../../include/qlin.h"
+#include "qlin_dev.h"
+#include "qlin_internal.h"
+
+namespace qlin {
+namespace {
+
+constexpr int CW = 4;              // waves per workgroup = per work unit
+constexpr int CT = 64 * CW;
+constexpr int TNC = 128;           // columns per tile: 16 lanes x 8 columns
+constexpr int TNP = TNC + 4;       // padded LDS row
+constexpr int W8_STEPS = 4;        // 32-wide K steps per wave per unit (W8)
+constexpr int W4_STEPS = 4;        // (W4: one group of 128)
+constexpr int KU_W8 = CW * W8_STEPS * 32;  // K rows per unit: 512
+constexpr int KU_W4 = CW * W4_STEPS * 32;  // 512
+constexpr int kSpinLimit = 1 << 22;        // polls of a dependency before giving up
+
+// Device descriptor of one job.
+struct alignas(16) ChainJob {
+  const _Float16* x;
+  long long ldx;
+  const uint8_t* w;
+  const void* s;
+  const uint8_t* z;
+  void* out;
+  long long ldo;
+  const void* res;
+  long long ldr;
+  long long part;   // first float of this job's partials within the partial region
+  int K, N, wk, sdt, odt;
+  int ntiles, splits, unit0, cnt0, level, index;
+};
+
+// Header at the start of a plan (device memory).
+struct alignas(16) ChainHdr {
+  int magic, nunits, njobs, nlevels;
+  int M, err, ncnt, w4;
+  long long jobs_off, unit_off, need_off, cnt_off, flag_off, part_off, bytes;
+};
+constexpr int kMagic = 0x71636831;  // "qch1"
+
+// Counters (uint32 indices from cnt_off).  Every counter that many workgroups update
+// sits on a 128-byte line of its own: atomics on one address serialize (about 18 ns
+// each, measured), so the hot ones are spread out.
+//   [32 q]                              queue q (q < kQueues): units q, q + 8, q + 16, ...
+//   [32 kQueues]                        workgroups that have left
+//   [kLevel0 + 32 l]                    finished jobs of level l
+//   [kLevel0 + 32 nlevels + 16 j]       finished tiles of job j (reset by its last tile)
+//   [... + 16 njobs + cnt0 + tile]      split-K arrivals of a tile (reset by its last unit)
+// Level done flags follow in a region of their own, one per 128-byte line.
+constexpr int kQueues = 8;
+constexpr int kLevel0 = 32 * (kQueues + 1);
+
+__device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ u32x4 ld_x_coherent(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1);
+}
+
+template <int COLS>
+__device__ __forceinline__ void ld8(const uint8_t* p, uint32_t d[2]) {
+  const u32x2 v = *(const u32x2*)p;
+  d[0] = v.x;
+  d[1] = v.y;
+}
+
+// Registers a unit's weights (and W4 group scales, zeros) are loaded into.
+template <bool W4>
+struct UnitRegs {
+  static constexpr int STEPS = W4 ? W4_STEPS : W8_STEPS;
+  static constexpr int NR = W4 ? 4 : 8;  // weight rows per lane per step
+  uint32_t w[STEPS][NR][2];
+  u32x4 sraw[2];  // W4: raw group scales of the lane's 8 columns
+  uint32_t zr[2];  // W4: their zeros
+};
+
+// A unit's place: job descriptor (uniform), tile, K split.
+struct UnitPos {
+  ChainJob J;
+  int tile, split;
+};
+
+__device__ __forceinline__ UnitPos decode_unit(const ChainJob* __restrict__ jobs, const int* __restrict__ unit_job,
+                                               int u) {
+  UnitPos p;
+  const int jn = __builtin_amdgcn_readfirstlane(unit_job[u]);
+  p.J = jobs[jn];
+  const int local = u - p.J.unit0;
+  p.tile = local / p.J.splits;
+  p.split = local - p.tile * p.J.splits;
+  return p;
+}
+
+// The wave's first K row and 32-wide steps of a unit.
+template <bool W4>
+__device__ __forceinline__ void wave_range(const UnitPos& P, int* k0, int* nsteps) {
+  constexpr int kw = UnitRegs<W4>::STEPS * 32;
+  const int wave = threadIdx.x >> 6;
+  *k0 = P.split * (CW * kw) + wave * kw;
+  *nsteps = max(0, min(UnitRegs<W4>::STEPS, (P.J.K - *k0) / 32));  // W4: 0 or 4 (K % 128 == 0)
+}
+
+// Issues every weight / scale / zero load of a unit (nothing waits for them here).
+template <bool W4>
+__device__ __forceinline__ void issue_loads(const UnitPos& P, UnitRegs<W4>& R) {
+  constexpr int STEPS = UnitRegs<W4>::STEPS, NR = UnitRegs<W4>::NR;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int K = P.J.K, N = P.J.N;
+  int k0, nsteps;
+  wave_range<W4>(P, &k0, &nsteps);
+  const int col = P.tile * TNC + j * 8;  // lane's first column; N % 16 == 0, so col < N => col + 8 <= N
+  const int ccl = col < N ? col : 0;
+  // steps past the wave's range (the last split of a K that is not a multiple of the
+  // unit) load the wave's last in-range step again, or step 0 of the matrix if it has
+  // none: every register is written, so none stays live from the previous unit
+  const int kb = nsteps > 0 ? k0 : 0;
+  const int slast = nsteps > 0 ? nsteps - 1 : 0;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int sc = s < slast ? s : slast;
+    const long long r0 = W4 ? (long long)((kb + 32 * sc) / 2 + 4 * g) : (long long)(kb + 32 * sc + 8 * g);
+    const uint8_t* base = P.J.w + r0 * N + ccl;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) ld8<8>(base + (long long)r * N, R.w[s][r]);
+  }
+  if constexpr (W4) {
+    const int gi = min(k0 / 128, K / 128 - 1);
+    const long long idx = (long long)gi * N + ccl;
+    const bool f32 = P.J.sdt == DT_F32;
+    const uint8_t* sb = (const uint8_t*)P.J.s + idx * (f32 ? 4 : 2);
+    R.sraw[0] = *(const u32x4*)sb;
+    R.sraw[1] = *(const u32x4*)(sb + (f32 ? 16 : 0));
+    if (P.J.z) ld8<8>(P.J.z + idx, R.zr);
+    else R.zr[0] = R.zr[1] = 0x08080808u;
+  }
+}
+
+// Activations of a unit, device-coherent (an earlier job may have written them).  Every
+// step is loaded (no branch around the accumulators): a step past the wave's range, a
+// row past M, or every step when `now` is false reads at an offset beyond the buffer's
+// range, which returns zeros and moves no data.
+template <bool W4>
+__device__ __forceinline__ void load_x(const UnitPos& P, int M, bool now, u32x4 xv[UnitRegs<W4>::STEPS]) {
+  constexpr int STEPS = UnitRegs<W4>::STEPS;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  int k0, nsteps;
+  wave_range<W4>(P, &k0, &nsteps);
+  const __amdgpu_buffer_rsrc_t xr = part_rsrc(P.J.x, (unsigned)(((long long)(M - 1) * P.J.ldx + P.J.K) * 2));
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const unsigned off = (unsigned)(((long long)j * P.J.ldx + k0 + 32 * s + 8 * g) * 2);
+    xv[s] = ld_x_coherent(xr, (now && s < nsteps && j < M) ? off : 0xFFFFFFF0u);
+  }
+}
+
+// Level L's tile count (cnt[2 + L]) reaches need[L] -> its done flag (one per 128-byte
+// line from flag_off) is set by the unit whose tile completed it.
+__device__ __forceinline__ unsigned* level_flag(uint8_t* plan, const ChainHdr& H, int l) {
+  return (unsigned*)(plan + H.flag_off) + 32 * l;
+}
+
+// The read-only parts of the plan (job descriptors, unit table, level sizes) come as
+// separate restrict-qualified arguments so that the compiler reads them with scalar
+// loads: the descriptors' pointers then stay in scalar registers.
+template <bool W4>
+__global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void chain_kernel(uint8_t* plan, const ChainJob* __restrict__ jobs,
+                                                   const int* __restrict__ unit_job,
+                                                   const unsigned* __restrict__ need) {
+  constexpr int STEPS = UnitRegs<W4>::STEPS;
+  const ChainHdr H = *(const ChainHdr*)plan;
+  unsigned* const cnt = (unsigned*)(plan + H.cnt_off);
+  __shared__ float red[CW * 16 * TNP];
+  __shared__ int s_unit, s_flag;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int j = lane & 15, g = lane >> 4;
+  const int M = H.M;
+  const int R4 = ((M + 3) >> 2) * 4;
+  const int nch = M * (TNC / 4);  // 4-column chunks of a tile's real rows
+  const long long MT = (long long)M * TNC;
+
+  // Workgroup b takes units from queue q = b % 8 (unit q + 8 i for the i-th take):
+  // every queue hands its units out in increasing order, so a unit only waits for units
+  // taken before it (in its own queue or in another, whose workgroups run).
+  const int q = (int)(blockIdx.x % kQueues);
+  unsigned* const queue = cnt + 32 * q;
+  if (tid == 0)
+    s_unit = (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kQueues + q;
+  __syncthreads();
+  int u = s_unit;
+  UnitRegs<W4> R;
+  UnitPos P;
+  u32x4 xv[STEPS];
+  // a level-0 unit's activations go out with its weights; a later level's after its wait
+  if (u < H.nunits) {
+    P = decode_unit(jobs, unit_job, u);
+    issue_loads<W4>(P, R);
+    load_x<W4>(P, M, P.J.level == 0, xv);
+  }
+  while (u < H.nunits) {
+    // the next unit's index, fetched now and read after this unit's partial stores
+    int nxt = 0;
+    if (tid == 0) nxt = (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kQueues + q;
+    const ChainJob& J = P.J;
+    const int K = J.K, N = J.N, S = J.splits, tile = P.tile, split = P.split;
+    int k0, nsteps;
+    wave_range<W4>(P, &k0, &nsteps);
+
+    // ---------------- dependency: level L waits for every tile of level L-1 ----------------
+    if (J.level > 0) {
+      if (tid == 0) {
+        const unsigned* f = level_flag(plan, H, J.level - 1);
+        int spins = 0, nap = 1;
+        while (ld_agent(f) == 0u) {
+          if (++spins > kSpinLimit) {
+            __hip_atomic_store((int*)(plan + offsetof(ChainHdr, err)), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          if (nap == 1) __builtin_amdgcn_s_sleep(1);
+          else if (nap == 2) __builtin_amdgcn_s_sleep(2);
+          else __builtin_amdgcn_s_sleep(6);
+          nap = nap < 3 ? nap + 1 : 3;
+        }
+      }
+      __syncthreads();
+    }
+
+    // ---------------- activations of a dependent unit, read after its wait ----------------
+    if (J.level > 0) load_x<W4>(P, M, true, xv);
+
+    // ---------------- MFMA ----------------
+    f32x4 acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!W4) {
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) {
+        const f16x8 av = bitcast<f16x8>(xv[s]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int q = t >> 2, b = t & 3;
+          u32x4 bw;
+          bw.x = w8_pair_f16(R.w[s][0][q], R.w[s][1][q], b);
+          bw.y = w8_pair_f16(R.w[s][2][q], R.w[s][3][q], b);
+          bw.z = w8_pair_f16(R.w[s][4][q], R.w[s][5][q], b);
+          bw.w = w8_pair_f16(R.w[s][6][q], R.w[s][7][q], b);
+          acc[t] = mfma_f16(av, bitcast<f16x8>(bw), acc[t]);
+        }
+      }
+    } else {
+      // (1024 + lo, 64 + hi) operands; the wave's K range is one group of 128, folded
+      // once at its end: scale * (acc - (c1 + z c2))
+      f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f}, c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+      const f16x8 boff = f16x8{(_Float16)1024.0f, (_Float16)64.0f, (_Float16)1024.0f, (_Float16)64.0f,
+                               (_Float16)1024.0f, (_Float16)64.0f, (_Float16)1024.0f, (_Float16)64.0f};
+      const f16x8 bone = f16x8{(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                               (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) {
+        const f16x8 av = bitcast<f16x8>(xv[s]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int q = t >> 2, b = t & 3;
+          u32x4 bw;
+          bw.x = w4_pair_offset(R.w[s][0][q], b);
+          bw.y = w4_pair_offset(R.w[s][1][q], b);
+          bw.z = w4_pair_offset(R.w[s][2][q], b);
+          bw.w = w4_pair_offset(R.w[s][3][q], b);
+          acc[t] = mfma_f16(av, bitcast<f16x8>(bw), acc[t]);
+        }
+        c1 = mfma_f16(av, boff, c1);
+        c2 = mfma_f16(av, bone, c2);
+      }
+      float sc[8];
+      cvt_scale4(R.sraw[0], J.sdt, sc);
+      if (J.sdt == DT_F32) {
+        cvt_scale4(R.sraw[1], J.sdt, sc + 4);
+      } else {
+        const u32x4 hi = u32x4{R.sraw[0].z, R.sraw[0].w, 0u, 0u};
+        cvt_scale4(hi, J.sdt, sc + 4);
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float z = (float)((R.zr[t >> 2] >> (8 * (t & 3))) & 0xFFu);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] = sc[t] * (acc[t][r] - fmaf(z, c2[r], c1[r]));
+      }
+    }
+
+    // ---------------- workgroup sum over the 4 waves (wave order) ----------------
+    if (4 * g < R4) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wave * 16 + 4 * g + r) * TNP + j * 8 + t] = acc[t][r];
+    }
+    __syncthreads();
+    float* const part = (float*)(plan + H.part_off) + J.part;
+    const __amdgpu_buffer_rsrc_t pr = part_rsrc(part, (unsigned)((long long)J.ntiles * S * MT * 4));
+    f32x4 v[2];  // chunks tid and tid + 256 (M <= 16: at most 512 chunks)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + CT * i;
+      v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (c < nch) {
+        const int row = c >> 5, cc = (c & 31) * 4;
+        f32x4 sum = *(const f32x4*)&red[row * TNP + cc];
+#pragma unroll
+        for (int wv = 1; wv < CW; ++wv) sum = sum + *(const f32x4*)&red[(wv * 16 + row) * TNP + cc];
+        v[i] = sum;
+      }
+    }
+    if (S > 1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = tid + CT * i;
+        if (c < nch) st_coherent(v[i], pr, (unsigned)((((long long)tile * S + split) * MT + c * 4) * 4));
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this thread has completed
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+    if (tid == 0) s_unit = (int)nxt;
+    __syncthreads();
+
+    // ---------------- the next unit's weights go out now (its registers are free) ----------------
+    const int un = s_unit;
+    UnitPos Pn;
+    if (un < H.nunits) {
+      Pn = decode_unit(jobs, unit_job, un);
+      issue_loads<W4>(Pn, R);
+      load_x<W4>(Pn, M, Pn.J.level == 0, xv);
+    }
+
+    // ---------------- split-K: the last unit of a tile to arrive sums the splits in order ----------------
+    bool finish = true;
+    if (S > 1) {
+      if (tid == 0) {
+        unsigned* cp = cnt + kLevel0 + 32 * H.nlevels + 16 * H.njobs + J.cnt0 + tile;
+        const unsigned prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (unsigned)(S - 1);
+        if (last) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_flag = last;
+      }
+      __syncthreads();
+      finish = s_flag != 0;  // uniform
+      if (finish) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int c = tid + CT * i;
+          if (c < nch) {
+            const unsigned off = (unsigned)(((long long)tile * S * MT + c * 4) * 4);
+            f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int p0 = 0; p0 < S; p0 += 8) {
+              f32x4 pp[8];
+#pragma unroll
+              for (int q = 0; q < 8; ++q) pp[q] = ld_coherent(pr, off + (unsigned)(min(p0 + q, S - 1) * MT * 4));
+#pragma unroll
+              for (int q = 0; q < 8; ++q)
+                if (p0 + q < S) sum = (p0 + q == 0) ? pp[q] : sum + pp[q];
+            }
+            v[i] = sum;
+          }
+        }
+      }
+    }
+
+    // ---------------- epilogue: column scale (W8), residual, 16-bit store, level count ----------------
+    if (finish) {
+      const __amdgpu_buffer_rsrc_t orr = part_rsrc(J.out, (unsigned)(((long long)(M - 1) * J.ldo + N) * 2));
+      const __amdgpu_buffer_rsrc_t rr =
+          part_rsrc(J.res ? J.res : J.out, (unsigned)(((long long)(M - 1) * (J.res ? J.ldr : J.ldo) + N) * 2));
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = tid + CT * i;
+        if (c < nch) {
+          const int row = c >> 5, gc = tile * TNC + (c & 31) * 4;
+          if (gc < N) {
+            float cs[4] = {1.f, 1.f, 1.f, 1.f};
+            if constexpr (!W4) cvt_scale4(ld_scale4_raw(J.s, J.sdt, gc), J.sdt, cs);
+            float y[4];
+            if (J.res) {
+              const u32x2 rv = bitcast<u32x2>(
+                  __builtin_amdgcn_raw_buffer_load_b64(rr, (unsigned)(((long long)row * J.ldr + gc) * 2), 0, kCpolSc1));
+              const uint32_t rw[2] = {rv.x, rv.y};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint16_t h = (uint16_t)(rw[e >> 1] >> (16 * (e & 1)));
+                y[e] = fmaf(v[i][e], cs[e], J.odt == DT_BF16 ? bf16_to_f32(h) : (float)bitcast<_Float16>(h));
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) y[e] = v[i][e] * cs[e];
+            }
+            u32x2 o;
+            o.x = (uint32_t)to_out16(y[0], J.odt) | ((uint32_t)to_out16(y[1], J.odt) << 16);
+            o.y = (uint32_t)to_out16(y[2], J.odt) | ((uint32_t)to_out16(y[3], J.odt) << 16);
+            __builtin_amdgcn_raw_buffer_store_b64(o, orr, (unsigned)(((long long)row * J.ldo + gc) * 2), 0, kCpolSc1);
+          }
+        }
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);  // the tile's output has reached the coherence point
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __syncthreads();
+      if (tid == 0) {
+        // the job's last tile counts the job for its level; the level's last job sets the flag
+        unsigned* jc = cnt + kLevel0 + 32 * H.nlevels + 16 * J.index;
+        const unsigned prev = __hip_atomic_fetch_add(jc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev + 1 == (unsigned)J.ntiles) {
+          __hip_atomic_store(jc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const unsigned pl =
+              __hip_atomic_fetch_add(cnt + kLevel0 + 32 * J.level, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (pl + 1 == need[J.level])
+            __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    __syncthreads();  // every thread is done with red, s_unit and s_flag of this unit
+    P = Pn;
+    u = un;
+  }
+  // the last workgroup to leave resets the queue, exit and level counters and flags
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(cnt + 32 * kQueues, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == gridDim.x - 1) {
+      for (int l = 0; l < H.nlevels; ++l) {
+        __hip_atomic_store(cnt + kLevel0 + 32 * l, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(level_flag(plan, H, l), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      for (int qq = 0; qq < kQueues; ++qq) __hip_atomic_store(cnt + 32 * qq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(cnt + 32 * kQueues, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+struct Layout {
+  long long jobs_off, unit_off, need_off, cnt_off, flag_off, part_off, bytes;
+  int nunits, nlevels, ncnt, w4;
+  long long part_floats;
+};
+
+long long align256(long long v) { return (v + 255) / 256 * 256; }
+
+int fail_chain(int code, const char* fmt, int i, int a = 0, int b = 0) {
+  char msg[256];
+  snprintf(msg, sizeof(msg), fmt, i, a, b);
+  return set_error(code, msg);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Validates the jobs and computes the plan layout (and, if `jobs_out`, the descriptors).
+int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::vector<ChainJob>* jobs_out,
+                 std::vector<int>* unit_job, std::vector<unsigned>* need) {
+  if (!jobs || njobs <= 0) return set_error(QLIN_ERR_INVALID, "qlin_chain: no jobs");
+  if (M < 1 || M > 16) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: M=%d (1-16 rows)", M);
+  long long units = 0, ncnt = 0, parts = 0;
+  int prev_level = 0;
+  const bool w4_chain = jobs[0].group != 0;
+  for (int i = 0; i < njobs; ++i) {
+    const qlin_chain_job& q = jobs[i];
+    const bool w4 = q.group != 0;
+    if (q.K <= 0 || q.N <= 0) return fail_chain(QLIN_ERR_INVALID, "qlin_chain: job %d: bad sizes K=%d N=%d", i, q.K, q.N);
+    if (w4 && q.group != 128)
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: W4 group %d (group 128 only)", i, q.group);
+    if (q.K % (w4 ? 128 : 32) != 0)
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: K=%d not a multiple of %d", i, q.K, w4 ? 128 : 32);
+    if (q.N % 16 != 0) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: N=%d not a multiple of 16", i, q.N);
+    if (!q.x || !q.w || !q.scale || !q.out) return fail_chain(QLIN_ERR_INVALID, "qlin_chain: job %d: null pointer", i);
+    if (!aligned16(q.x) || !aligned16(q.w) || !aligned16(q.scale) || (q.zero && !aligned16(q.zero)) ||
+        !aligned16(q.out) || (q.residual && !aligned16(q.residual)))
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: pointers must be 16-byte aligned", i);
+    if (q.ldx < q.K || q.ldx % 8 != 0 || q.ldo < q.N || q.ldo % 4 != 0 ||
+        (q.residual && (q.ldr < q.N || q.ldr % 4 != 0)))
+      return fail_chain(QLIN_ERR_INVALID, "qlin_chain: job %d: row strides (ldx >= K, multiple of 8; ldo/ldr >= N, multiple of 4)", i);
+    if (q.scale_dtype != QLIN_F16 && q.scale_dtype != QLIN_BF16 && q.scale_dtype != QLIN_F32)
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: scale dtype %d", i, q.scale_dtype);
+    if (q.out_dtype != QLIN_F16 && q.out_dtype != QLIN_BF16)
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: output dtype %d", i, q.out_dtype);
+    if (!w4 && q.zero) return fail_chain(QLIN_ERR_INVALID, "qlin_chain: job %d: zeros given for a W8 job", i);
+    if (w4 != w4_chain)
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: a chain holds W8 jobs or W4 jobs, not both", i);
+    if (q.level < 0 || q.level < prev_level || q.level > prev_level + 1 || (i == 0 && q.level != 0))
+      return fail_chain(QLIN_ERR_INVALID, "qlin_chain: job %d: level %d (levels start at 0 and rise by at most 1)", i,
+                        q.level);
+    // byte offsets within 32-bit buffer ranges
+    if (((long long)(M - 1) * q.ldx + q.K) * 2 >= (1LL << 31) || ((long long)(M - 1) * q.ldo + q.N) * 2 >= (1LL << 31))
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: activation or output too large", i);
+    prev_level = q.level;
+    const int ku = w4 ? KU_W4 : KU_W8;
+    const int splits = (q.K + ku - 1) / ku;
+    const int ntiles = (q.N + TNC - 1) / TNC;
+    if ((long long)ntiles * splits * M * TNC * 4 >= (1LL << 31))
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: partials too large", i);
+    if (jobs_out) {
+      ChainJob d;
+      memset(&d, 0, sizeof(d));
+      d.x = (const _Float16*)q.x;
+      d.ldx = q.ldx;
+      d.w = (const uint8_t*)q.w;
+      d.s = q.scale;
+      d.z = q.zero;
+      d.out = q.out;
+      d.ldo = q.ldo;
+      d.res = q.residual;
+      d.ldr = q.residual ? q.ldr : 0;
+      d.part = parts;
+      d.K = q.K;
+      d.N = q.N;
+      d.wk = w4 ? WK_W4 : WK_W8;
+      d.sdt = q.scale_dtype;
+      d.odt = q.out_dtype;
+      d.ntiles = ntiles;
+      d.splits = splits;
+      d.unit0 = (int)units;
+      d.cnt0 = (int)ncnt;
+      d.level = q.level;
+      d.index = i;
+      jobs_out->push_back(d);
+      for (long long t = 0; t < (long long)ntiles * splits; ++t) unit_job->push_back(i);
+      if ((int)need->size() <= q.level) need->resize(q.level + 1, 0u);
+      (*need)[q.level] += 1u;  // jobs of the level
+    }
+    units += (long long)ntiles * splits;
+    if (splits > 1) {
+      ncnt += ntiles;
+      parts += (long long)ntiles * splits * M * TNC;
+    }
+    if (units > (1LL << 30)) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: too many work units (job %d)", i);
+  }
+  L->nunits = (int)units;
+  L->nlevels = prev_level + 1;
+  L->ncnt = (int)(kLevel0 + 32LL * L->nlevels + 16LL * njobs + ncnt);
+  L->part_floats = parts;
+  L->jobs_off = align256(sizeof(ChainHdr));
+  L->unit_off = align256(L->jobs_off + (long long)njobs * sizeof(ChainJob));
+  L->need_off = align256(L->unit_off + units * 4);
+  L->w4 = w4_chain ? 1 : 0;
+  L->cnt_off = align256(L->need_off + (long long)L->nlevels * 4);
+  L->flag_off = align256(L->cnt_off + (long long)L->ncnt * 4);
+  L->part_off = align256(L->flag_off + (long long)L->nlevels * 128);
+  L->bytes = align256(L->part_off + parts * 4);
+  return QLIN_OK;
+}
+
+std::mutex g_mu;
+int g_grid[64][2];                       // resident workgroups per device and weight kind
+struct PlanInfo {
+  const void* plan;
+  int w4;
+  long long jobs_off, unit_off, need_off;
+};
+std::vector<PlanInfo> g_plans;  // plans initialized in this process
+
+int chain_grid(int w4, int* grid) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) return set_error(QLIN_ERR_HIP, "qlin_chain_run: hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_grid[dev][w4] == 0) {
+    int cus = 0, per = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, w4 ? chain_kernel<true> : chain_kernel<false>, CT, 0);
+    if (e != hipSuccess || cus <= 0 || per <= 0) return set_error(QLIN_ERR_HIP, "qlin_chain_run: occupancy query failed");
+    g_grid[dev][w4] = cus * per;
+  }
+  *grid = g_grid[dev][w4];
+  return QLIN_OK;
+}
+
+void remember_plan(const PlanInfo& info) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (auto& p : g_plans)
+    if (p.plan == info.plan) {
+      p = info;
+      return;
+    }
+  g_plans.push_back(info);
+}
+
+bool find_plan(const void* plan, PlanInfo* out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (auto& p : g_plans)
+    if (p.plan == plan) {
+      *out = p;
+      return true;
+    }
+  return false;
+}
+
+}  // namespace
+}  // namespace qlin
+
+extern "C" size_t qlin_chain_bytes(const qlin_chain_job* jobs, int njobs, int M) {
+  qlin::Layout L;
+  if (qlin::layout_chain(jobs, njobs, M, &L, nullptr, nullptr, nullptr) != QLIN_OK) return 0;
+  return (size_t)L.bytes;
+}
+
+extern "C" int qlin_chain_init(const qlin_chain_job* jobs, int njobs, int M, void* plan, size_t plan_bytes,
+                               void* stream) {
+  using namespace qlin;
+  set_error(QLIN_OK, "");
+  Layout L;
+  std::vector<ChainJob> d;
+  std::vector<int> uj;
+  std::vector<unsigned> need;
+  const int rc = layout_chain(jobs, njobs, M, &L, &d, &uj, &need);
+  if (rc != QLIN_OK) return rc;
+  if (!plan || plan_bytes < (size_t)L.bytes) return set_error(QLIN_ERR_WORKSPACE, "qlin_chain_init: plan buffer too small");
+  if (!aligned16(plan)) return set_error(QLIN_ERR_UNSUPPORTED, "qlin_chain_init: plan must be 16-byte aligned");
+  need.resize(L.nlevels, 0u);
+  // header, descriptors, unit table, level sizes and zeroed counters, in one copy
+  std::vector<uint8_t> img((size_t)L.part_off, 0);
+  ChainHdr h;
+  memset(&h, 0, sizeof(h));
+  h.magic = kMagic;
+  h.nunits = L.nunits;
+  h.njobs = njobs;
+  h.nlevels = L.nlevels;
+  h.M = M;
+  h.ncnt = L.ncnt;
+  h.jobs_off = L.jobs_off;
+  h.unit_off = L.unit_off;
+  h.need_off = L.need_off;
+  h.cnt_off = L.cnt_off;
+  h.flag_off = L.flag_off;
+  h.part_off = L.part_off;
+  h.w4 = L.w4;
+  h.bytes = L.bytes;
+  memcpy(img.data(), &h, sizeof(h));
+  memcpy(img.data() + L.jobs_off, d.data(), d.size() * sizeof(ChainJob));
+  memcpy(img.data() + L.unit_off, uj.data(), uj.size() * sizeof(int));
+  memcpy(img.data() + L.need_off, need.data(), need.size() * sizeof(unsigned));
+  hipError_t e = hipMemcpyAsync(plan, img.data(), img.size(), hipMemcpyHostToDevice, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);  // img is freed on return
+  if (e != hipSuccess) {
+    char msg[160];
+    snprintf(msg, sizeof(msg), "qlin_chain_init: copy: HIP error %d (%s)", (int)e, hipGetErrorString(e));
+    return set_error(QLIN_ERR_HIP, msg);
+  }
+  remember_plan(PlanInfo{plan, L.w4, L.jobs_off, L.unit_off, L.need_off});
+  return QLIN_OK;
+}
+
+extern "C" int qlin_chain_run(void* plan, void* stream) {
+  using namespace qlin;
+  set_error(QLIN_OK, "");
+  if (!plan || !aligned16(plan)) return set_error(QLIN_ERR_INVALID, "qlin_chain_run: null or misaligned plan");
+  PlanInfo pi;
+  if (!find_plan(plan, &pi))
+    return set_error(QLIN_ERR_INVALID, "qlin_chain_run: plan not initialized by qlin_chain_init in this process");
+  int grid = 0;
+  const int rc = chain_grid(pi.w4, &grid);
+  if (rc != QLIN_OK) return rc;
+  uint8_t* const p = (uint8_t*)plan;
+  const ChainJob* jobs = (const ChainJob*)(p + pi.jobs_off);
+  const int* units = (const int*)(p + pi.unit_off);
+  const unsigned* need = (const unsigned*)(p + pi.need_off);
+  if (pi.w4) hipLaunchKernelGGL(chain_kernel<true>, dim3(grid), dim3(CT), 0, (hipStream_t)stream, p, jobs, units, need);
+  else hipLaunchKernelGGL(chain_kernel<false>, dim3(grid), dim3(CT), 0, (hipStream_t)stream, p, jobs, units, need);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char msg[160];
+    snprintf(msg, sizeof(msg), "qlin_chain_run: HIP error %d (%s)", (int)e, hipGetErrorString(e));
+    return set_error(QLIN_ERR_HIP, msg);
+  }
+  return QLIN_OK;
+}

@@ -71,7 +71,9 @@ _SIGS = {
     "qlin_w4_zeros_unpack": [_P, _I, _I, _I, _I, _P, _P],
 }
 
-EXPORTS = ("qlin_version", "qlin_last_error", "qlin_workspace_bytes", *_SIGS)
+# the decode-chain entry points are declared in kernels/chain.py (they take a struct array)
+EXPORTS = ("qlin_version", "qlin_last_error", "qlin_workspace_bytes", *_SIGS,
+           "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run")
 
 
 def lib() -> ctypes.CDLL:

@@ -27,8 +27,9 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 22
-    for n in ("qlin_gemm_i8", "qlin_gemm_i8_noalloc", "qlin_gemm_w4", "qlin_proj3_i8", "qlin_proj3_w4",
+    assert len(names) == 25
+    for n in ("qlin_gemm_i8", "qlin_gemm_i8_noalloc", "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run",
+              "qlin_gemm_w4", "qlin_proj3_i8", "qlin_proj3_w4",
               "qlin_mlp_gate_up_quant_i8", "qlin_mlp_gate_up_quant_w4", "qlin_linear_w8",
               "qlin_linear_w4", "qlin_w4_unpack", "qlin_w4_dequant_f32",
               "qlin_requant_w4_sym", "qlin_requant_w8_row", "qlin_w4_repack_gptq",
@@ -154,3 +155,26 @@ def test_w4_dispatch_follows_weight_dtype():
         gemm.gemm_i8(a, s, p, ps, out)
     with pytest.raises(ValueError, match=r"uint8 \[K/2=64"):
         gemm.proj3(a, s, p, ps, None, None, None, None, out)
+
+
+def test_chain_validation_without_gpu():
+    """qlin_chain_bytes validates the job list on the host: a level that jumps by 2, a
+    W4 group other than 128 and a misaligned pointer are refused with a message."""
+    qlin, L = _lib()
+    from qwen35_amd.kernels import chain as CH
+    CH._bind(L)
+
+    def job(level=0, group=0, K=2048, N=512, x=0x10000):
+        return CH._Job(x=x, ldx=K, w=0x20000, scale=0x30000, scale_dtype=qlin.QLIN_F16, zero=None, K=K, N=N,
+                       group=group, out=0x40000, out_dtype=qlin.QLIN_F16, ldo=N, residual=None, ldr=0,
+                       level=level)
+    ok = (CH._Job * 2)(job(0), job(1))
+    assert L.qlin_chain_bytes(ok, 2, 4) > 0
+    bad = (CH._Job * 2)(job(0), job(2))
+    assert L.qlin_chain_bytes(bad, 2, 4) == 0
+    assert b"level" in L.qlin_last_error()
+    assert L.qlin_chain_bytes((CH._Job * 1)(job(group=64)), 1, 1) == 0
+    assert b"group" in L.qlin_last_error()
+    assert L.qlin_chain_bytes((CH._Job * 1)(job(x=0x10008)), 1, 1) == 0
+    assert b"aligned" in L.qlin_last_error()
+    assert L.qlin_chain_bytes((CH._Job * 1)(job()), 1, 17) == 0
