@@ -24,7 +24,7 @@
 //     trick): lane (g, j) reads 4 adjacent columns of its 8 K rows and builds the B
 //     operands of 4 MFMAs; MFMA column j of instruction t is output column 4j + t.
 //     W8 values are exact integers in fp16 and the column scale multiplies the fp32
-//     result; W4 (nibble - z) is exact and the group scale is folded into the fp16
+//     result; W4 (nibble - z) is exact and the group scale (times 2^8) is folded into the fp16
 //     weight (one fp16 rounding per weight).
 //   * NSTAGE K tiles of 64 in an LDS ring with one barrier per tile.  Before it, a
 //     wave waits (vmcnt) for the copy of the next tile it needs; after it, the stage
@@ -101,10 +101,18 @@ __device__ __forceinline__ void dma_v(const void* vaddr, uint32_t m0) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(vaddr), "{m0}"(m0) : "memory");
 }
 
+// W4 group scales enter the fp16 weight values multiplied by 2^8 (exact), and the
+// epilogue multiplies the fp32 result by 2^-8 (exact): the products (nibble - z) * s * 2^8
+// are normal fp16 numbers for scales in [2^-22, 17] (|nibble - z| <= 15), where an
+// unshifted scale below 2^-14 would lose precision as a subnormal.
+constexpr float kW4ScaleShift = 256.0f;
+
 __device__ __forceinline__ _Float16 scale_f16(uint32_t bits, int dt) {
-  if (dt == DT_F32) return (_Float16)bitcast<float>(bits);
-  if (dt == DT_BF16) return (_Float16)bf16_to_f32((uint16_t)bits);
-  return bitcast<_Float16>((uint16_t)bits);
+  float s;
+  if (dt == DT_F32) s = bitcast<float>(bits);
+  else if (dt == DT_BF16) s = bf16_to_f32((uint16_t)bits);
+  else s = (float)bitcast<_Float16>((uint16_t)bits);
+  return (_Float16)(s * kW4ScaleShift);
 }
 
 }  // namespace
@@ -481,7 +489,7 @@ void prefill_kernel(const TlArgs a) {
   // wave's 64 (MFMA t = column 4j + t)
   const int colb = n0 + wn * 64 + 4 * j;
   if (kg != 0 || colb >= N) return;
-  float cs[4] = {1.f, 1.f, 1.f, 1.f};
+  float cs[4] = {1.f / kW4ScaleShift, 1.f / kW4ScaleShift, 1.f / kW4ScaleShift, 1.f / kW4ScaleShift};
   if constexpr (WK == WK_W8) cvt_scale4(csraw, a.sdt, cs);
   // The output type and the residual are uniform: branch once here, so each of the
   // 128 values of a lane costs a multiply, a conversion and (with a residual) an add.

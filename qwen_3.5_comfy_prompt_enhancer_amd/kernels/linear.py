@@ -11,7 +11,11 @@ are the gfx950 counterpart and read the same packed layouts as the engine kernel
 
 `x` is fp16 [M, K] (row stride may exceed K); `out` / `residual` are fp16 or bf16
 [M, N] row-major.  Weights are converted to fp16 exactly in registers and
-multiplied on MFMA with fp32 accumulation; scales are applied in fp32.
+multiplied on MFMA with fp32 accumulation.  W8 column scales multiply the fp32
+result.  W4 group scales are applied in fp32 per group for M <= 16; for M > 16 (the
+tiled prefill kernel) each group scale, times 2^8, is folded into the fp16 weight
+values (one fp16 rounding; exact range for scales in [2^-22, 17]) and the result is
+multiplied by 2^-8 in fp32.
 """
 from __future__ import annotations
 

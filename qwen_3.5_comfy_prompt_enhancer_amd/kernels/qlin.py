@@ -7,7 +7,7 @@ The device helpers the reference's kernels/common.py defines as Triton functions
 
 * loading `libqlin.so` with ctypes and declaring its C ABI (include/qlin.h);
 * tensor -> pointer / dtype-code marshalling and the current HIP stream;
-* the per-device split-K workspace (allocated once, zero-filled, reused);
+* the split-K workspace of each (device, stream) (allocated once, zero-filled, reused);
 * status code -> exception (ValueError for bad arguments, RuntimeError otherwise).
 
 There is no fallback: if the library is missing or no GPU is present, the
@@ -128,22 +128,41 @@ def check(status: int, name: str) -> None:
     raise RuntimeError(msg)
 
 
-_ws: dict[int, torch.Tensor] = {}
+_ws: dict[tuple[int, int], torch.Tensor] = {}
+_ws_first: dict[int, torch.Tensor] = {}
 _ws_lock = threading.Lock()
 
 
-def workspace(device: torch.device) -> torch.Tensor:
-    """Per-device split-K workspace (zero-filled once; the kernels leave their
-    arrival counters at zero after every call, so it is never cleared again)."""
+def workspace(device: torch.device, stream: int | None = None) -> torch.Tensor:
+    """Split-K workspace of (device, stream), zero-filled once; the kernels leave their
+    arrival counters at zero after every call, so it is never cleared again.
+
+    Each stream gets its own, so calls running at the same time on two streams never
+    share arrival counters or partial sums.  A call made while a stream is being
+    captured into a HIP graph, on a stream that has no workspace yet, uses the
+    device's first workspace (a zero-fill cannot go into the graph): call once
+    outside capture first, and do not replay such a graph concurrently with other
+    calls on the device."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    w = _ws.get(idx)
-    if w is None:
-        with _ws_lock:
-            w = _ws.get(idx)
-            if w is None:
-                nbytes = lib().qlin_workspace_bytes()
-                w = torch.zeros(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
-                _ws[idx] = w
+    if stream is None:
+        stream = torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream
+    key = (idx, int(stream))
+    w = _ws.get(key)
+    if w is not None:
+        return w
+    with _ws_lock:
+        w = _ws.get(key)
+        if w is None:
+            if torch.cuda.is_current_stream_capturing():
+                w = _ws_first.get(idx)
+                if w is None:
+                    raise RuntimeError("the first quantized-linear call on a device must run outside HIP graph "
+                                       "capture (it allocates the split-K workspace)")
+                return w
+            nbytes = lib().qlin_workspace_bytes()
+            w = torch.zeros(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
+            _ws[key] = w
+            _ws_first.setdefault(idx, w)
     return w
 
 

@@ -578,3 +578,21 @@ def test_config4_chain_shapes_full_size(M, K, N):
     H.assert_out_close(y.cpu()[:, cols], H.linear_w4_ref_cols(x, packed, s, z, cols))
     y2 = _run_w4((x * 2).to(torch.float16), packed, s, z)
     _assert_doubled(y, y2)
+
+
+@pytest.mark.parametrize("scale", [1e-5, 8.0])
+@pytest.mark.parametrize("M", [4, 64, 300])
+def test_w4_extreme_group_scales(scale, M):
+    """bf16 group scales near 1e-5 (below fp16's normal range on their own) and near 8,
+    through the decode path (M = 4, scales applied in fp32) and the prefill tiles
+    (M = 64, 300: the scale times 2^8 is folded into the fp16 weight), against the
+    oracle."""
+    K, N = 1024, 1024
+    x = H.act_f16(M, K, seed=900 + M)
+    packed, s, z = H.w4(K, N, seed=901, group=128, zeros="random")
+    s = (torch.rand(s.shape, generator=H.gen(902)) * scale + scale / 2).to(torch.bfloat16)
+    y = _run_w4(x, packed, s, z)
+    ref = H.linear_w4_ref_cols(x, packed, s, z, np.arange(N))
+    if scale >= 1.0:  # keep the fp16 output in range
+        assert np.abs(ref).max() < 6e4
+    H.assert_out_close(y.cpu(), ref)

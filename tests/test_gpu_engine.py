@@ -470,3 +470,60 @@ def test_engine_scale_property_full_size(M, K, N):
     gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y)
     gemm.gemm_i8(a.cuda(), (as_ * 2).cuda(), b.cuda(), bs.cuda(), y2)
     assert torch.equal(y2, (y.float() * 2).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+def test_wide_decode_residual_edge_tile(kind):
+    """A wide decode launch (N >= 131072 takes one-wave 256-column tiles for W4, 128 for
+    W8) whose last tile is partial, with a residual and 4 rows: the epilogue's later
+    passes read the residual only inside the row."""
+    gemm, _ = _g()
+    M, K, N = 4, 1024, 131072 + 144
+    a, as_ = H.engine_act(M, K, seed=920)
+    if kind == "w8":
+        b, bs = H.engine_w8(K, N, seed=921)
+        bz = None
+    else:
+        b, bs, bz = _w4_engine(K, N, seed=921, zeros="random")
+    hid = torch.randn((M, N), generator=H.gen(922)).to(torch.bfloat16)
+    h = hid.cuda()
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), h, residual=h, b_z=None if bz is None else bz.cuda())
+    cols = np.concatenate([np.arange(N - 512, N), H.sample_cols(N - 512, 1024, seed=923)])
+    if kind == "w8":
+        ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy()[:, cols], bs.numpy()[cols],
+                            residual=_bf16(hid)[:, cols])
+    else:
+        ref = R.gemm_w4_ref(a.numpy(), as_.numpy(), b.numpy()[:, cols], _bf16(bs)[:, cols], bz.numpy()[:, cols],
+                            residual=_bf16(hid)[:, cols])
+    H.assert_out_close(h.cpu()[:, cols], ref)
+
+
+def test_two_streams_use_separate_workspaces():
+    """Split-K decode calls issued on two streams at once: each stream has its own
+    workspace (arrival counters and partials), so both results equal the same calls
+    made on one stream."""
+    gemm, _ = _g()
+    from qwen35_amd.kernels import qlin as C
+    M, K, N = 4, 6144, 2048                     # a split-K decode plan
+    a, as_ = H.engine_act(M, K, seed=930)
+    b, bs = H.engine_w8(K, N, seed=931)
+    a2, as2 = H.engine_act(M, K, seed=932)
+    a, as_, a2, as2, b, bs = a.cuda(), as_.cuda(), a2.cuda(), as2.cuda(), b.cuda(), bs.cuda()
+    ref1 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ref2 = torch.empty_like(ref1)
+    gemm.gemm_i8(a, as_, b, bs, ref1)
+    gemm.gemm_i8(a2, as2, b, bs, ref2)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs1 = [torch.empty_like(ref1) for _ in range(20)]
+    outs2 = [torch.empty_like(ref1) for _ in range(20)]
+    torch.cuda.synchronize()
+    for o1, o2 in zip(outs1, outs2):
+        with torch.cuda.stream(s1):
+            gemm.gemm_i8(a, as_, b, bs, o1)
+        with torch.cuda.stream(s2):
+            gemm.gemm_i8(a2, as2, b, bs, o2)
+    torch.cuda.synchronize()
+    assert C.workspace(ref1.device, s1.cuda_stream).data_ptr() != C.workspace(ref1.device, s2.cuda_stream).data_ptr()
+    for o1, o2 in zip(outs1, outs2):
+        assert torch.equal(o1, ref1)
+        assert torch.equal(o2, ref2)
