@@ -632,7 +632,7 @@ def decode_pmc(args):
 def layout_bench(args):
     """The load-time layout producers at a 9B-class projection (K=4096, N=12288):
     GPU requantization of fp32 weights (W8 per column, W4 g32) and the GPTQ / AWQ int4
-    repacks.  HBM-bound byte work: algorithmic bytes = one read of the input and one
+    repacks (GPTQ, AWQ, compressed-tensors).  HBM-bound byte work: algorithmic bytes = one read of the input and one
     write of the outputs; time per launch from HIP events on the launching stream."""
     import torch
     dev = torch.device("cuda", 0)
@@ -642,11 +642,13 @@ def layout_bench(args):
     w = (torch.randn((K, N), generator=gen) * 0.02).to(dev)
     qg = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), generator=gen, dtype=torch.int32).to(dev)
     qa = torch.randint(-2 ** 31, 2 ** 31 - 1, (K, N // 8), generator=gen, dtype=torch.int32).to(dev)
+    qc = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 8), generator=gen, dtype=torch.int32).to(dev)
     cases = {
         "requant_w8_row": (lambda: lay.requant_w8_row(w), 4 * K * N + K * N + 4 * N),
         "requant_w4_sym_g32": (lambda: lay.requant_w4_sym(w, 32), 4 * K * N + K * N // 2 + 2 * (K // 32) * N),
         "w4_repack_gptq": (lambda: lay.gptq_w4_to_engine(qg), K * N // 2 + K * N // 2),
         "w4_repack_awq": (lambda: lay.awq_w4_to_engine(qa), K * N // 2 + K * N // 2),
+        "w4_repack_ct": (lambda: lay.ct_w4_to_engine(qc, K=K), K * N // 2 + K * N // 2),
     }
     res = {}
     for name, (fn, nbytes) in cases.items():

@@ -265,6 +265,14 @@ int qlin_w4_repack_gptq(const int32_t* qweight, int K, int N, uint8_t* packed, v
  * (quant_formats.py:211-220, 442-444, 466).  K even, N % 8 == 0, packed 8-byte aligned. */
 int qlin_w4_repack_awq(const int32_t* qweight, int K, int N, uint8_t* packed, void* stream);
 
+/* compressed-tensors pack-quantized symmetric int4 weight_packed int32 [N, W] (8
+ * straight-order K nibbles per word, one output feature per row) -> engine packed
+ * [K/2, N]: the nibble decode, trim to K and pair packing of the transposed nibbles in
+ * decode_ct (quant_formats.py:199-208, 311-316, 348-349).  Even K <= 8 W, N % 16 == 0,
+ * packed 16-byte aligned.  The group scales [N, K/G] are transposed by the caller
+ * (quant_formats.py:350). */
+int qlin_w4_repack_ct(const int32_t* weight_packed, int N, int W, int K, uint8_t* packed, void* stream);
+
 /* qzeros int32 [G, N/8] (8 N-nibbles per word; AWQ order if awq_order) -> uint8
  * zeros[G, N] = nibble + add: GPTQ's effective zero is nibble + 1
  * (quant_formats.py:396-400, 418-424), AWQ's the nibble (quant_formats.py:445-446). */

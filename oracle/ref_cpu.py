@@ -311,6 +311,26 @@ def awq_w4_to_engine(qweight) -> np.ndarray:
     return pack_pairs(nib)
 
 
+def ct_w4_to_engine(weight_packed, K: int | None = None) -> np.ndarray:
+    """compressed-tensors pack-quantized symmetric int4: weight_packed int32 [N, W]
+    (8 K-nibbles per word in straight order along the input dimension, one output
+    feature per row) -> engine packed [K/2, N]: the straight-order nibble decode
+    (quant_formats.py:199-208, 311), the trim to K (quant_formats.py:315-316, 329),
+    then the pair packing of the transposed nibbles (quant_formats.py:348-349,
+    246-250).  K defaults to 8 W."""
+    qw = np.asarray(weight_packed)
+    nib = nibbles_i32(qw)
+    if K is not None:
+        nib = nib[:, :K]
+    return pack_pairs(nib.T)
+
+
+def ct_scale_to_engine(weight_scale) -> np.ndarray:
+    """compressed-tensors group scales [N, K/G] -> engine [K/G, N]
+    (quant_formats.py:324-327, 350)."""
+    return np.ascontiguousarray(np.asarray(weight_scale).T)
+
+
 def gptq_zeros(qzeros, plus_one: bool = True) -> np.ndarray:
     """GPTQ qzeros int32 [G, N/8] -> uint8 zeros [G, N], N-packed straight order, with
     the +1 of the effective zero (quant_formats.py:396-400, 418-424)."""

@@ -917,6 +917,19 @@ int qlin_w4_repack_awq(const int32_t* qweight, int K, int N, uint8_t* packed, vo
   return hip_status("qlin_w4_repack_awq", launch_repack_awq(qweight, K, N, packed, (hipStream_t)stream));
 }
 
+int qlin_w4_repack_ct(const int32_t* weight_packed, int N, int W, int K, uint8_t* packed, void* stream) {
+  g_err[0] = 0;
+  if (N < 0 || W < 0 || K < 0 || K % 2 != 0 || (long long)K > 8LL * W)
+    return fail(QLIN_ERR_INVALID, "qlin_w4_repack_ct: need even K <= 8 W (N=%d W=%d K=%d)", N, W, K);
+  if (N % 16 != 0) return fail(QLIN_ERR_UNSUPPORTED, "qlin_w4_repack_ct: N=%d is not a multiple of 16", N);
+  if ((long long)N * K == 0) return QLIN_OK;
+  if (!weight_packed || !packed) return fail(QLIN_ERR_INVALID, "qlin_w4_repack_ct: null pointer");
+  if (!aligned(weight_packed, 4) || !aligned(packed, 16))
+    return fail(QLIN_ERR_UNSUPPORTED, "qlin_w4_repack_ct: weight_packed 4-byte and packed 16-byte aligned");
+  if ((K / 2 + 63) / 64 > 65535) return fail(QLIN_ERR_UNSUPPORTED, "qlin_w4_repack_ct: K=%d too large", K);
+  return hip_status("qlin_w4_repack_ct", launch_repack_ct(weight_packed, N, W, K, packed, (hipStream_t)stream));
+}
+
 int qlin_w4_zeros_unpack(const int32_t* qzeros, int G, int N, int awq_order, int add, uint8_t* zeros,
                          void* stream) {
   g_err[0] = 0;

@@ -239,6 +239,45 @@ __global__ void repack_awq_kernel(const uint32_t* __restrict__ qw, int K, int N,
 }
 
 // z[g][8c + j] = nibble (awq ? kAwqRev[j] : j) of qzeros[g][c], plus `add`
+// compressed-tensors int4 (quant_formats.py:282-354): weight_packed int32 [N][W], 8
+// straight-order K nibbles per word, one output feature per row.  Byte i of word w
+// holds nibbles k = 8w + 2i (low) and 8w + 2i + 1 (high): exactly the engine's pair
+// byte of packed row 4w + i, column n.  So the engine layout [K/2][N] is the byte
+// transpose of the [N][4W] byte view, cut to K/2 rows.  A 64 x 64 byte tile goes
+// through LDS: loaded as dwords along a source row, stored 16 bytes along N.
+__global__ void repack_ct_kernel(const uint32_t* __restrict__ qw, int N, int W, int KB,
+                                 uint8_t* __restrict__ packed) {
+  __shared__ uint8_t t[64][64 + 4];  // [column n - n0][packed row j - j0]
+  const int n0 = blockIdx.x * 64, j0 = blockIdx.y * 64;
+  const int tid = threadIdx.x;
+  {
+    const int r = tid >> 2, c = (tid & 3) * 16;  // source row n0 + r, bytes j0 + c ...
+    const int n = n0 + r;
+    if (n < N) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = j0 + c + 4 * q;  // first byte of the word
+        if (j < KB) {
+          const uint32_t v = qw[(long long)n * W + (j >> 2)];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) t[r][c + 4 * q + b] = (uint8_t)(v >> (8 * b));
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int jr = tid >> 2, c = (tid & 3) * 16;  // packed row j0 + jr, columns n0 + c ...
+  const int j = j0 + jr, n = n0 + c;
+  if (j < KB && n < N) {  // N % 16 == 0: the 16 columns are all in range
+    uint32_t w4[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w4[q] = (uint32_t)t[c + 4 * q][jr] | ((uint32_t)t[c + 4 * q + 1][jr] << 8) |
+              ((uint32_t)t[c + 4 * q + 2][jr] << 16) | ((uint32_t)t[c + 4 * q + 3][jr] << 24);
+    *(u32x4*)(packed + (long long)j * N + n) = u32x4{w4[0], w4[1], w4[2], w4[3]};
+  }
+}
+
 __global__ void zeros_unpack_kernel(const uint32_t* __restrict__ qz, int G, int N, int awq, int add,
                                     uint8_t* __restrict__ z) {
   const long long total = (long long)G * N;
@@ -320,6 +359,13 @@ hipError_t launch_repack_gptq(const int32_t* qw, int K, int N, uint8_t* packed, 
 hipError_t launch_repack_awq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st) {
   hipLaunchKernelGGL(repack_awq_kernel, grid_for((long long)(K / 2) * (N / 8)), dim3(256), 0, st,
                      (const uint32_t*)qw, K, N, packed);
+  return hipGetLastError();
+}
+
+hipError_t launch_repack_ct(const int32_t* qw, int N, int W, int K, uint8_t* packed, hipStream_t st) {
+  const int KB = K / 2;
+  hipLaunchKernelGGL(repack_ct_kernel, dim3((unsigned)((N + 63) / 64), (unsigned)((KB + 63) / 64)), dim3(256), 0, st,
+                     (const uint32_t*)qw, N, W, KB, packed);
   return hipGetLastError();
 }
 

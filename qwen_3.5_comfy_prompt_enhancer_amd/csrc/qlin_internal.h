@@ -121,6 +121,7 @@ hipError_t launch_requant_w4(const float* w, int K, int N, int group, uint8_t* p
 hipError_t launch_requant_w8(const float* w, int K, int N, int8_t* q, float* scale, hipStream_t st);
 hipError_t launch_repack_gptq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st);
 hipError_t launch_repack_awq(const int32_t* qw, int K, int N, uint8_t* packed, hipStream_t st);
+hipError_t launch_repack_ct(const int32_t* qw, int N, int W, int K, uint8_t* packed, hipStream_t st);
 hipError_t launch_zeros_unpack(const int32_t* qz, int G, int N, int awq, int add, uint8_t* z, hipStream_t st);
 
 }  // namespace qlin

@@ -21,7 +21,10 @@ and the external int4 formats' nibble decode into the engine layout:
 * `awq_w4_to_engine(qweight)`: int32 [K, N/8] in AWQ order -> packed [K/2, N]
   (quant_formats.py:442-444, 466);
 * `gptq_zeros(qzeros, plus_one=True)` / `awq_zeros(qzeros)`: int32 [G, N/8] -> uint8
-  [G, N] (quant_formats.py:396-400, 445-446).
+  [G, N] (quant_formats.py:396-400, 445-446);
+* `ct_w4_to_engine(weight_packed, K=None, weight_scale=None)`: compressed-tensors
+  symmetric int4, int32 [N, W] -> packed [K/2, N], and its group scales [N, K/G] ->
+  [K/G, N] (quant_formats.py:282-354, the native-group branch at 348-350).
 """
 from __future__ import annotations
 
@@ -30,7 +33,7 @@ import torch
 from . import qlin as C
 
 __all__ = ["w4_unpack", "w4_dequant_f32", "w8_dequant_f32", "requant_w4_sym", "requant_w8_row",
-           "gptq_w4_to_engine", "awq_w4_to_engine", "gptq_zeros", "awq_zeros"]
+           "gptq_w4_to_engine", "awq_w4_to_engine", "gptq_zeros", "awq_zeros", "ct_w4_to_engine"]
 
 
 def w4_unpack(packed: torch.Tensor) -> torch.Tensor:
@@ -147,3 +150,23 @@ def gptq_zeros(qzeros: torch.Tensor, plus_one: bool = True) -> torch.Tensor:
 def awq_zeros(qzeros: torch.Tensor) -> torch.Tensor:
     """AWQ qzeros int32 [G, N/8] (AWQ nibble order) -> uint8 zeros [G, N]."""
     return _zeros(qzeros, 1, 0)
+
+
+def ct_w4_to_engine(weight_packed: torch.Tensor, K: int | None = None, weight_scale: torch.Tensor | None = None):
+    """compressed-tensors pack-quantized symmetric int4 -> the engine W4 layout.
+
+    `weight_packed` int32 [N, W] (8 K-nibbles per word, straight order; one output
+    feature per row), `K` the input features (default 8 W; `weight_shape` of the
+    checkpoint).  Returns packed uint8 [K/2, N] (the value of a nibble is nibble - 8:
+    zero point 8, the engine's default), and, if `weight_scale` [N, K/G] is given, the
+    scales transposed to [K/G, N] as `decode_ct` returns them (quant_formats.py:350)."""
+    weight_packed = _i32_words("weight_packed", weight_packed)
+    N, W = weight_packed.shape
+    K = 8 * W if K is None else int(K)
+    packed = torch.empty((K // 2, N), dtype=torch.uint8, device=weight_packed.device)
+    C.call("qlin_w4_repack_ct", C.ptr(weight_packed), N, W, K, C.ptr(packed), C.stream_of(weight_packed))
+    if weight_scale is None:
+        return packed
+    if weight_scale.dim() != 2 or weight_scale.shape[0] != N:
+        raise ValueError(f"weight_scale must be [N={N}, K/G]")
+    return packed, weight_scale.t().contiguous()

@@ -69,6 +69,7 @@ _SIGS = {
     "qlin_w4_repack_gptq": [_P, _I, _I, _P, _P],
     "qlin_w4_repack_awq": [_P, _I, _I, _P, _P],
     "qlin_w4_zeros_unpack": [_P, _I, _I, _I, _I, _P, _P],
+    "qlin_w4_repack_ct": [_P, _I, _I, _I, _P, _P],
 }
 
 # the decode-chain entry points are declared in kernels/chain.py (they take a struct array)

@@ -27,13 +27,13 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 25
+    assert len(names) == 26
     for n in ("qlin_gemm_i8", "qlin_gemm_i8_noalloc", "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run",
               "qlin_gemm_w4", "qlin_proj3_i8", "qlin_proj3_w4",
               "qlin_mlp_gate_up_quant_i8", "qlin_mlp_gate_up_quant_w4", "qlin_linear_w8",
               "qlin_linear_w4", "qlin_w4_unpack", "qlin_w4_dequant_f32",
               "qlin_requant_w4_sym", "qlin_requant_w8_row", "qlin_w4_repack_gptq",
-              "qlin_w4_repack_awq", "qlin_w4_zeros_unpack"):
+              "qlin_w4_repack_awq", "qlin_w4_zeros_unpack", "qlin_w4_repack_ct"):
         assert n in names
 
 

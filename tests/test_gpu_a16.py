@@ -167,6 +167,34 @@ def test_repacked_gptq_feeds_the_gemm():
     H.assert_out_close(y, ref)
 
 
+@pytest.mark.parametrize("N,W,K", [(48, 25, 200), (64, 8, 62), (6144, 256, 2048), (4096, 1536, 12288)])
+def test_w4_repack_ct_bit_exact(N, W, K):
+    """compressed-tensors weight_packed int32 [N, W] -> engine packed [K/2, N] equals the
+    oracle bit for bit, partial tiles and a K short of 8 W included."""
+    layout, _ = _k()
+    qw = _rand_words(N, W, seed=23)
+    p = layout.ct_w4_to_engine(qw.cuda(), K=K)
+    assert p.shape == (K // 2, N) and p.dtype == torch.uint8
+    assert np.array_equal(p.cpu().numpy(), R.ct_w4_to_engine(qw.numpy(), K=K))
+
+
+def test_repacked_ct_feeds_the_gemm():
+    """A compressed-tensors symmetric int4 checkpoint (zero point 8, group 128),
+    decoded on the GPU, runs through the W4 GEMMs: decode (M = 4) and prefill tiles
+    (M = 96), against the oracle's dequantize + fp32 matmul of the same codes."""
+    layout, _ = _k()
+    K, N = 2048, 1024
+    qw = _rand_words(N, K // 8, seed=24)
+    s_ct = (torch.rand((N, K // 128), generator=H.gen(25)) * 1e-3).to(torch.bfloat16)
+    packed, s = layout.ct_w4_to_engine(qw.cuda(), K=K, weight_scale=s_ct.cuda())
+    assert torch.equal(s.cpu(), s_ct.t())
+    ref_packed = torch.from_numpy(R.ct_w4_to_engine(qw.numpy(), K=K))
+    for M in (4, 96):
+        x = H.act_f16(M, K, seed=26 + M)
+        y = _run_w4(x, packed.cpu(), s.cpu(), None)
+        H.assert_out_close(y, H.linear_w4_ref_cols(x, ref_packed, s_ct.t().contiguous(), None, np.arange(N)))
+
+
 def test_repack_bad_arguments_raise():
     layout, _ = _k()
     with pytest.raises(ValueError):

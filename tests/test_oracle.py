@@ -369,3 +369,35 @@ def test_zero_unpack_orders():
     assert np.array_equal(R.gptq_zeros(_awq_words(z, list(range(8)))), z + 1)
     assert np.array_equal(R.gptq_zeros(_awq_words(z, list(range(8))), plus_one=False), z)
     assert np.array_equal(R.awq_zeros(_awq_words(z)), z)
+
+
+def _ct_words(nib):
+    """nibbles [N, K] (one output feature per row) -> compressed-tensors words [N, K/8]:
+    nibble j of word w = element k = 8w + j of the row (straight order)."""
+    N, K = nib.shape
+    return _words_from_nibbles(nib.reshape(N, K // 8, 8))
+
+
+def test_ct_repack_known_answer_and_byte_transpose():
+    """Word 0x76543210 holds k = 0..7 = 0..7: the engine pair bytes of rows 0..3 are
+    0x10, 0x32, 0x54, 0x76, the word's own bytes.  In general the packed matrix is the
+    byte transpose of the [N, 4W] byte view of the words."""
+    w = np.array([[0x76543210]], dtype=np.int32)
+    assert R.ct_w4_to_engine(w)[:, 0].tolist() == [0x10, 0x32, 0x54, 0x76]
+    qw = RNG.integers(-2 ** 31, 2 ** 31, size=(24, 10), dtype=np.int64).astype(np.int32)
+    assert np.array_equal(R.ct_w4_to_engine(qw), qw.view(np.uint8).reshape(24, 40).T)
+    assert np.array_equal(R.ct_w4_to_engine(qw, K=62), qw.view(np.uint8).reshape(24, 40).T[:31])
+
+
+def test_ct_repack_round_trip_and_planted_mistake():
+    nib = RNG.integers(0, 16, size=(40, 64), dtype=np.uint8)
+    assert np.array_equal(R.unpack_w4(R.ct_w4_to_engine(_ct_words(nib))), nib.T)
+    # a decoder that put the odd K in the low nibble would not round-trip
+    swapped = R.ct_w4_to_engine(_ct_words(nib))
+    swapped = ((swapped >> 4) | (swapped << 4)).astype(np.uint8)
+    assert not np.array_equal(R.unpack_w4(swapped), nib.T)
+
+
+def test_ct_scale_transpose():
+    s = RNG.standard_normal((6, 4)).astype(np.float32)
+    assert np.array_equal(R.ct_scale_to_engine(s), s.T)
