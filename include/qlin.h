@@ -151,6 +151,107 @@ int qlin_mlp_gate_up_quant_w4(const int8_t* a_q, const float* a_s, int M, int K,
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Activation producers: the int8 codes + per-64 fp32 scales the engine-signature
+ * entry points consume, made from 16-bit activations.  Per 64 columns
+ * s = max(amax/127, 1e-8), q = round_half_away(y / s) clamped to +-127
+ * (kernels/norm.py:15-25).  The arithmetic is fixed operation by operation (fp32,
+ * no fused multiply-add; sums of squares in a fixed lane order; rsqrt as 1/sqrt;
+ * exp by Cody-Waite reduction and a degree-7 Taylor polynomial), so the codes do
+ * not depend on M or on which launch made them.
+ * ------------------------------------------------------------------------- */
+
+#define QLIN_PRO_RMSNORM 1
+#define QLIN_PRO_GATE_MUL 2
+#define QLIN_PRO_NORM_GATED 3
+
+/* y = x * rsqrt(mean(x^2) + eps) * (w + 1 if one_plus else w), quantized.
+ * x [M,K] bf16/fp16 (x_dtype), row stride ldx; w [K] (w_dtype bf16/fp16/fp32);
+ * q int8 [M,K] (row stride K), s fp32 [M,K/64].  K % 64 == 0.
+ * Replaces rmsnorm_quant (kernels/norm.py:48-57, kernel norm.py:28-41). */
+int qlin_rmsnorm_quant(const void* x, int64_t ldx, int x_dtype, const void* w, int w_dtype,
+                       int M, int K, float eps, int one_plus, int8_t* q, float* s, void* stream);
+
+/* y = a * sigmoid(g[gate column]), quantized; a [M,N] (row stride lda), g [M,*] (row
+ * stride ldg >= 2N) laid out as heads of 2*hd values with the gates in the second
+ * half; both `dtype` (bf16/fp16).  hd % 8 == 0, N % hd == 0, N % 64 == 0.
+ * Replaces gate_mul_quant (kernels/norm.py:182-188, kernel norm.py:168-179). */
+int qlin_gate_mul_quant(const void* a, int64_t lda, const void* g, int64_t ldg, int dtype,
+                        int M, int N, int hd, int8_t* q, float* s, void* stream);
+
+/* Per (row, head of hd): y = bf16(v * rsqrt(mean_head(v^2) + eps) * w * silu(z)),
+ * quantized.  v [T,N] contiguous, z [T,*] (row stride ldz), both `dtype`; w [hd]
+ * (w_dtype).  hd in {128, 256, 512}.
+ * Replaces norm_gated_quant (kernels/norm.py:127-137, kernel norm.py:95-124). */
+int qlin_norm_gated_quant(const void* v, const void* z, int64_t ldz, int dtype,
+                          const void* w, int w_dtype, int T, int N, int hd, float eps,
+                          int8_t* q, float* s, void* stream);
+
+/* The producers' exp on n fp32 values (test entry point: no reference counterpart;
+ * the reference uses Triton's exp). */
+int qlin_pro_exp_f32(const float* x, float* y, int n, void* stream);
+
+/* One producer, as the qlin_pro_* linears below take it. */
+typedef struct qlin_producer {
+  int kind;         /* QLIN_PRO_RMSNORM, QLIN_PRO_GATE_MUL or QLIN_PRO_NORM_GATED */
+  const void* x;    /* rmsnorm: x [M,K]; gate_mul: a [M,K]; norm_gated: v [M,K] contiguous */
+  int64_t ldx;      /* row stride of x (ignored for norm_gated) */
+  int x_dtype;      /* QLIN_BF16 or QLIN_F16, for x and g */
+  const void* g;    /* gate_mul: gate rows; norm_gated: z; rmsnorm: NULL */
+  int64_t ldg;
+  const void* w;    /* norm weight (rmsnorm [K], norm_gated [hd]); gate_mul: NULL */
+  int w_dtype;
+  int hd;           /* head size (gate_mul, norm_gated) */
+  int one_plus;     /* rmsnorm */
+  float eps;
+  int8_t* q;        /* optional: the codes [M,K] and scales [M,K/64] are written here */
+  float* s;         /*   too (NULL: not kept; they then pass through the workspace) */
+} qlin_producer;
+
+/* The engine-signature linears with their activation producer in the same call: no
+ * counterpart in the reference, whose engine launches the producer (kernels/norm.py)
+ * and then the linear (kernels/gemm.py / w4.py) -- e.g. rmsnorm_quant + proj3 at
+ * engine.py:220-226, gate_mul_quant + gemm_i8 at engine.py:265-268, norm_gated_quant +
+ * gemm_i8 at engine.py:236-240, rmsnorm_quant + mlp_gate_up_quant at engine.py:272-276.
+ * Results equal the two-call sequence bit for bit.  Decode-shaped launches make the
+ * codes of their rows and K range in a prologue, with their first weight loads in
+ * flight; wide launches (the vocab head) and prefill's tiled kernel run the producer
+ * as a launch of its own first.  The producer's inputs must not overlap `out`.
+ * Arguments after `K` are those of the entry point named in the suffix. */
+int qlin_pro_gemm_i8(const qlin_producer* pro, int M, int K,
+                     const int8_t* b, const void* b_s, int bs_dtype, int N,
+                     void* out, int64_t ldo, const void* residual, int64_t ldr,
+                     void* workspace, size_t workspace_bytes, void* stream);
+int qlin_pro_gemm_w4(const qlin_producer* pro, int M, int K,
+                     const uint8_t* b, const void* b_s, int bs_dtype, const uint8_t* b_z,
+                     int group, int N,
+                     void* out, int64_t ldo, const void* residual, int64_t ldr,
+                     void* workspace, size_t workspace_bytes, void* stream);
+int qlin_pro_proj3_i8(const qlin_producer* pro, int M, int K,
+                      const int8_t* w1, const void* s1, int n1,
+                      const int8_t* w2, const void* s2, int n2,
+                      const int8_t* w3, const void* s3, int n3, int bs_dtype,
+                      void* out, int64_t ldo,
+                      void* workspace, size_t workspace_bytes, void* stream);
+int qlin_pro_proj3_w4(const qlin_producer* pro, int M, int K,
+                      const uint8_t* w1, const void* s1, const uint8_t* z1, int n1,
+                      const uint8_t* w2, const void* s2, const uint8_t* z2, int n2,
+                      const uint8_t* w3, const void* s3, const uint8_t* z3, int n3,
+                      int bs_dtype, int group,
+                      void* out, int64_t ldo,
+                      void* workspace, size_t workspace_bytes, void* stream);
+int qlin_pro_mlp_gate_up_quant_i8(const qlin_producer* pro, int M, int K,
+                                  const int8_t* wg, const void* sg,
+                                  const int8_t* wu, const void* su, int bs_dtype, int N,
+                                  int8_t* out_q, float* out_s,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+int qlin_pro_mlp_gate_up_quant_w4(const qlin_producer* pro, int M, int K,
+                                  const uint8_t* wg, const void* sg, const uint8_t* zg,
+                                  const uint8_t* wu, const void* su, const uint8_t* zu,
+                                  int bs_dtype, int group, int N,
+                                  int8_t* out_q, float* out_s,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * A16 weight-only core (fp16 activations; the form the engine's linears take when
  * activations stay in floating point).  The reference computes this on its CPU path
  * as "dequantize through quant_formats.py (quant_formats.py:6-9), then an fp32

@@ -249,6 +249,150 @@ def mlp_gate_up_quant_ref(a_q, a_s, wg, sg, wu, su, zg=None, zu=None):
 
 
 # ----------------------------------------------------------------------------
+# Activation producers (kernels/norm.py): 16-bit activations -> int8 codes + per-64
+# fp32 scales, the input of every engine-signature linear
+#
+# The reference computes these in Triton, whose reduction order and rsqrt/exp are
+# implementation details; the kernels here fix them, and these functions restate the
+# fixed form operation by operation (float32, every operation rounded, no fused
+# multiply-add), so the int8 codes can be compared bit for bit.
+# ----------------------------------------------------------------------------
+
+# exp(x) = 2^n * exp(r), n = rint(x * log2(e)), r = x - n * ln2 with ln2 split in two
+# (Cody and Waite): LN2_HI has 15 significant bits, so n * LN2_HI is exact for |n| <= 127.
+LOG2E_F32 = np.float32(float.fromhex("0x1.715476p+0"))
+LN2_HI_F32 = np.float32(float.fromhex("0x1.62e4p-1"))
+LN2_LO_F32 = np.float32(float.fromhex("0x1.7f7d1cp-20"))
+# Taylor coefficients 1/7!, 1/6!, ..., 1/0! rounded to fp32 (Horner order)
+EXP_POLY_F32 = [np.float32(float.fromhex(h)) for h in (
+    "0x1.a01a02p-13", "0x1.6c16c2p-10", "0x1.111112p-7", "0x1.555556p-5",
+    "0x1.555556p-3", "0x1p-1", "0x1p+0", "0x1p+0")]
+
+
+def exp_f32(x) -> np.ndarray:
+    """exp in fp32 as the producer kernels compute it (they need no libm): Cody-Waite
+    reduction, the degree-7 Taylor polynomial of exp(r) on |r| <= ln2/2 in Horner
+    form, then the exact scaling by 2^n; +inf above 88, 0 below -87 (so no result is
+    subnormal).  Stands in for the reference's `tl.exp` / `tl.sigmoid`
+    (kernels/norm.py:178, kernels/common.py:32-34)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        n = np.rint(x * LOG2E_F32).astype(np.float32)
+        r = ((x - n * LN2_HI_F32) - n * LN2_LO_F32).astype(np.float32)
+        p = np.full_like(r, EXP_POLY_F32[0])
+        for c in EXP_POLY_F32[1:]:
+            p = (p * r).astype(np.float32)
+            p = (p + c).astype(np.float32)
+        ni = np.where(np.isfinite(n), n, 0).astype(np.int32)
+        y = np.ldexp(p, ni).astype(np.float32)
+    y = np.where(x > np.float32(88.0), np.float32(np.inf), y)
+    y = np.where(x < np.float32(-87.0), np.float32(0.0), y)
+    return y.astype(np.float32)
+
+
+def sigmoid_f32(x) -> np.ndarray:
+    """`1 / (1 + exp(-x))` with exp_f32 (tl.sigmoid, kernels/norm.py:178)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore", divide="ignore"):
+        return (np.float32(1.0) / (np.float32(1.0) + exp_f32(-x))).astype(np.float32)
+
+
+def silu_f32(x) -> np.ndarray:
+    """`x * sigmoid(x)` with exp_f32 (kernels/common.py:32-34, used by
+    kernels/norm.py:114)."""
+    x = np.asarray(x, dtype=np.float32)
+    return (x * sigmoid_f32(x)).astype(np.float32)
+
+
+def sumsq_lanes(x, lanes: int) -> np.ndarray:
+    """Sum of squares of each row of x [M, L] in the kernels' fixed order: 8-element
+    chunks; lane l of `lanes` folds chunks l, l + lanes, ... (each chunk's elements
+    in order, `acc = acc + v * v`, both operations rounded); then an xor butterfly
+    over the lanes (`acc = acc + acc[l ^ m]` for m = lanes/2, ..., 1).  The reference
+    writes `tl.sum(x * x, axis=0)` (kernels/norm.py:39, 113) and leaves the order to
+    Triton."""
+    x = np.asarray(x, dtype=np.float32)
+    M, L = x.shape
+    assert L % 8 == 0 and lanes & (lanes - 1) == 0
+    x2 = (x * x).astype(np.float32)
+    nc = L // 8
+    P = -(-nc // lanes)
+    pad = np.zeros((M, P * lanes * 8), dtype=np.float32)  # + 0.0 leaves a sum of squares unchanged
+    pad[:, :L] = x2
+    X = pad.reshape(M, P, lanes, 8)
+    acc = np.zeros((M, lanes), dtype=np.float32)
+    for i in range(P):
+        for e in range(8):
+            acc = (acc + X[:, i, :, e]).astype(np.float32)
+    idx = np.arange(lanes)
+    m = lanes // 2
+    while m >= 1:
+        acc = (acc + acc[:, idx ^ m]).astype(np.float32)
+        m //= 2
+    return acc[:, 0]
+
+
+def rms_inv(ss, n: int, eps: float) -> np.ndarray:
+    """`rsqrt(ss / n + eps)` as `1 / sqrt(.)`, each operation correctly rounded in
+    fp32 (kernels/norm.py:39-40, 113-114 use tl.rsqrt)."""
+    ss = np.asarray(ss, dtype=np.float32)
+    var = (ss / np.float32(n)).astype(np.float32)
+    return (np.float32(1.0) / np.sqrt((var + np.float32(eps)).astype(np.float32))).astype(np.float32)
+
+
+def rmsnorm_quant_ref(x, w, eps: float = 1e-6, one_plus: bool = True):
+    """RMSNorm of each row, then per-64 int8 quant (kernels/norm.py:28-57):
+    `y = x * rsqrt(mean(x^2) + eps) * (w + 1 if one_plus else w)`, left to right,
+    then `_quant_groups` (norm.py:15-25).  The sum of squares is one 64-lane
+    sumsq_lanes.  x: [M, K] values of the 16-bit input; w: [K].
+    Returns (q int8 [M, K], s fp32 [M, K // 64])."""
+    x = np.asarray(x, dtype=np.float32)
+    w = np.asarray(w, dtype=np.float32)
+    if one_plus:
+        w = (w + np.float32(1.0)).astype(np.float32)
+    r = rms_inv(sumsq_lanes(x, 64), x.shape[1], eps)
+    y = ((x * r[:, None]).astype(np.float32) * w[None, :]).astype(np.float32)
+    return quant_groups(y)
+
+
+def gate_cols(N: int, hd: int) -> np.ndarray:
+    """Column of the gate of activation column k in G [M, heads, 2 hd], the gate
+    in the second half of each head (kernels/norm.py:171, 176)."""
+    k = np.arange(N)
+    return (k // hd) * (2 * hd) + hd + (k % hd)
+
+
+def gate_mul_quant_ref(a, g, hd: int = 256):
+    """`y = a * sigmoid(G[gate column])`, then per-64 int8 quant
+    (kernels/norm.py:168-188).  a: [M, N]; g: [M, >= 2 N] gate rows."""
+    a = np.asarray(a, dtype=np.float32)
+    g = np.asarray(g, dtype=np.float32)
+    gv = g[:, gate_cols(a.shape[1], hd)]
+    y = (a * sigmoid_f32(gv)).astype(np.float32)
+    return quant_groups(y)
+
+
+def norm_gated_quant_ref(v, z, w, eps: float = 1e-6):
+    """Per (row, head) gated RMSNorm, bf16 round trip, per-64 int8 quant
+    (kernels/norm.py:95-137): `y = x * rsqrt(mean_head(x^2) + eps) * w * silu(z)`,
+    left to right; hd = len(w).  The head's sum of squares is one sumsq_lanes over
+    hd / 8 lanes (one 8-element chunk each).  v, z: [T, N] (z already the gate
+    columns); w: [hd].  Returns (q int8 [T, N], s fp32 [T, N // 64])."""
+    v = np.asarray(v, dtype=np.float32)
+    z = np.asarray(z, dtype=np.float32)
+    w = np.asarray(w, dtype=np.float32)
+    T, N = v.shape
+    hd = w.shape[0]
+    heads = v.reshape(T * (N // hd), hd)
+    r = rms_inv(sumsq_lanes(heads, hd // 8), hd, eps).reshape(T, N // hd)
+    rr = np.repeat(r, hd, axis=1)
+    ww = np.tile(w, N // hd)
+    y = ((v * rr).astype(np.float32) * ww[None, :]).astype(np.float32)
+    y = (y * silu_f32(z)).astype(np.float32)
+    return quant_groups(round_bf16(y))
+
+
+# ----------------------------------------------------------------------------
 # Load-time producers of the packed layouts (read-only contract)
 # ----------------------------------------------------------------------------
 

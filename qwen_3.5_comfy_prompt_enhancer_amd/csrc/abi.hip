@@ -159,7 +159,53 @@ SkArgs row_block(const SkArgs& a, int m0, int rows) {
   if (a.res) b.res = (const uint16_t*)a.res + (long long)m0 * a.ldr;
   if (a.oq) b.oq = a.oq + (long long)m0 * a.ncols;
   if (a.os) b.os = a.os + (long long)m0 * (a.ncols / 64);
+  if (a.pro.kind != PRO_NONE) {
+    ProArgs& p = b.pro;
+    p.x = (const uint16_t*)a.pro.x + (long long)m0 * a.pro.ldx;
+    if (a.pro.g) p.g = (const uint16_t*)a.pro.g + (long long)m0 * a.pro.ldg;
+    if (a.pro.q) p.q = a.pro.q + (long long)m0 * a.K, p.s = a.pro.s + (long long)m0 * (a.K / 64);
+    p.tq = a.pro.tq + (long long)m0 * a.K;
+    p.ts = a.pro.ts + (long long)m0 * (a.K / 64);
+  }
   return b;
+}
+
+// Activation producer of a call (a.pro): run it as a launch of its own, writing the
+// codes and scales to a.pro.tq / a.pro.ts, which the call then reads as its
+// activations.
+int pro_materialize(const char* fn, SkArgs& a, hipStream_t stream) {
+  ProArgs p = a.pro;
+  p.q = p.tq;
+  p.s = p.ts;
+  QL_TRY(hip_status(fn, launch_producer(p, a.M, a.K, stream)));
+  a.x = p.tq;
+  a.xs = p.ts;
+  a.pro.kind = PRO_NONE;
+  return QLIN_OK;
+}
+
+// Fused prologue for a skinny launch plan: places the code block of the workgroup's
+// rows and K range after the finish layout in dynamic LDS.  False when the plan has
+// no fused instantiation or the block does not fit (the caller then materializes).
+bool pro_plan(SkLaunch& L, SkArgs& a, int K, int rows) {
+  L.pro = 1;
+  if (!skinny_pro_ok(L, a.group)) {
+    L.pro = 0;
+    return false;
+  }
+  const int kr = (a.lanes == 2) ? a.kchunk : std::min(K, L.waves * a.kchunk);
+  const int mt = std::min(16, rows);
+  const size_t off = (L.lds + 15) & ~(size_t)15;
+  const int ldq = kr + 16;  // 16 bytes of padding staggers the rows over the LDS banks
+  const size_t bytes = (size_t)mt * ldq + (size_t)mt * (kr / 64) * sizeof(float) + (size_t)mt * sizeof(float);
+  if (bytes > kProLdsBytes) {
+    L.pro = 0;
+    return false;
+  }
+  a.pro.lds_off = (int)off;
+  a.pro.ldq = ldq;
+  L.lds = off + bytes;
+  return true;
 }
 
 int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
@@ -196,6 +242,8 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
                           (S > 1 ? 1.45e-6 * S : 0.0);
     tiled = force_tiled || t_tiled < t_rows;
   }
+  // the tiled kernel has no producer prologue: make the activations first
+  if (tiled && a.pro.kind != PRO_NONE) QL_TRY(pro_materialize(fn, a, stream));
   const int TN = tiled ? 128 : (S == 1 ? 64 : 128);
   long long ntiles = 0;
   for (int s = 0; s < (P.epi == EPI_STORE ? a.nseg : 1); ++s) ntiles += (a.seg[s].n + TN - 1) / TN;
@@ -235,6 +283,7 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
       L.epi = P.epi;
       L.cols = TN / 16;
       L.waves = 2;
+      L.pro = 0;
       int acc = 0;
       for (int s = 0; s < b.nseg; ++s) {
         b.seg[s].tile0 = (P.epi == EPI_STORE) ? acc : 0;
@@ -249,6 +298,7 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
       L.grid = dim3((unsigned)(ntiles * S), (unsigned)rtiles, 1);
       const int rg0 = ((rows < 16 ? rows : 16) + 3) / 4;
       L.lds = ((size_t)L.waves * P.nsets * rg0 * 4 * (TN + 4) + (size_t)P.nsets * TN) * sizeof(float);
+      if (b.pro.kind != PRO_NONE && !pro_plan(L, b, P.K, rows)) QL_TRY(pro_materialize(fn, b, stream));
       err = launch_skinny(L, b, stream);
     }
     if (err != hipSuccess) return hip_status(fn, err);
@@ -270,6 +320,7 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   L.wk = P.wk;
   L.hz = P.hz ? 1 : 0;
   L.epi = P.epi;
+  L.pro = 0;
 
   auto count_tiles = [&](int tn) {
     int nt = 0;
@@ -371,6 +422,9 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   L.lds = ((size_t)waves * P.nsets * rg0 * 4 * (TN + 4) + (size_t)P.nsets * TN) * sizeof(float);
   if ((long long)ntiles * splits > 0x7FFFFFFFLL || rtiles > 65535)
     return fail(QLIN_ERR_UNSUPPORTED, "%s: grid too large (M=%d, N=%d)", fn, P.M, P.ncols);
+  // activation producer: fused into the prologue of narrow plans; wide plans (every
+  // workgroup would redo the whole row) make the activations with a launch of their own
+  if (a.pro.kind != PRO_NONE && (wide || !pro_plan(L, a, P.K, P.M))) QL_TRY(pro_materialize(fn, a, stream));
   if (clear && splits > 1) QL_TRY(hip_status(fn, clear_counters(workspace, (long long)rtiles * ntiles, stream)));
   return hip_status(fn, launch_skinny(L, a, stream));
 }
@@ -395,6 +449,61 @@ int check_engine_act(const char* fn, const int8_t* a_q, const float* a_s, int M,
   if (K % 64 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 64", fn, K);
   if (!aligned(a_q, 8) || !aligned(a_s, 4))
     return fail(QLIN_ERR_UNSUPPORTED, "%s: activations must be 8-byte aligned", fn);
+  return QLIN_OK;
+}
+
+// Validates an activation producer (kernels/norm.py:28-57, 95-137, 168-188) for M rows
+// of K columns and completes it: norm_gated reads v contiguous (row stride K), and the
+// codes go to q / s or, without them, to the end of the workspace, which is taken off
+// *wsb so no split-K partial reaches it.
+int setup_pro(const char* fn, ProArgs& p, int M, int K, void* ws, size_t* wsb) {
+  if (p.kind != PRO_RMSNORM && p.kind != PRO_GATE_MUL && p.kind != PRO_NORM_GATED)
+    return fail(QLIN_ERR_INVALID, "%s: unknown producer kind %d", fn, p.kind);
+  if (K % 64 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 64", fn, K);
+  if (p.xdt != QLIN_BF16 && p.xdt != QLIN_F16)
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: activation dtype %d (need bf16 or fp16)", fn, p.xdt);
+  if (!p.x) return fail(QLIN_ERR_INVALID, "%s: null producer input", fn);
+  if (p.kind == PRO_NORM_GATED) p.ldx = K;
+  if (p.ldx < K || p.ldx % 8 != 0 || !aligned(p.x, 16))
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: producer input must be 16-byte aligned with a row stride >= K and a "
+                "multiple of 8", fn);
+  if (p.kind != PRO_GATE_MUL) {
+    if (!p.w) return fail(QLIN_ERR_INVALID, "%s: null norm weight", fn);
+    if (!dtype_scale_ok(p.wdt)) return fail(QLIN_ERR_UNSUPPORTED, "%s: norm weight dtype %d", fn, p.wdt);
+    if (!aligned(p.w, 16)) return fail(QLIN_ERR_UNSUPPORTED, "%s: norm weight must be 16-byte aligned", fn);
+  }
+  if (p.kind != PRO_RMSNORM) {
+    if (!p.g) return fail(QLIN_ERR_INVALID, "%s: null gate input", fn);
+    if (p.ldg % 8 != 0 || !aligned(p.g, 16))
+      return fail(QLIN_ERR_UNSUPPORTED, "%s: gate input must be 16-byte aligned with a row stride multiple of 8", fn);
+  }
+  if (p.kind == PRO_GATE_MUL) {
+    if (p.hd <= 0 || p.hd % 8 != 0 || K % p.hd != 0)
+      return fail(QLIN_ERR_UNSUPPORTED, "%s: head size %d must be a multiple of 8 dividing K=%d", fn, p.hd, K);
+    if (p.ldg < 2LL * K) return fail(QLIN_ERR_INVALID, "%s: gate row stride %lld < 2 K", fn, (long long)p.ldg);
+  }
+  if (p.kind == PRO_NORM_GATED) {
+    if ((p.hd != 128 && p.hd != 256 && p.hd != 512) || K % p.hd != 0)
+      return fail(QLIN_ERR_UNSUPPORTED, "%s: head size %d (need 128, 256 or 512, dividing K=%d)", fn, p.hd, K);
+    if (p.ldg < K) return fail(QLIN_ERR_INVALID, "%s: z row stride %lld < K", fn, (long long)p.ldg);
+  }
+  if ((p.q == nullptr) != (p.s == nullptr)) return fail(QLIN_ERR_INVALID, "%s: give both q and s, or neither", fn);
+  if (p.q && (!aligned(p.q, 8) || !aligned(p.s, 4)))
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: q must be 8-byte aligned", fn);
+  if (p.q) {
+    p.tq = p.q;
+    p.ts = p.s;
+  } else {
+    const size_t qb = ((size_t)M * K + 255) & ~(size_t)255;
+    const size_t sb = ((size_t)M * (K / 64) * sizeof(float) + 255) & ~(size_t)255;
+    if (!ws || *wsb < kCounterBytes + qb + sb)
+      return fail(QLIN_ERR_WORKSPACE, "%s: no room in the workspace for the activation codes", fn);
+    *wsb -= qb + sb;
+    p.tq = (int8_t*)ws + *wsb;
+    p.ts = (float*)((char*)ws + *wsb + qb);
+  }
+  p.lds_off = 0;
+  p.ldq = 0;
   return QLIN_OK;
 }
 
@@ -434,10 +543,17 @@ SkArgs base_args() {
 // Common body of gemm_i8 / gemm_w4.
 int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int M, int K, const void* b,
                 const void* b_s, int bs_dtype, const uint8_t* b_z, int group, int N, void* out, int64_t ldo,
-                const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream, bool clear = false) {
+                const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream, bool clear = false,
+                const ProArgs* pro = nullptr) {
   QL_TRY(check_common(fn, M, K, N));
   if (M == 0 || N == 0) return QLIN_OK;
-  QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  ProArgs pa{};
+  if (pro) {
+    pa = *pro;
+    QL_TRY(setup_pro(fn, pa, M, K, ws, &wsb));
+  } else {
+    QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  }
   if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
   if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
   QL_TRY(check_weight(fn, b, b_s, b_z, N, wk));
@@ -458,6 +574,7 @@ int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int
   a.odt = QLIN_BF16;
   a.res = residual;
   a.ldr = ldr;
+  a.pro = pa;
   Problem P{ACT_I8, wk, EPI_STORE, b_z != nullptr, M, K, a.group, 1, N};
   if (clear && (!ws || wsb <= kCounterBytes)) return fail(QLIN_ERR_WORKSPACE, "%s: no scratch", fn);
   return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream, clear);
@@ -466,12 +583,18 @@ int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int
 int engine_proj3(const char* fn, int wk, const int8_t* a_q, const float* a_s, int M, int K, const void* w1,
                  const void* s1, const uint8_t* z1, int n1, const void* w2, const void* s2, const uint8_t* z2,
                  int n2, const void* w3, const void* s3, const uint8_t* z3, int n3, int bs_dtype, int group,
-                 void* out, int64_t ldo, void* ws, size_t wsb, void* stream) {
+                 void* out, int64_t ldo, void* ws, size_t wsb, void* stream, const ProArgs* pro = nullptr) {
   const int NT = n1 + n2 + n3;
   QL_TRY(check_common(fn, M, K, NT));
   if (n1 < 0 || n2 < 0 || n3 < 0) return fail(QLIN_ERR_INVALID, "%s: negative N", fn);
   if (M == 0 || NT == 0) return QLIN_OK;
-  QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  ProArgs pa{};
+  if (pro) {
+    pa = *pro;
+    QL_TRY(setup_pro(fn, pa, M, K, ws, &wsb));
+  } else {
+    QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  }
   if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
   if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
   QL_TRY(check_weight(fn, w1, s1, z1, n1, wk));
@@ -503,6 +626,7 @@ int engine_proj3(const char* fn, int wk, const int8_t* a_q, const float* a_s, in
   a.out = out;
   a.ldo = ldo;
   a.odt = QLIN_BF16;
+  a.pro = pa;
   Problem P{ACT_I8, wk, EPI_STORE, hz, M, K, a.group, 1, NT};
   return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
 }
@@ -510,10 +634,16 @@ int engine_proj3(const char* fn, int wk, const int8_t* a_q, const float* a_s, in
 int engine_gate_up(const char* fn, int wk, int epi, const int8_t* a_q, const float* a_s, int M, int K,
                    const void* wg, const void* sg, const uint8_t* zg, const void* wu, const void* su,
                    const uint8_t* zu, int bs_dtype, int group, int N, void* out, int8_t* out_q, float* out_s,
-                   void* ws, size_t wsb, void* stream) {
+                   void* ws, size_t wsb, void* stream, const ProArgs* pro = nullptr) {
   QL_TRY(check_common(fn, M, K, N));
   if (M == 0 || N == 0) return QLIN_OK;
-  QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  ProArgs pa{};
+  if (pro) {
+    pa = *pro;
+    QL_TRY(setup_pro(fn, pa, M, K, ws, &wsb));
+  } else {
+    QL_TRY(check_engine_act(fn, a_q, a_s, M, K));
+  }
   if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
   if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
   QL_TRY(check_weight(fn, wg, sg, zg, N, wk));
@@ -544,6 +674,7 @@ int engine_gate_up(const char* fn, int wk, int epi, const int8_t* a_q, const flo
   a.odt = QLIN_BF16;
   a.oq = out_q;
   a.os = out_s;
+  a.pro = pa;
   Problem P{ACT_I8, wk, epi, zg != nullptr, M, K, a.group, 2, N};
   return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream);
 }
@@ -845,6 +976,158 @@ int qlin_linear_w4(const void* x, int x_dtype, int M, int K, int64_t ldx, const 
   g_err[0] = 0;
   return a16_linear("qlin_linear_w4", WK_W4, x, x_dtype, M, K, ldx, w, scale, s_dtype, zero, group, N, out,
                     out_dtype, ldo, residual, ldr, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Activation producers (kernels/norm.py) and the linears that make their own
+// activations from them
+// ---------------------------------------------------------------------------
+
+static ProArgs pro_from(const qlin_producer* p) {
+  ProArgs a{};
+  a.kind = p->kind;
+  a.x = p->x;
+  a.ldx = p->ldx;
+  a.xdt = p->x_dtype;
+  a.g = p->g;
+  a.ldg = p->ldg;
+  a.w = p->w;
+  a.wdt = p->w_dtype;
+  a.hd = p->hd;
+  a.one_plus = p->one_plus;
+  a.eps = p->eps;
+  a.q = p->q;
+  a.s = p->s;
+  return a;
+}
+
+static int produce(const char* fn, ProArgs p, int M, int K, void* stream) {
+  if (M < 0 || K < 0) return fail(QLIN_ERR_INVALID, "%s: bad sizes M=%d K=%d", fn, M, K);
+  if (M == 0 || K == 0) return QLIN_OK;
+  if (!p.q || !p.s) return fail(QLIN_ERR_INVALID, "%s: null q or s", fn);
+  size_t none = 0;
+  QL_TRY(setup_pro(fn, p, M, K, nullptr, &none));
+  return hip_status(fn, launch_producer(p, M, K, (hipStream_t)stream));
+}
+
+int qlin_rmsnorm_quant(const void* x, int64_t ldx, int x_dtype, const void* w, int w_dtype, int M, int K, float eps,
+                       int one_plus, int8_t* q, float* s, void* stream) {
+  g_err[0] = 0;
+  ProArgs p{};
+  p.kind = PRO_RMSNORM;
+  p.x = x;
+  p.ldx = ldx;
+  p.xdt = x_dtype;
+  p.w = w;
+  p.wdt = w_dtype;
+  p.one_plus = one_plus ? 1 : 0;
+  p.eps = eps;
+  p.q = q;
+  p.s = s;
+  return produce("qlin_rmsnorm_quant", p, M, K, stream);
+}
+
+int qlin_gate_mul_quant(const void* a, int64_t lda, const void* g, int64_t ldg, int dtype, int M, int N, int hd,
+                        int8_t* q, float* s, void* stream) {
+  g_err[0] = 0;
+  ProArgs p{};
+  p.kind = PRO_GATE_MUL;
+  p.x = a;
+  p.ldx = lda;
+  p.xdt = dtype;
+  p.g = g;
+  p.ldg = ldg;
+  p.hd = hd;
+  p.q = q;
+  p.s = s;
+  return produce("qlin_gate_mul_quant", p, M, N, stream);
+}
+
+int qlin_norm_gated_quant(const void* v, const void* z, int64_t ldz, int dtype, const void* w, int w_dtype, int T,
+                          int N, int hd, float eps, int8_t* q, float* s, void* stream) {
+  g_err[0] = 0;
+  ProArgs p{};
+  p.kind = PRO_NORM_GATED;
+  p.x = v;
+  p.ldx = N;
+  p.xdt = dtype;
+  p.g = z;
+  p.ldg = ldz;
+  p.w = w;
+  p.wdt = w_dtype;
+  p.hd = hd;
+  p.eps = eps;
+  p.q = q;
+  p.s = s;
+  return produce("qlin_norm_gated_quant", p, T, N, stream);
+}
+
+int qlin_pro_exp_f32(const float* x, float* y, int n, void* stream) {
+  g_err[0] = 0;
+  if (n < 0) return fail(QLIN_ERR_INVALID, "qlin_pro_exp_f32: n=%d", n);
+  if (n > 0 && (!x || !y)) return fail(QLIN_ERR_INVALID, "qlin_pro_exp_f32: null pointer");
+  return hip_status("qlin_pro_exp_f32", launch_pro_exp(x, y, n, (hipStream_t)stream));
+}
+
+#define QL_PRO_ARG(fn)                                                      \
+  if (!pro) return fail(QLIN_ERR_INVALID, "%s: null producer", fn);        \
+  const ProArgs pa = pro_from(pro);
+
+int qlin_pro_gemm_i8(const qlin_producer* pro, int M, int K, const int8_t* b, const void* b_s, int bs_dtype, int N,
+                     void* out, int64_t ldo, const void* residual, int64_t ldr, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  QL_PRO_ARG("qlin_pro_gemm_i8")
+  return engine_gemm("qlin_pro_gemm_i8", WK_W8, nullptr, nullptr, M, K, b, b_s, bs_dtype, nullptr, 64, N, out, ldo,
+                     residual, ldr, workspace, workspace_bytes, stream, false, &pa);
+}
+
+int qlin_pro_gemm_w4(const qlin_producer* pro, int M, int K, const uint8_t* b, const void* b_s, int bs_dtype,
+                     const uint8_t* b_z, int group, int N, void* out, int64_t ldo, const void* residual, int64_t ldr,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  QL_PRO_ARG("qlin_pro_gemm_w4")
+  return engine_gemm("qlin_pro_gemm_w4", WK_W4, nullptr, nullptr, M, K, b, b_s, bs_dtype, b_z, group, N, out, ldo,
+                     residual, ldr, workspace, workspace_bytes, stream, false, &pa);
+}
+
+int qlin_pro_proj3_i8(const qlin_producer* pro, int M, int K, const int8_t* w1, const void* s1, int n1,
+                      const int8_t* w2, const void* s2, int n2, const int8_t* w3, const void* s3, int n3, int bs_dtype,
+                      void* out, int64_t ldo, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  QL_PRO_ARG("qlin_pro_proj3_i8")
+  return engine_proj3("qlin_pro_proj3_i8", WK_W8, nullptr, nullptr, M, K, w1, s1, nullptr, n1, w2, s2, nullptr, n2,
+                      w3, s3, nullptr, n3, bs_dtype, 64, out, ldo, workspace, workspace_bytes, stream, &pa);
+}
+
+int qlin_pro_proj3_w4(const qlin_producer* pro, int M, int K, const uint8_t* w1, const void* s1, const uint8_t* z1,
+                      int n1, const uint8_t* w2, const void* s2, const uint8_t* z2, int n2, const uint8_t* w3,
+                      const void* s3, const uint8_t* z3, int n3, int bs_dtype, int group, void* out, int64_t ldo,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  QL_PRO_ARG("qlin_pro_proj3_w4")
+  return engine_proj3("qlin_pro_proj3_w4", WK_W4, nullptr, nullptr, M, K, w1, s1, z1, n1, w2, s2, z2, n2, w3, s3, z3,
+                      n3, bs_dtype, group, out, ldo, workspace, workspace_bytes, stream, &pa);
+}
+
+int qlin_pro_mlp_gate_up_quant_i8(const qlin_producer* pro, int M, int K, const int8_t* wg, const void* sg,
+                                  const int8_t* wu, const void* su, int bs_dtype, int N, int8_t* out_q, float* out_s,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  QL_PRO_ARG("qlin_pro_mlp_gate_up_quant_i8")
+  return engine_gate_up("qlin_pro_mlp_gate_up_quant_i8", WK_W8, EPI_GATEUP_Q, nullptr, nullptr, M, K, wg, sg, nullptr,
+                        wu, su, nullptr, bs_dtype, 64, N, nullptr, out_q, out_s, workspace, workspace_bytes, stream,
+                        &pa);
+}
+
+int qlin_pro_mlp_gate_up_quant_w4(const qlin_producer* pro, int M, int K, const uint8_t* wg, const void* sg,
+                                  const uint8_t* zg, const uint8_t* wu, const void* su, const uint8_t* zu,
+                                  int bs_dtype, int group, int N, int8_t* out_q, float* out_s, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  QL_PRO_ARG("qlin_pro_mlp_gate_up_quant_w4")
+  return engine_gate_up("qlin_pro_mlp_gate_up_quant_w4", WK_W4, EPI_GATEUP_Q, nullptr, nullptr, M, K, wg, sg, zg, wu,
+                        su, zu, bs_dtype, group, N, nullptr, out_q, out_s, workspace, workspace_bytes, stream, &pa);
 }
 
 int qlin_w4_unpack(const uint8_t* packed, int K, int N, uint8_t* nib, void* stream) {

@@ -16,6 +16,36 @@ struct Seg {
   int tile0;         // first column tile that belongs to it
 };
 
+// Activation producer (kernels/norm.py) of an engine-signature call: the int8 codes
+// and per-64 scales are made from 16-bit activations, by a launch of their own or in
+// the prologue of the linear's launch (producers.h).
+enum ProKind { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_GATE_MUL = 2, PRO_NORM_GATED = 3 };
+
+struct ProArgs {
+  int kind;            // ProKind
+  const void* x;       // rmsnorm: rows [M][ldx]; gate_mul: a [M][ldx]; norm_gated: v [M][K]
+  long long ldx;
+  int xdt;             // DT_BF16 or DT_F16 (x and g)
+  const void* g;       // gate_mul: gate rows [M][ldg] (head h: 2 hd values, gates in the
+                       // second half); norm_gated: z [M][ldg]
+  long long ldg;
+  const void* w;       // norm weight: rmsnorm [K], norm_gated [hd]
+  int wdt;             // DT_BF16, DT_F16 or DT_F32
+  int hd;              // head size (gate_mul, norm_gated)
+  int one_plus;        // rmsnorm: scale by w + 1
+  float eps;
+  int8_t* q;           // codes [M][K] (written by the standalone producer; optional copy
+  float* s;            // in a fused launch) and scales [M][K/64]
+  int8_t* tq;          // where a call that cannot fuse the producer puts the codes and
+  float* ts;           // scales first: q / s, or the end of the workspace
+  int lds_off;         // fused launch: byte offset of the code block in dynamic LDS
+  int ldq;             // fused launch: row stride of the LDS code block (bytes)
+};
+
+// Dynamic LDS a fused-prologue launch may add for its code block (plans that need
+// more make their activations with a launch of their own).
+constexpr size_t kProLdsBytes = 64 * 1024;
+
 // Arguments of the skinny (row-tile of <= 16 rows) MFMA kernel.
 struct SkArgs {
   const void* x;       // ACT_F16: fp16 [M][ldx]; ACT_I8: int8 [M][K]
@@ -43,12 +73,14 @@ struct SkArgs {
                        // [(s*waves + w)*kchunk, +kchunk); 2 = the two waves of split s fold
                        // the alternate 64-wide blocks of [s*kchunk, (s+1)*kchunk) (wave w:
                        // block offsets w, w+2, ...), the K order of the tiled int8 kernel
+  ProArgs pro;         // fused prologue (launches with SkLaunch::pro set); x / xs unused
 };
 
 struct SkLaunch {
   int act, wk, hz, epi, cols;
   int ks;          // K-loop fold structure (KStruct in skinny_kernel.h), set by launch_skinny
   int waves;       // waves per workgroup
+  int pro;         // 1: the launch makes its activations in a prologue (SkArgs::pro)
   dim3 grid;
   size_t lds;      // dynamic LDS bytes
 };
@@ -110,6 +142,14 @@ int gemm_i8_scratch(const char* fn, const int8_t* a_q, const float* a_s, int M, 
                     const void* b_s, int bs_dtype, int N, void* out, int64_t ldo, const void* residual,
                     int64_t ldr, void* scratch, size_t scratch_bytes, void* stream);
 size_t counter_bytes();
+
+// Standalone producer launch: codes and scales of all M rows into p.q / p.s.
+hipError_t launch_producer(const ProArgs& p, int M, int K, hipStream_t st);
+// Evaluates the producers' exp on n values (a test entry point).
+hipError_t launch_pro_exp(const float* x, float* y, int n, hipStream_t st);
+// whether a skinny launch plan (act, wk, hz, epi, cols, waves) has a fused-prologue
+// instantiation (skinny_pro_w8.hip, skinny_pro_w4.hip) for weight group `group`
+bool skinny_pro_ok(const SkLaunch& L, int group);
 
 hipError_t launch_w4_unpack(const uint8_t* p, int K, int N, uint8_t* out, hipStream_t st);
 hipError_t launch_w4_dequant(const uint8_t* p, const void* s, int sdt, const uint8_t* z,

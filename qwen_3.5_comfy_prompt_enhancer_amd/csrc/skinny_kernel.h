@@ -33,8 +33,10 @@
 //   * Every load of a 32-wide K step is issued D steps ahead from a register ring.
 #pragma once
 
+#include <algorithm>
 #include <type_traits>
 
+#include "producers.h"
 #include "qlin_dev.h"
 #include "qlin_internal.h"
 
@@ -218,9 +220,13 @@ struct SkOcc {
   static constexpr int value = (ACT == ACT_I8 && COLS == 8 && !(WK == WK_W4 && EPI != EPI_STORE)) ? 2 : 1;
 };
 
-template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW, int KS>
+// PRO: the launch makes its int8 activations itself (producers.h): a prologue writes the
+// codes and scales of the workgroup's rows and K range into LDS, after the first weight
+// loads are in flight, and the K loop reads them from there.
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW, int KS, bool PRO = false>
 __global__ __launch_bounds__(64 * MAXW)
 __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skinny_kernel(const SkArgs a) {
+  static_assert(!PRO || ACT == ACT_I8, "the prologue makes int8 activations");
   constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;  // weight sets feeding one output tile
   constexpr int TN = 16 * COLS;
   constexpr int NQ = COLS / 4;
@@ -279,6 +285,9 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   const int kb = inter ? split * a.kchunk + 64 * wave : (split * nw + wave) * a.kchunk;
   const int ke = min(K, kb + a.kchunk);
   const int kst = inter ? 128 : 64;  // K distance between this wave's consecutive 64-wide blocks
+  // K range of the workgroup (its waves' ranges together)
+  const int kwb = inter ? split * a.kchunk : split * nw * a.kchunk;
+  const int kwe = min(K, kwb + (inter ? a.kchunk : nw * a.kchunk));
 
   f32x4 acc[NS][COLS];
 #pragma unroll
@@ -343,7 +352,7 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   auto load_step = [&](Step& st, int k) {
     if constexpr (F16) {
       st.xv = *(const u32x4*)(xpf + k);
-    } else {
+    } else if constexpr (!PRO) {
       st.xv = *(const u32x2*)(xpi + k);
 #pragma unroll
       for (int r = 0; r < 4; ++r) st.as_[r] = a.xs[asrow[r] + k / 64];
@@ -385,8 +394,24 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   // faster for them: their waves are longer and hold more registers).
   constexpr int U = 4;
   constexpr bool kExactLoads = F16 && !W4;
+  // PRO: the workgroup's codes, [Mt][ldq] bytes over [kwb, kwe), then scales [Mt][lng]
+  uint8_t* const plq = (uint8_t*)red + a.pro.lds_off;
+  const int plng = (kwe - kwb) >> 6;
+  float* const pls = (float*)(plq + (long long)Mt * a.pro.ldq);
+  float* const plr = pls + Mt * plng;
+  auto prologue = [&]() {
+    if constexpr (PRO) {
+      ProOut o;
+      o.lq = plq;
+      o.ls = pls;
+      o.ldq = a.pro.ldq;
+      o.lng = plng;
+      o.emit = a.pro.q != nullptr && tile == 0;
+      pro_block(a.pro, K, rt * 16, Mt, kwb, kwe, o, plr);
+    }
+  };
   auto run_pipeline = [&](auto&& compute) {
-    if (nsteps <= 0) return;
+    if (!PRO && nsteps <= 0) return;
     if constexpr (kExactLoads) {
       // steps [base0, nsteps): fewer than U + D, in at most two static chunks of U
       auto tail = [&](int base0) {
@@ -423,8 +448,14 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       tail(base0);
     } else {
       // every load issued unconditionally, the step index clamped to the last step
+      if (nsteps > 0) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) load_step(buf[d], kof(d < nsteps ? d : nsteps - 1));
+        for (int d = 0; d < D; ++d) load_step(buf[d], kof(d < nsteps ? d : nsteps - 1));
+      }
+      if constexpr (PRO) {
+        prologue();  // every wave, with its first loads in flight
+        if (nsteps <= 0) return;
+      }
       const int nfull = nsteps - nsteps % U;
       for (int base = 0; base < nfull; base += U) {
         static_for<0, U>([&](auto uc) {
@@ -535,13 +566,29 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int t = 0; t < COLS; ++t) iacc[s][t] = i32x4{0, 0, 0, 0};
+    // PRO: rows of this lane's A operand and of its activation scales within the row
+    // tile (rows past Mt read the last real row; their results are never stored)
+    const int parow = min(j, Mt - 1);
+    int psrow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) psrow[r] = min(4 * g + r, Mt - 1);
     run_pipeline([&](const Step& st, int k, auto uc) {
       constexpr int u = decltype(uc)::value;
-      uint64_t ap = (uint64_t)st.xv.x | ((uint64_t)st.xv.y << 32);
+      u32x2 xv;
+      float as_[4];
+      if constexpr (PRO) {
+        xv = *(const u32x2*)(plq + (long long)parow * a.pro.ldq + (k - kwb) + 8 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) as_[r] = pls[psrow[r] * plng + ((k - kwb) >> 6)];
+      } else {
+        xv = st.xv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) as_[r] = st.as_[r];
+      }
+      uint64_t ap = (uint64_t)xv.x | ((uint64_t)xv.y << 32);
       if constexpr (W4) {
         // k slots: even K values first, then odd (the nibble split order below)
-        ap = (uint64_t)perm(st.xv.y, st.xv.x, 0x06040200u) |
-             ((uint64_t)perm(st.xv.y, st.xv.x, 0x07050301u) << 32);
+        ap = (uint64_t)perm(xv.y, xv.x, 0x06040200u) | ((uint64_t)perm(xv.y, xv.x, 0x07050301u) << 32);
       }
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -575,7 +622,7 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
             for (int t = 0; t < COLS; ++t) {
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                acc[s][t][r] = fmaf((float)iacc[s][t][r], st.as_[r], acc[s][t][r]);
+                acc[s][t][r] = fmaf((float)iacc[s][t][r], as_[r], acc[s][t][r]);
               iacc[s][t] = i32x4{0, 0, 0, 0};
             }
         } else {
@@ -589,7 +636,7 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
               for (int r = 0; r < 4; ++r) {
                 int v = iacc[s][t][r] >> 4;  // exact: the MFMA summed 16 * (nibble - 8)
                 if constexpr (HZ) v += (8 - (int)byte_of(st.z[s].d[t >> 2], t & 3)) * sx[r];
-                acc[s][t][r] = fmaf((float)v, st.as_[r] * ws[t], acc[s][t][r]);
+                acc[s][t][r] = fmaf((float)v, as_[r] * ws[t], acc[s][t][r]);
               }
               iacc[s][t] = i32x4{0, 0, 0, 0};
             }
@@ -774,14 +821,15 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   }
 }
 
-template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW, int KS>
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool SPLIT, int MAXW, int KS, bool PRO = false>
 hipError_t launch_v(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
-  auto* k = skinny_kernel<ACT, WK, HZ, EPI, COLS, SPLIT, MAXW, KS>;
+  auto* k = skinny_kernel<ACT, WK, HZ, EPI, COLS, SPLIT, MAXW, KS, PRO>;
   // Largest dynamic LDS of this variant (MAXW finish slots of 16 rows, the column
-  // scales); the kernel's static LDS comes on top, so the limit is raised to exactly
-  // this, not to the whole 160 KB.
+  // scales, the prologue's code block); the kernel's static LDS comes on top, so the
+  // limit is raised to exactly this, not to the whole 160 KB.
   constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;
-  constexpr size_t kMaxLds = ((size_t)MAXW * NS * 16 * (16 * COLS + 4) + (size_t)NS * 16 * COLS) * sizeof(float);
+  constexpr size_t kFinLds = ((size_t)MAXW * NS * 16 * (16 * COLS + 4) + (size_t)NS * 16 * COLS) * sizeof(float);
+  constexpr size_t kMaxLds = PRO ? std::min<size_t>(kFinLds + kProLdsBytes, 160 * 1024 - 256) : kFinLds;
   if (L.lds > kMaxLds) return hipErrorInvalidValue;
   if constexpr (kMaxLds > 65536) {
     static bool attr_set = false;  // benign race: every caller sets the same value
@@ -798,26 +846,30 @@ hipError_t launch_v(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
 
 // BIG: the variant also exists with up to 8 waves per workgroup.  COLS = 4: the
 // one-pass variants (K over up to 8 waves of one workgroup, no split).
-template <int ACT, int WK, bool HZ, int EPI, int COLS, bool BIG, int KS>
+template <int ACT, int WK, bool HZ, int EPI, int COLS, bool BIG, int KS, bool PRO = false>
 hipError_t launch_t(const SkLaunch& L, const SkArgs& a, hipStream_t st) {
   if constexpr (COLS == 4) {
     if (a.splits > 1 || L.waves > 8) return hipErrorInvalidValue;
-    return launch_v<ACT, WK, HZ, EPI, 4, false, 8, KS>(L, a, st);
+    return launch_v<ACT, WK, HZ, EPI, 4, false, 8, KS, PRO>(L, a, st);
   } else {
     if (L.waves > 4) {
       if constexpr (BIG) {
-        if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 8, KS>(L, a, st);
-        return launch_v<ACT, WK, HZ, EPI, COLS, false, 8, KS>(L, a, st);
+        if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 8, KS, PRO>(L, a, st);
+        return launch_v<ACT, WK, HZ, EPI, COLS, false, 8, KS, PRO>(L, a, st);
       }
       return hipErrorInvalidValue;
     }
-    if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 4, KS>(L, a, st);
-    return launch_v<ACT, WK, HZ, EPI, COLS, false, 4, KS>(L, a, st);
+    if (a.splits > 1) return launch_v<ACT, WK, HZ, EPI, COLS, true, 4, KS, PRO>(L, a, st);
+    return launch_v<ACT, WK, HZ, EPI, COLS, false, 4, KS, PRO>(L, a, st);
   }
 }
 
 #define QL_CASE(A, W, Z, E, C, B, KSV)                                                          \
   if (L.act == A && L.wk == W && (L.hz != 0) == Z && L.epi == E && L.cols == C && L.ks == KSV) \
     return launch_t<A, W, Z, E, C, B, KSV>(L, a, st);
+// the fused-prologue variant of a case
+#define QL_CASE_PRO(W, Z, E, C, B)                                                         \
+  if (L.wk == W && (L.hz != 0) == Z && L.epi == E && L.cols == C && L.ks == KS_STEP2) \
+    return launch_t<ACT_I8, W, Z, E, C, B, KS_STEP2, true>(L, a, st);
 
 }  // namespace qlin

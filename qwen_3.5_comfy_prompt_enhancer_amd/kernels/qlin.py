@@ -70,11 +70,18 @@ _SIGS = {
     "qlin_w4_repack_awq": [_P, _I, _I, _P, _P],
     "qlin_w4_zeros_unpack": [_P, _I, _I, _I, _I, _P, _P],
     "qlin_w4_repack_ct": [_P, _I, _I, _I, _P, _P],
+    "qlin_rmsnorm_quant": [_P, _L, _I, _P, _I, _I, _I, ctypes.c_float, _I, _P, _P, _P],
+    "qlin_gate_mul_quant": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _P],
+    "qlin_norm_gated_quant": [_P, _P, _L, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P, _P, _P],
+    "qlin_pro_exp_f32": [_P, _P, _I, _P],
 }
 
-# the decode-chain entry points are declared in kernels/chain.py (they take a struct array)
+# the decode-chain entry points are declared in kernels/chain.py (they take a struct array),
+# the fused-producer linears in kernels/fused.py (they take a struct)
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_workspace_bytes", *_SIGS,
-           "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run")
+           "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run",
+           "qlin_pro_gemm_i8", "qlin_pro_gemm_w4", "qlin_pro_proj3_i8", "qlin_pro_proj3_w4",
+           "qlin_pro_mlp_gate_up_quant_i8", "qlin_pro_mlp_gate_up_quant_w4")
 
 
 def lib() -> ctypes.CDLL:

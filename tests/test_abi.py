@@ -27,8 +27,11 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 26
-    for n in ("qlin_gemm_i8", "qlin_gemm_i8_noalloc", "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run",
+    assert len(names) == 36
+    for n in ("qlin_rmsnorm_quant", "qlin_gate_mul_quant", "qlin_norm_gated_quant", "qlin_pro_exp_f32",
+              "qlin_pro_gemm_i8", "qlin_pro_gemm_w4", "qlin_pro_proj3_i8", "qlin_pro_proj3_w4",
+              "qlin_pro_mlp_gate_up_quant_i8", "qlin_pro_mlp_gate_up_quant_w4",
+              "qlin_gemm_i8", "qlin_gemm_i8_noalloc", "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run",
               "qlin_gemm_w4", "qlin_proj3_i8", "qlin_proj3_w4",
               "qlin_mlp_gate_up_quant_i8", "qlin_mlp_gate_up_quant_w4", "qlin_linear_w8",
               "qlin_linear_w4", "qlin_w4_unpack", "qlin_w4_dequant_f32",
@@ -178,3 +181,42 @@ def test_chain_validation_without_gpu():
     assert L.qlin_chain_bytes((CH._Job * 1)(job(x=0x10008)), 1, 1) == 0
     assert b"aligned" in L.qlin_last_error()
     assert L.qlin_chain_bytes((CH._Job * 1)(job()), 1, 17) == 0
+
+
+def test_producer_validation_without_gpu():
+    """The activation producers refuse bad arguments on the host with a message: K not a
+    multiple of 64, an fp32 input, a norm_gated head size the reference's kernel cannot
+    serve (64), a gate stride under 2 N, and missing q / s."""
+    qlin, L = _lib()
+    F = ctypes.c_float
+    rc = L.qlin_rmsnorm_quant(FAKE, I64(96), qlin.QLIN_BF16, FAKE, qlin.QLIN_BF16, 1, 96, F(1e-6), 1, FAKE, FAKE,
+                              None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"K=96" in L.qlin_last_error()
+    rc = L.qlin_rmsnorm_quant(FAKE, I64(128), qlin.QLIN_F32, FAKE, qlin.QLIN_BF16, 1, 128, F(1e-6), 1, FAKE, FAKE,
+                              None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"activation dtype" in L.qlin_last_error()
+    rc = L.qlin_norm_gated_quant(FAKE, FAKE, I64(128), qlin.QLIN_BF16, FAKE, qlin.QLIN_BF16, 1, 128, 64, F(1e-6),
+                                 FAKE, FAKE, None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"head size 64" in L.qlin_last_error()
+    rc = L.qlin_gate_mul_quant(FAKE, I64(256), FAKE, I64(256), qlin.QLIN_BF16, 1, 256, 128, FAKE, FAKE, None)
+    assert rc == qlin.QLIN_ERR_INVALID and b"2 K" in L.qlin_last_error()
+    rc = L.qlin_rmsnorm_quant(FAKE, I64(128), qlin.QLIN_BF16, FAKE, qlin.QLIN_BF16, 1, 128, F(1e-6), 1, None, None,
+                              None)
+    assert rc == qlin.QLIN_ERR_INVALID and b"null q" in L.qlin_last_error()
+
+
+def test_fused_producer_validation_without_gpu():
+    """A fused linear without a producer, or without q / s and without a workspace for the
+    codes, is refused before anything is launched."""
+    qlin, L = _lib()
+    from qwen35_amd.kernels import fused as FU
+    f = FU._fn("qlin_pro_gemm_i8")
+    rc = f(None, 1, 128, FAKE, FAKE, qlin.QLIN_F32, 64, FAKE, 64, None, 0, None, 0, None)
+    assert rc == qlin.QLIN_ERR_INVALID and b"null producer" in L.qlin_last_error()
+    p = FU._CProducer(kind=1, x=0x10000, ldx=128, x_dtype=qlin.QLIN_BF16, g=None, ldg=0, w=0x20000,
+                      w_dtype=qlin.QLIN_BF16, hd=0, one_plus=1, eps=1e-6, q=None, s=None)
+    rc = f(ctypes.byref(p), 1, 128, FAKE, FAKE, qlin.QLIN_F32, 64, FAKE, 64, None, 0, None, 0, None)
+    assert rc == qlin.QLIN_ERR_WORKSPACE and b"workspace" in L.qlin_last_error()
+    p.kind = 7
+    rc = f(ctypes.byref(p), 1, 128, FAKE, FAKE, qlin.QLIN_F32, 64, FAKE, 64, None, 0, None, 0, None)
+    assert rc == qlin.QLIN_ERR_INVALID and b"producer kind" in L.qlin_last_error()

@@ -401,3 +401,165 @@ def test_ct_repack_round_trip_and_planted_mistake():
 def test_ct_scale_transpose():
     s = RNG.standard_normal((6, 4)).astype(np.float32)
     assert np.array_equal(R.ct_scale_to_engine(s), s.T)
+
+
+# ---------------------------------------------------------------- activation producers
+
+def _exp_no_lo(x):
+    """exp_f32 with the low part of ln2 dropped (a planted mistake)."""
+    x = np.asarray(x, dtype=np.float32)
+    n = np.rint(x * R.LOG2E_F32).astype(np.float32)
+    r = (x - n * R.LN2_HI_F32).astype(np.float32)
+    p = np.full_like(r, R.EXP_POLY_F32[0])
+    for c in R.EXP_POLY_F32[1:]:
+        p = ((p * r).astype(np.float32) + c).astype(np.float32)
+    return np.ldexp(p, n.astype(np.int32)).astype(np.float32)
+
+
+def _exp_rel_err(f, x):
+    y = f(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    return float((np.abs(y - ref) / ref).max())
+
+
+def test_exp_f32_against_fp64():
+    """The producers' exp is within 2 ulp (2^-22 relative) of exp in fp64 over its whole
+    finite range; dropping the low part of ln2 breaks that bound."""
+    x = np.concatenate([np.linspace(-87.0, 88.0, 400_001, dtype=np.float32),
+                        (RNG.standard_normal(200_000) * 8).astype(np.float32)])
+    x = x[(x >= -87.0) & (x <= 88.0)]
+    assert _exp_rel_err(R.exp_f32, x) <= 2.0 ** -22
+    assert _exp_rel_err(_exp_no_lo, x) > 2.0 ** -22
+    assert R.exp_f32(np.float32(0.0)) == 1.0
+    e = R.exp_f32(np.array([88.5, 1e30, -87.5, -1e30], dtype=np.float32))
+    assert np.isinf(e[0]) and np.isinf(e[1]) and e[2] == 0.0 and e[3] == 0.0
+    # sigmoid / silu against fp64 (outside the saturated ends)
+    z = np.linspace(-60.0, 60.0, 100_001, dtype=np.float32)
+    sg = 1.0 / (1.0 + np.exp(-z.astype(np.float64)))
+    assert np.abs(R.sigmoid_f32(z) - sg).max() <= 4 * 2.0 ** -24
+    assert np.abs(R.silu_f32(z) - z * sg).max() <= 60 * 4 * 2.0 ** -24
+
+
+def test_sumsq_lanes_sums_every_square():
+    """With small integers every partial sum is exact whatever the order, so the fixed
+    lane order must give the exact sum of squares; random rows stay within the fp32
+    bound of the fp64 sum."""
+    for L, lanes in ((2048, 64), (128, 16), (8, 64), (520, 64)):
+        xi = RNG.integers(-100, 101, size=(3, L))
+        ss = R.sumsq_lanes(xi.astype(np.float32), lanes)
+        assert (ss == (xi.astype(np.int64) ** 2).sum(axis=1)).all()
+    x = RNG.standard_normal((4, 4096)).astype(np.float32)
+    ref = (x.astype(np.float64) ** 2).sum(axis=1)
+    assert (np.abs(R.sumsq_lanes(x, 64) - ref) <= 4096 * 2.0 ** -24 * ref).all()
+
+
+def _bf16(a):
+    return R.round_bf16(np.asarray(a, dtype=np.float32))
+
+
+def _codes_vs_fp64(q, s, y64, tie_margin=1e-3):
+    """Whether the codes equal the fp64 computation away from rounding ties and differ
+    by at most 1 near them, and the scales agree to a few fp32 ulp."""
+    M, K = y64.shape
+    g = y64.reshape(M, K // 64, 64)
+    s64 = np.maximum(np.abs(g).max(axis=2) / 127.0, 1e-8)
+    if not np.allclose(s, s64, rtol=4 * 2.0 ** -24, atol=0):
+        return False
+    v = g / s64[:, :, None]
+    q64 = np.clip(np.trunc(v + np.where(v >= 0, 0.5, -0.5)), -127, 127).reshape(M, K)
+    qi = q.astype(np.int64)
+    far = (np.abs(np.abs(v - np.trunc(v)) - 0.5) > tie_margin).reshape(M, K)
+    return bool(np.abs(qi - q64).max() <= 1 and (qi[far] == q64[far]).all())
+
+
+def _rms_y64(x, w, eps, one_plus):
+    x64 = x.astype(np.float64)
+    w64 = w.astype(np.float64) + (1.0 if one_plus else 0.0)
+    r = 1.0 / np.sqrt((x64 ** 2).mean(axis=1) + eps)
+    return x64 * r[:, None] * w64[None, :]
+
+
+def test_rmsnorm_quant_against_fp64_and_planted_mistakes():
+    """rmsnorm_quant codes equal an fp64 RMSNorm + quant away from rounding ties; a
+    variance over K - 1 and a forgotten `w + 1` both change codes."""
+    M, K = 6, 2048
+    x = _bf16(RNG.standard_normal((M, K)) * 3)
+    w = _bf16(RNG.standard_normal(K) * 0.1)
+    for one_plus in (True, False):
+        q, s = R.rmsnorm_quant_ref(x, w, 1e-6, one_plus)
+        assert _codes_vs_fp64(q, s, _rms_y64(x, w, 1e-6, one_plus))
+    q, s = R.rmsnorm_quant_ref(x, w, 1e-6, True)
+    wrong_n = _rms_y64(x, w, 1e-6, True) * np.sqrt((K - 1) / K)  # var = sum / (K - 1)
+    qn = np.clip(np.trunc(wrong_n / np.repeat(s, 64, axis=1) + 0.5 * np.sign(wrong_n)), -127, 127)
+    assert not (qn == q).all()
+    assert not _codes_vs_fp64(q, s, _rms_y64(x, w, 1e-6, False))
+
+
+def test_rmsnorm_quant_closed_forms():
+    """A constant row with a zero weight and one_plus normalizes to +-1 everywhere: every
+    code is +-127 and every scale (1/sqrt(1 + eps/c^2))/127; a zero row gives the
+    scale floor 1e-8 and zero codes."""
+    K = 256
+    x = np.stack([np.full(K, 3.0), np.full(K, -0.5), np.zeros(K)]).astype(np.float32)
+    q, s = R.rmsnorm_quant_ref(x, np.zeros(K, np.float32), 1e-6, True)
+    assert (q[0] == 127).all() and (q[1] == -127).all() and (q[2] == 0).all()
+    assert np.allclose(s[0], 1.0 / np.sqrt(1 + 1e-6 / 9) / 127, rtol=1e-6)
+    assert (s[2] == np.float32(1e-8)).all()
+
+
+def test_gate_mul_head_layout_and_fp64():
+    """With gates +100 in the second half of every head and -100 in the first,
+    sigmoid is exactly 1 on the gates the kernel must read, so y == a and the codes are
+    quant_groups(a); reading the first half instead gives zeros.  Random gates agree
+    with fp64 away from ties."""
+    M, N, hd = 3, 512, 64
+    a = _bf16(RNG.standard_normal((M, N)))
+    g = np.full((M, N // hd, 2 * hd), -100.0, dtype=np.float32)
+    g[:, :, hd:] = 100.0
+    g = g.reshape(M, 2 * N)
+    q, s = R.gate_mul_quant_ref(a, g, hd)
+    qa, sa = R.quant_groups(a)
+    assert (q == qa).all() and (s == sa).all()
+    first_half = np.repeat(np.arange(N // hd) * 2 * hd, hd) + np.tile(np.arange(hd), N // hd)
+    y_wrong = a * R.sigmoid_f32(g[:, first_half])
+    assert not (R.quant_groups(y_wrong)[0] == q).all()
+    g = _bf16(RNG.standard_normal((M, 2 * N)) * 2)
+    q, s = R.gate_mul_quant_ref(a, g, hd)
+    gv = g[:, R.gate_cols(N, hd)].astype(np.float64)
+    assert _codes_vs_fp64(q, s, a.astype(np.float64) / (1.0 + np.exp(-gv)))
+
+
+def test_norm_gated_quant_per_head_and_fp64():
+    """Per-head norm: with eps = 0, scaling one head's v by 4 leaves every code and
+    scale unchanged (power-of-two scaling is exact through the sum, the division and
+    the sqrt); a norm over the whole row would not.  Random inputs agree with fp64
+    (bf16 rounding before the quant: codes within 1, scales within a bf16 step)."""
+    T, hd, NV = 3, 128, 4
+    N = hd * NV
+    v = _bf16(RNG.standard_normal((T, N)))
+    z = _bf16(RNG.standard_normal((T, N)) * 2)
+    w = _bf16(RNG.standard_normal(hd) * 0.5 + 1.0)
+    q, s = R.norm_gated_quant_ref(v, z, w, 0.0)
+    v2 = v.copy()
+    v2[:, hd:2 * hd] *= 4
+    q2, s2 = R.norm_gated_quant_ref(v2, z, w, 0.0)
+    assert (q2 == q).all() and (s2 == s).all()
+
+    def whole_row(v_):
+        r = R.rms_inv(R.sumsq_lanes(v_, 64), N, 0.0)
+        y = (v_ * r[:, None]).astype(np.float32) * np.tile(w, NV)[None, :]
+        return R.quant_groups(R.round_bf16((y * R.silu_f32(z)).astype(np.float32)))[0]
+    assert not (whole_row(v2) == whole_row(v)).all()
+    q, s = R.norm_gated_quant_ref(v, z, w, 1e-6)
+    v64 = v.astype(np.float64).reshape(T, NV, hd)
+    r = 1.0 / np.sqrt((v64 ** 2).mean(axis=2) + 1e-6)
+    z64 = z.astype(np.float64)
+    y64 = (v64 * r[:, :, None]).reshape(T, N) * np.tile(w, NV) * (z64 / (1.0 + np.exp(-z64)))
+    y64 = _bf16(y64).astype(np.float64)  # the reference's bf16 round trip (kernels/norm.py:116)
+    g = y64.reshape(T, N // 64, 64)
+    s64 = np.maximum(np.abs(g).max(axis=2) / 127.0, 1e-8)
+    assert np.allclose(s, s64, rtol=2.0 ** -8, atol=0)
+    v_ = g / s64[:, :, None]
+    q64 = np.clip(np.trunc(v_ + np.where(v_ >= 0, 0.5, -0.5)), -127, 127).reshape(T, N)
+    assert np.abs(q.astype(np.int64) - q64).max() <= 1
+    assert (q.astype(np.int64) != q64).mean() < 0.005
