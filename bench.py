@@ -409,7 +409,29 @@ def engine_bench(args, kind):
         return K * N if kind == "w8" else K * N // 2 + (K // 128) * N * 2
 
     layer_wbytes = wbytes(2048, 8192) + wbytes(2048, 2048) + 2 * wbytes(2048, 6144) + wbytes(6144, 2048)
-    res = {}
+    res, pro_res = {}, {}
+    fused = importlib.import_module(f"{ALIAS}.kernels.fused")
+    normk = importlib.import_module(f"{ALIAS}.kernels.norm")
+    nw_in = (torch.rand(2048, generator=gen) * 0.1).to(torch.bfloat16).to(dev)
+    nw_post = (torch.rand(2048, generator=gen) * 0.1).to(torch.bfloat16).to(dev)
+
+    def timed(run):
+        run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / args.steps / layers
+
     for M in (1, 4, 512):
         a = torch.randint(-127, 128, (M, 2048), generator=gen, dtype=torch.int8).to(dev)
         s = (torch.rand(M, 32, generator=gen) * 1e-2).to(dev)
@@ -432,21 +454,39 @@ def engine_bench(args, kind):
                 fns[2](a, s, L["g"][0], L["g"][1], L["u"][0], L["u"][1], hq, hs)
                 fns[1](a6, s6, L["d"][0], L["d"][1], hid, residual=hid)
 
-        run_layers()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            run_layers()
-        for _ in range(args.warmup):
-            g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        res[M] = e0.elapsed_time(e1) * 1e-3 / args.steps / layers
+        res[M] = timed(run_layers)
+
+        # the same layer with its activation producers (engine.py:244-279 with the
+        # attention output's gate_mul_quant): producer launches + linears, then the
+        # fused calls that make their activations in the linear's own launch
+        hid.copy_(torch.randn(M, 2048, generator=gen).to(torch.bfloat16).to(dev))
+        aout = (torch.randn(M, 2048, generator=gen)).to(torch.bfloat16).to(dev)
+        xq = torch.empty(M, 2048, dtype=torch.int8, device=dev)
+        xs = torch.empty(M, 32, dtype=torch.float32, device=dev)
+
+        def run_unfused():
+            for L in lw:
+                normk.rmsnorm_quant(hid, nw_in, xq, xs, 1e-6)
+                fns[0](xq, xs, L["qkv"][0], L["qkv"][1], L["z"][0], L["z"][1], None, None, qkvz)
+                normk.gate_mul_quant(aout, qkvz, xq, xs, hd=256)
+                fns[1](xq, xs, L["o"][0], L["o"][1], hid, residual=hid)
+                normk.rmsnorm_quant(hid, nw_post, xq, xs, 1e-6)
+                fns[2](xq, xs, L["g"][0], L["g"][1], L["u"][0], L["u"][1], hq, hs)
+                fns[1](hq, hs, L["d"][0], L["d"][1], hid, residual=hid)
+
+        def run_fused():
+            for L in lw:
+                fused.pro_proj3(fused.Producer.rmsnorm(hid, nw_in, 1e-6), L["qkv"][0], L["qkv"][1], L["z"][0],
+                                L["z"][1], None, None, qkvz)
+                fused.pro_gemm_i8(fused.Producer.gate_mul(aout, qkvz, hd=256), L["o"][0], L["o"][1], hid,
+                                  residual=hid)
+                fused.pro_mlp_gate_up_quant(fused.Producer.rmsnorm(hid, nw_post, 1e-6), L["g"][0], L["g"][1],
+                                            L["u"][0], L["u"][1], hq, hs)
+                fns[1](hq, hs, L["d"][0], L["d"][1], hid, residual=hid)
+
+        pro_res[M] = (timed(run_unfused), timed(run_fused))
+        log(f"engine {kind} layer with producers M={M:4d}: {pro_res[M][0] * 1e6:7.1f} us as producer + linear "
+            f"launches, {pro_res[M][1] * 1e6:7.1f} us fused")
     act_bytes = lambda M: M * (2048 * 3 + 6144) + M * 4 * (32 * 3 + 96)
     out_bytes = lambda M: M * 2 * (8192 + 2048 * 2 * 2) + M * (6144 + 96 * 4)
     dec_bytes = {M: layer_wbytes + act_bytes(M) + out_bytes(M) for M in (1, 4)}
@@ -455,7 +495,7 @@ def engine_bench(args, kind):
         extra = (f"{dec_bytes[M] / res[M] / 1e9:7.0f} GB/s" if M in dec_bytes
                  else f"{flops / res[M] / 1e12:7.1f} TOPS")
         log(f"engine {kind} layer M={M:4d}: {res[M] * 1e6:8.1f} us per layer  {extra}")
-    return dec_bytes, flops, res
+    return dec_bytes, flops, res, pro_res
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -807,7 +847,7 @@ def main() -> int:
         dtype = "f16 x int8" if kind == "w8" else "f16 x int4"
     elif wl in ("engine-w8", "engine-w4"):
         kind = wl.split("-")[1]
-        dec_bytes, pf_flops, res = engine_bench(args, kind)
+        dec_bytes, pf_flops, res, pro_res = engine_bench(args, kind)
         # value: decode rows M = 1 and 4 through the engine's calls, weight-streaming GB/s
         t = (res[1] + res[4]) / 2
         value = (dec_bytes[1] + dec_bytes[4]) / (res[1] + res[4]) / 1e9
@@ -818,6 +858,9 @@ def main() -> int:
                   "shapes_KN": [[K, N] for (_, K, N) in ENGINE_LAYER],
                   "prefill_chunk_M512_us_per_layer": round(res[512] * 1e6, 1),
                   "prefill_chunk_M512_tops": round(pf_flops / res[512] / 1e12, 1),
+                  "with_producers_us_per_layer": {
+                      str(M): {"producer_then_linear": round(u * 1e6, 1), "fused": round(f * 1e6, 1)}
+                      for M, (u, f) in pro_res.items()},
                   "launch": "hipgraph of all layers per M"}
         dtype = "i8 x int8" if kind == "w8" else "i8 x int4"
     else:

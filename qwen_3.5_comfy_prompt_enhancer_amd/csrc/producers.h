@@ -59,48 +59,11 @@ __device__ __forceinline__ float pro_rms_inv(float ss, int n, float eps) {
   return 1.0f / __builtin_sqrtf(var + eps);
 }
 
-// 8 consecutive 16-bit values (bf16 or fp16) -> fp32; p + idx 16-byte aligned.
-__device__ __forceinline__ void pro_ld8(const void* p, int dt, long long idx, float v[8]) {
-  const u32x4 q = *(const u32x4*)((const uint16_t*)p + idx);
-  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-    v[e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
-  }
-}
-
-// 8 consecutive values of a norm weight (bf16, fp16 or fp32) -> fp32.
-__device__ __forceinline__ void pro_ldw8(const void* p, int dt, long long idx, float v[8]) {
-  if (dt == DT_F32) {
-    const f32x4 a = *(const f32x4*)((const float*)p + idx);
-    const f32x4 b = *(const f32x4*)((const float*)p + idx + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = a[e], v[4 + e] = b[e];
-  } else {
-    pro_ld8(p, dt, idx, v);
-  }
-}
-
 // Sum over a team of `lanes` consecutive lanes (a power of two) by an xor butterfly:
 // every lane of the team ends with the same value.
 __device__ __forceinline__ float pro_team_sum(float acc, int lanes) {
 #pragma clang fp contract(off)
   for (int m = lanes >> 1; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
-  return acc;
-}
-
-// One lane's share of a sum of squares: chunks c0, c0 + step, ... below nc, 8 values
-// each, in order.
-__device__ __forceinline__ float pro_sumsq_part(const void* x, int dt, long long off, int c0, int step, int nc) {
-#pragma clang fp contract(off)
-  float acc = 0.0f;
-  for (int c = c0; c < nc; c += step) {
-    float v[8];
-    pro_ld8(x, dt, off + 8LL * c, v);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = acc + v[e] * v[e];
-  }
   return acc;
 }
 
@@ -147,22 +110,156 @@ __device__ __forceinline__ void pro_put(const ProArgs& p, const ProOut& o, int K
   }
 }
 
-// Codes and scales of rows [row0, row0 + rows) over the K range [kb, ke) (multiples of
-// 64).  Called by every thread of the workgroup (it holds barriers); `lr` is LDS for
-// `rows` floats.
-__device__ __forceinline__ void pro_block(const ProArgs& p, int K, int row0, int rows, int kb, int ke,
+// Chunks of a row's sum of squares a lane loads ahead (K <= 64 * 8 * kProSumPre);
+// longer rows load the rest when they are summed.
+constexpr int kProSumPre = 8;
+
+// The loads of a producer block that go out before the linear's first weight loads.
+// A wave's memory loads complete in issue order, so loads issued after the weights
+// would wait for them: issued first, they return while the weights stream in.
+struct ProPre {
+  u32x4 xs[kProSumPre];  // rmsnorm: this lane's first chunks of its wave's first row
+  u32x4 x, g;            // the thread's first item: 8 activations, 8 gates / z values
+  u32x4 w0, w1;          // and 8 norm-weight values (w1: the second half of fp32 ones)
+};
+
+__device__ __forceinline__ u32x4 pro_raw(const void* p, long long idx16) {
+  return *(const u32x4*)((const uint16_t*)p + idx16);
+}
+
+__device__ __forceinline__ void pro_cvt8(u32x4 q, int dt, float v[8]) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+    v[e] = (dt == DT_BF16) ? bf16_to_f32(h) : (float)bitcast<_Float16>(h);
+  }
+}
+
+// Raw norm-weight values k .. k+7 (16-bit: one vector; fp32: two).
+__device__ __forceinline__ void pro_raw_w(const void* p, int dt, long long k, u32x4& w0, u32x4& w1) {
+  if (dt == DT_F32) {
+    w0 = *(const u32x4*)((const float*)p + k);
+    w1 = *(const u32x4*)((const float*)p + k + 4);
+  } else {
+    w0 = pro_raw(p, k);
+    w1 = w0;
+  }
+}
+
+__device__ __forceinline__ void pro_cvt_w(u32x4 w0, u32x4 w1, int dt, float v[8]) {
+  if (dt == DT_F32) {
+    const uint32_t a[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bitcast<float>(a[e]);
+  } else {
+    pro_cvt8(w0, dt, v);
+  }
+}
+
+// Geometry of a producer block: rows [row0, row0 + rows), K range [kb, ke) (multiples
+// of 64).  rmsnorm / gate_mul items are (row, 64-column group) for 8-lane teams;
+// norm_gated items are (row, head) for teams of hd / 8 lanes.
+struct ProGeo {
+  int row0, rows, kb, ke;
+  int ng;      // 64-column groups of the range
+  int T;       // norm_gated: team size; 8 otherwise
+  int h0, nh;  // norm_gated: heads overlapping the range
+};
+
+__device__ __forceinline__ ProGeo pro_geo(const ProArgs& p, int row0, int rows, int kb, int ke) {
+  ProGeo g;
+  g.row0 = row0;
+  g.rows = rows;
+  g.kb = kb;
+  g.ke = ke;
+  g.ng = (ke - kb) >> 6;
+  g.T = (p.kind == PRO_NORM_GATED) ? (p.hd >> 3) : 8;
+  g.h0 = (p.kind == PRO_NORM_GATED) ? kb / p.hd : 0;
+  g.nh = (p.kind == PRO_NORM_GATED) ? (ke + p.hd - 1) / p.hd - g.h0 : 0;
+  return g;
+}
+
+// Issues the block's first loads (every thread: its wave's first row for rmsnorm's
+// sum of squares, its first item).  Branch-free: every load goes out, from clamped
+// in-bounds addresses, and pro_block uses only the applicable ones (a load whose
+// result is merged at a control-flow join is waited for at the join, which would
+// hold the weight loads behind it).
+__device__ __forceinline__ void pro_issue(const ProArgs& p, int K, const ProGeo& G, ProPre& pp) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const bool ng_kind = p.kind == PRO_NORM_GATED;
+  // rmsnorm's chunks (other kinds read the same in-bounds addresses and ignore them)
+  const long long soff = (long long)(G.row0 + min(wave, G.rows - 1)) * p.ldx;
+  const int nc = K >> 3;
+#pragma unroll
+  for (int i = 0; i < kProSumPre; ++i) pp.xs[i] = pro_raw(p.x, soff + 8LL * min(lane + 64 * i, nc - 1));
+  // the first item
+  long long xi, gi, wi;
+  if (ng_kind) {
+    const int tl = tid & (G.T - 1);
+    const int it = min(tid / G.T, G.rows * G.nh - 1);
+    const int r = it / G.nh, h = G.h0 + (it - r * G.nh);
+    xi = (long long)(G.row0 + r) * K + (long long)h * p.hd + 8 * tl;
+    gi = (long long)(G.row0 + r) * p.ldg + (long long)h * p.hd + 8 * tl;
+    wi = 8 * tl;
+  } else {
+    const int it = min(tid >> 3, G.rows * G.ng - 1);
+    const int r = it / G.ng;
+    const int k = G.kb + (it - r * G.ng) * 64 + 8 * (tid & 7);
+    xi = (long long)(G.row0 + r) * p.ldx + k;
+    gi = (long long)(G.row0 + r) * p.ldg + (long long)(k / max(p.hd, 1)) * (2 * p.hd) + p.hd + (k % max(p.hd, 1));
+    wi = k;
+  }
+  // kinds without gates or norm weight read fixed addresses of x instead (distinct from
+  // the item's own, so the compiler cannot turn them into copies behind a branch)
+  const bool has_g = p.kind != PRO_RMSNORM, has_w = p.kind != PRO_GATE_MUL;
+  pp.x = pro_raw(p.x, xi);
+  pp.g = pro_raw(has_g ? p.g : p.x, has_g ? gi : 0);
+  const bool f32w = has_w && p.wdt == DT_F32;
+  const uint8_t* wb = has_w ? (const uint8_t*)p.w + wi * (f32w ? 4 : 2) : (const uint8_t*)p.x + 16;
+  pp.w0 = *(const u32x4*)wb;
+  pp.w1 = *(const u32x4*)(wb + (f32w ? 16 : 0));
+}
+
+// Codes and scales of the block (pro_issue's loads first, then the rest), into LDS
+// and / or the global code matrices.  Called by every thread of the workgroup (it
+// holds barriers); `lr` is LDS for `rows` floats.
+__device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo& G, const ProPre& pp,
                                           const ProOut& o, float* lr) {
 #pragma clang fp contract(off)
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
-  const int ng = (ke - kb) >> 6;
+  const int rows = G.rows, row0 = G.row0, kb = G.kb, ke = G.ke, ng = G.ng;
   if (p.kind == PRO_RMSNORM || p.kind == PRO_GATE_MUL) {
     if (p.kind == PRO_RMSNORM) {
-      // each row's inverse RMS over the whole row, one wave per row
+      // each row's inverse RMS over the whole row, one wave per row; the chunks of a
+      // lane are folded in order: the prefetched ones, then the rest
       const int wave = tid >> 6, lane = tid & 63, nw = nthr >> 6;
+      const int nc = K >> 3;
       for (int r = wave; r < rows; r += nw) {
         const long long off = (long long)(row0 + r) * p.ldx;
-        const float ss = pro_team_sum(pro_sumsq_part(p.x, p.xdt, off, lane, 64, K >> 3), 64);
+        float acc = 0.0f;
+        int c0 = lane;
+        if (r == wave) {
+#pragma unroll
+          for (int i = 0; i < kProSumPre; ++i) {
+            if (lane + 64 * i < nc) {
+              float v[8];
+              pro_cvt8(pp.xs[i], p.xdt, v);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) acc = acc + v[e] * v[e];
+            }
+          }
+          c0 = lane + 64 * kProSumPre;
+        }
+        for (int c = c0; c < nc; c += 64) {
+          float v[8];
+          pro_cvt8(pro_raw(p.x, off + 8LL * c), p.xdt, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc = acc + v[e] * v[e];
+        }
+        const float ss = pro_team_sum(acc, 64);
         if (lane == 0) lr[r] = pro_rms_inv(ss, K, p.eps);
       }
       __syncthreads();
@@ -171,11 +268,14 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, int row0, int
     for (int it = tid >> 3; it < rows * ng; it += nthr >> 3) {
       const int r = it / ng;
       const int k = kb + (it - r * ng) * 64 + 8 * t8;
+      const bool first = it == (tid >> 3);
       float x[8], y[8];
+      pro_cvt8(first ? pp.x : pro_raw(p.x, (long long)(row0 + r) * p.ldx + k), p.xdt, x);
       if (p.kind == PRO_RMSNORM) {
         float w[8];
-        pro_ld8(p.x, p.xdt, (long long)(row0 + r) * p.ldx + k, x);
-        pro_ldw8(p.w, p.wdt, k, w);
+        u32x4 w0 = pp.w0, w1 = pp.w1;
+        if (!first) pro_raw_w(p.w, p.wdt, k, w0, w1);
+        pro_cvt_w(w0, w1, p.wdt, w);
         const float ri = lr[r];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -185,9 +285,8 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, int row0, int
       } else {
         // gates of head h sit at [h * 2 hd + hd, (h + 1) * 2 hd) of the gate row
         float gv[8];
-        pro_ld8(p.x, p.xdt, (long long)(row0 + r) * p.ldx + k, x);
         const long long gc = (long long)(k / p.hd) * (2 * p.hd) + p.hd + (k % p.hd);
-        pro_ld8(p.g, p.xdt, (long long)(row0 + r) * p.ldg + gc, gv);
+        pro_cvt8(first ? pp.g : pro_raw(p.g, (long long)(row0 + r) * p.ldg + gc), p.xdt, gv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = x[e] * pro_sigmoid(gv[e]);
       }
@@ -196,22 +295,23 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, int row0, int
   } else {
     // PRO_NORM_GATED: teams of hd / 8 lanes, one (row, head) each; a head's groups are
     // written where they fall inside [kb, ke)
-    const int T = p.hd >> 3;
+    const int T = G.T;
     const int tl = tid & (T - 1);
-    const int h0 = kb / p.hd, h1 = (ke + p.hd - 1) / p.hd;
-    const int nh = h1 - h0;
+    const int nh = G.nh;
     for (int it = tid / T; it < rows * nh; it += nthr / T) {
       const int r = it / nh;
-      const int h = h0 + (it - r * nh);
+      const int h = G.h0 + (it - r * nh);
+      const bool first = it == tid / T;
       const long long off = (long long)(row0 + r) * K + (long long)h * p.hd;
       float x[8], zv[8], w[8], y[8];
-      pro_ld8(p.x, p.xdt, off + 8 * tl, x);
+      pro_cvt8(first ? pp.x : pro_raw(p.x, off + 8 * tl), p.xdt, x);
       float acc = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = acc + x[e] * x[e];
       const float ri = pro_rms_inv(pro_team_sum(acc, T), p.hd, p.eps);
-      pro_ld8(p.g, p.xdt, (long long)(row0 + r) * p.ldg + (long long)h * p.hd + 8 * tl, zv);
-      pro_ldw8(p.w, p.wdt, 8 * tl, w);
+      pro_cvt8(first ? pp.g : pro_raw(p.g, (long long)(row0 + r) * p.ldg + (long long)h * p.hd + 8 * tl), p.xdt,
+               zv);
+      pro_cvt_w(pp.w0, pp.w1, p.wdt, w);  // the same 8 weights for every head
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float sz = zv[e] * pro_sigmoid(zv[e]);

@@ -21,7 +21,10 @@ __global__ __launch_bounds__(kProThreads) void producer_kernel(const ProArgs p, 
   o.ldq = 0;
   o.lng = 0;
   o.emit = true;
-  pro_block(p, K, blockIdx.x, 1, 0, K, o, lr);
+  const ProGeo G = pro_geo(p, blockIdx.x, 1, 0, K);
+  ProPre pp;
+  pro_issue(p, K, G, pp);
+  pro_block(p, K, G, pp, o, lr);
 }
 
 __global__ void pro_exp_kernel(const float* x, float* y, int n) {

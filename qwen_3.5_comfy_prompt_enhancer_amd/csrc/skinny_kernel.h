@@ -399,6 +399,8 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
   const int plng = (kwe - kwb) >> 6;
   float* const pls = (float*)(plq + (long long)Mt * a.pro.ldq);
   float* const plr = pls + Mt * plng;
+  ProGeo pgeo;
+  ProPre ppre;
   auto prologue = [&]() {
     if constexpr (PRO) {
       ProOut o;
@@ -407,7 +409,7 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       o.ldq = a.pro.ldq;
       o.lng = plng;
       o.emit = a.pro.q != nullptr && tile == 0;
-      pro_block(a.pro, K, rt * 16, Mt, kwb, kwe, o, plr);
+      pro_block(a.pro, K, pgeo, ppre, o, plr);
     }
   };
   auto run_pipeline = [&](auto&& compute) {
@@ -448,13 +450,21 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       tail(base0);
     } else {
       // every load issued unconditionally, the step index clamped to the last step
-      if (nsteps > 0) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) load_step(buf[d], kof(d < nsteps ? d : nsteps - 1));
-      }
       if constexpr (PRO) {
+        // the prologue's loads go out first (a wave's loads complete in issue order),
+        // then the first weight loads -- unconditionally, so that no control-flow join
+        // lies between them and the prologue's waits (waves without steps load the
+        // workgroup's first K rows and drop them)
+        pgeo = pro_geo(a.pro, rt * 16, Mt, kwb, kwe);
+        pro_issue(a.pro, K, pgeo, ppre);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_step(buf[d], nsteps > 0 ? kof(d < nsteps ? d : nsteps - 1) : kwb);
         prologue();  // every wave, with its first loads in flight
         if (nsteps <= 0) return;
+      } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_step(buf[d], kof(d < nsteps ? d : nsteps - 1));
       }
       const int nfull = nsteps - nsteps % U;
       for (int base = 0; base < nfull; base += U) {
