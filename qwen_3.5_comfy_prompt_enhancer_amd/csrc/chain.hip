@@ -29,8 +29,8 @@
 //     device-coherent stores and an arrival counter; the last unit to arrive sums the
 //     splits in split order (deterministic), applies the W8 column scale and the
 //     residual (one fmaf), and stores the 16-bit output with device-coherent stores.
-//     After those stores complete it counts the tile for its job; a job's last tile
-//     counts the job for its level, and a level's last job sets the level's flag.
+//     After those stores complete it counts the tile for its level, and the level's
+//     last tile sets the level's flag.
 //   * The K order of an output depends on (K, N) only, so rows of an M = 4 step equal
 //     an M = 1 step bit for bit.
 //   * The last workgroup to leave resets the queues, the exit and level counters and
@@ -56,11 +56,15 @@ constexpr int CW = 4;              // waves per workgroup = per work unit
 constexpr int CT = 64 * CW;
 constexpr int TNC = 128;           // columns per tile: 16 lanes x 8 columns
 constexpr int TNP = TNC + 4;       // padded LDS row
-constexpr int W8_STEPS = 4;        // 32-wide K steps per wave per unit (W8)
-constexpr int W4_STEPS = 4;        // (W4: one group of 128)
-constexpr int KU_W8 = CW * W8_STEPS * 32;  // K rows per unit: 512
-constexpr int KU_W4 = CW * W4_STEPS * 32;  // 512
+constexpr int RING = 4;            // 32-wide K steps a wave has in flight (its register ring)
+constexpr int KU = CW * RING * 32; // K rows of the shortest unit: 512 (W4: one group of 128 per wave)
 constexpr int kSpinLimit = 1 << 22;        // polls of a dependency before giving up
+// Levels whose units at the shortest length outnumber the workgroups that fit the chip
+// this many times over (kPlanSlots: 3 workgroups on each of 256 CUs) take longer W8
+// units -- up to a tile's whole K -- streamed through the same register ring: fewer
+// split-K exchanges, the same parallelism.
+constexpr int kPlanSlots = 768;
+constexpr int kLongFactor = 2;
 
 // Device descriptor of one job.
 struct alignas(16) ChainJob {
@@ -76,6 +80,8 @@ struct alignas(16) ChainJob {
   long long part;   // first float of this job's partials within the partial region
   int K, N, wk, sdt, odt;
   int ntiles, splits, unit0, cnt0, level, index;
+  int wsteps;       // 32-wide K steps per wave per unit (a multiple of RING; W4: RING)
+  int pad_[3];
 };
 
 // Header at the start of a plan (device memory).
@@ -91,9 +97,9 @@ constexpr int kMagic = 0x71636831;  // "qch1"
 // each, measured), so the hot ones are spread out.
 //   [32 q]                              queue q (q < kQueues): units q, q + 8, q + 16, ...
 //   [32 kQueues]                        workgroups that have left
-//   [kLevel0 + 32 l]                    finished jobs of level l
-//   [kLevel0 + 32 nlevels + 16 j]       finished tiles of job j (reset by its last tile)
-//   [... + 16 njobs + cnt0 + tile]      split-K arrivals of a tile (reset by its last unit)
+//   [kLevel0 + 32 l]                    finished tiles of level l
+//   [kLevel0 + 32 nlevels + 16 njobs + cnt0 + tile]
+//                                       split-K arrivals of a tile (reset by its last unit)
 // Level done flags follow in a region of their own, one per 128-byte line.
 constexpr int kQueues = 8;
 constexpr int kLevel0 = 32 * (kQueues + 1);
@@ -113,10 +119,11 @@ __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t d[2]) {
   d[1] = v.y;
 }
 
-// Registers a unit's weights (and W4 group scales, zeros) are loaded into.
+// Registers a unit's weights (and W4 group scales, zeros) are loaded into: a ring of
+// RING steps.
 template <bool W4>
 struct UnitRegs {
-  static constexpr int STEPS = W4 ? W4_STEPS : W8_STEPS;
+  static constexpr int STEPS = RING;
   static constexpr int NR = W4 ? 4 : 8;  // weight rows per lane per step
   uint32_t w[STEPS][NR][2];
   u32x4 sraw[2];  // W4: raw group scales of the lane's 8 columns
@@ -143,35 +150,46 @@ __device__ __forceinline__ UnitPos decode_unit(const ChainJob* __restrict__ jobs
 // The wave's first K row and 32-wide steps of a unit.
 template <bool W4>
 __device__ __forceinline__ void wave_range(const UnitPos& P, int* k0, int* nsteps) {
-  constexpr int kw = UnitRegs<W4>::STEPS * 32;
+  const int kw = P.J.wsteps * 32;
   const int wave = threadIdx.x >> 6;
   *k0 = P.split * (CW * kw) + wave * kw;
-  *nsteps = max(0, min(UnitRegs<W4>::STEPS, (P.J.K - *k0) / 32));  // W4: 0 or 4 (K % 128 == 0)
+  *nsteps = max(0, min(P.J.wsteps, (P.J.K - *k0) / 32));  // W4: 0 or 4 (K % 128 == 0)
 }
 
-// Issues every weight / scale / zero load of a unit (nothing waits for them here).
+// Issues the weight loads of step i of the wave's range into one ring slot.  Steps past
+// the range (the last split of a K that is not a multiple of the unit) load the wave's
+// last in-range step again, or step 0 of the matrix if it has none: every register is
+// written, so none stays live from the previous unit.
+template <bool W4>
+__device__ __forceinline__ void load_w_step(const UnitPos& P, int k0, int nsteps, int i,
+                                            uint32_t (&w)[UnitRegs<W4>::NR][2]) {
+  constexpr int NR = UnitRegs<W4>::NR;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int N = P.J.N;
+  const int col = P.tile * TNC + j * 8;  // lane's first column; N % 16 == 0, so col < N => col + 8 <= N
+  const int ccl = col < N ? col : 0;
+  const int kb = nsteps > 0 ? k0 : 0;
+  const int slast = nsteps > 0 ? nsteps - 1 : 0;
+  const int sc = i < slast ? i : slast;
+  const long long r0 = W4 ? (long long)((kb + 32 * sc) / 2 + 4 * g) : (long long)(kb + 32 * sc + 8 * g);
+  const uint8_t* base = P.J.w + r0 * N + ccl;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) ld8<8>(base + (long long)r * N, w[r]);
+}
+
+// Issues every load of a unit's first RING steps (weights, W4 scales and zeros; nothing
+// waits for them here).
 template <bool W4>
 __device__ __forceinline__ void issue_loads(const UnitPos& P, UnitRegs<W4>& R) {
-  constexpr int STEPS = UnitRegs<W4>::STEPS, NR = UnitRegs<W4>::NR;
-  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  constexpr int STEPS = UnitRegs<W4>::STEPS;
+  const int lane = threadIdx.x & 63, j = lane & 15;
   const int K = P.J.K, N = P.J.N;
   int k0, nsteps;
   wave_range<W4>(P, &k0, &nsteps);
-  const int col = P.tile * TNC + j * 8;  // lane's first column; N % 16 == 0, so col < N => col + 8 <= N
+  const int col = P.tile * TNC + j * 8;
   const int ccl = col < N ? col : 0;
-  // steps past the wave's range (the last split of a K that is not a multiple of the
-  // unit) load the wave's last in-range step again, or step 0 of the matrix if it has
-  // none: every register is written, so none stays live from the previous unit
-  const int kb = nsteps > 0 ? k0 : 0;
-  const int slast = nsteps > 0 ? nsteps - 1 : 0;
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const int sc = s < slast ? s : slast;
-    const long long r0 = W4 ? (long long)((kb + 32 * sc) / 2 + 4 * g) : (long long)(kb + 32 * sc + 8 * g);
-    const uint8_t* base = P.J.w + r0 * N + ccl;
-#pragma unroll
-    for (int r = 0; r < NR; ++r) ld8<8>(base + (long long)r * N, R.w[s][r]);
-  }
+  for (int s = 0; s < STEPS; ++s) load_w_step<W4>(P, k0, nsteps, s, R.w[s]);
   if constexpr (W4) {
     const int gi = min(k0 / 128, K / 128 - 1);
     const long long idx = (long long)gi * N + ccl;
@@ -184,26 +202,49 @@ __device__ __forceinline__ void issue_loads(const UnitPos& P, UnitRegs<W4>& R) {
   }
 }
 
-// Activations of a unit, device-coherent (an earlier job may have written them).  Every
-// step is loaded (no branch around the accumulators): a step past the wave's range, a
-// row past M, or every step when `now` is false reads at an offset beyond the buffer's
-// range, which returns zeros and moves no data.
+// Activations of step i of the wave's range, device-coherent (an earlier job may have
+// written them).  Every step is loaded (no branch around the accumulators): a step past
+// the wave's range, a row past M, or any step when `now` is false reads at an offset
+// beyond the buffer's range, which returns zeros and moves no data.
+__device__ __forceinline__ u32x4 load_x_step(const UnitPos& P, __amdgpu_buffer_rsrc_t xr, int M, bool now, int k0,
+                                             int nsteps, int i) {
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const unsigned off = (unsigned)(((long long)j * P.J.ldx + k0 + 32 * i + 8 * g) * 2);
+  return ld_x_coherent(xr, (now && i < nsteps && j < M) ? off : 0xFFFFFFF0u);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_rsrc(const UnitPos& P, int M) {
+  return part_rsrc(P.J.x, (unsigned)(((long long)(M - 1) * P.J.ldx + P.J.K) * 2));
+}
+
+// The activations of a unit's first RING steps.
 template <bool W4>
 __device__ __forceinline__ void load_x(const UnitPos& P, int M, bool now, u32x4 xv[UnitRegs<W4>::STEPS]) {
   constexpr int STEPS = UnitRegs<W4>::STEPS;
-  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   int k0, nsteps;
   wave_range<W4>(P, &k0, &nsteps);
-  const __amdgpu_buffer_rsrc_t xr = part_rsrc(P.J.x, (unsigned)(((long long)(M - 1) * P.J.ldx + P.J.K) * 2));
+  const __amdgpu_buffer_rsrc_t xr = x_rsrc(P, M);
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const unsigned off = (unsigned)(((long long)j * P.J.ldx + k0 + 32 * s + 8 * g) * 2);
-    xv[s] = ld_x_coherent(xr, (now && s < nsteps && j < M) ? off : 0xFFFFFFF0u);
+  for (int s = 0; s < STEPS; ++s) xv[s] = load_x_step(P, xr, M, now, k0, nsteps, s);
+}
+
+// One 32-wide W8 step: 8 MFMAs of the lane's 8 columns against the step's activations.
+__device__ __forceinline__ void w8_step(const uint32_t (&w)[8][2], u32x4 x, f32x4 (&acc)[8]) {
+  const f16x8 av = bitcast<f16x8>(x);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int q = t >> 2, b = t & 3;
+    u32x4 bw;
+    bw.x = w8_pair_f16(w[0][q], w[1][q], b);
+    bw.y = w8_pair_f16(w[2][q], w[3][q], b);
+    bw.z = w8_pair_f16(w[4][q], w[5][q], b);
+    bw.w = w8_pair_f16(w[6][q], w[7][q], b);
+    acc[t] = mfma_f16(av, bitcast<f16x8>(bw), acc[t]);
   }
 }
 
-// Level L's tile count (cnt[2 + L]) reaches need[L] -> its done flag (one per 128-byte
-// line from flag_off) is set by the unit whose tile completed it.
+// Level L's tile count reaches need[L] (the level's tiles) -> its done flag (one per
+// 128-byte line from flag_off) is set by the unit whose tile completed it.
 __device__ __forceinline__ unsigned* level_flag(uint8_t* plan, const ChainHdr& H, int l) {
   return (unsigned*)(plan + H.flag_off) + 32 * l;
 }
@@ -281,20 +322,22 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (!W4) {
-#pragma unroll
-      for (int s = 0; s < STEPS; ++s) {
-        const f16x8 av = bitcast<f16x8>(xv[s]);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int q = t >> 2, b = t & 3;
-          u32x4 bw;
-          bw.x = w8_pair_f16(R.w[s][0][q], R.w[s][1][q], b);
-          bw.y = w8_pair_f16(R.w[s][2][q], R.w[s][3][q], b);
-          bw.z = w8_pair_f16(R.w[s][4][q], R.w[s][5][q], b);
-          bw.w = w8_pair_f16(R.w[s][6][q], R.w[s][7][q], b);
-          acc[t] = mfma_f16(av, bitcast<f16x8>(bw), acc[t]);
-        }
+      // the wave's steps through the RING-deep register ring: each step's slot is
+      // refilled with the step RING ahead as soon as its MFMAs are issued; the last
+      // RING steps issue no loads
+      const int ncyc = J.wsteps / RING;
+      const __amdgpu_buffer_rsrc_t xr = x_rsrc(P, M);
+      for (int cyc = 0; cyc + 1 < ncyc; ++cyc) {
+        static_for<0, RING>([&](auto sc) {
+          constexpr int s = decltype(sc)::value;
+          w8_step(R.w[s], xv[s], acc);
+          const int nx = RING * (cyc + 1) + s;
+          load_w_step<false>(P, k0, nsteps, nx, R.w[s]);
+          xv[s] = load_x_step(P, xr, M, true, k0, nsteps, nx);
+        });
       }
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) w8_step(R.w[s], xv[s], acc);
     } else {
       // (1024 + lo, 64 + hi) operands; the wave's K range is one group of 128, folded
       // once at its end: scale * (acc - (c1 + z c2))
@@ -453,16 +496,12 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       __syncthreads();
       if (tid == 0) {
-        // the job's last tile counts the job for its level; the level's last job sets the flag
-        unsigned* jc = cnt + kLevel0 + 32 * H.nlevels + 16 * J.index;
-        const unsigned prev = __hip_atomic_fetch_add(jc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (prev + 1 == (unsigned)J.ntiles) {
-          __hip_atomic_store(jc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const unsigned pl =
-              __hip_atomic_fetch_add(cnt + kLevel0 + 32 * J.level, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (pl + 1 == need[J.level])
-            __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        // the tile counts for its level; the level's last tile sets the level's flag (one
+        // atomic on the critical path between levels)
+        const unsigned pl =
+            __hip_atomic_fetch_add(cnt + kLevel0 + 32 * J.level, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (pl + 1 == need[J.level])
+          __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     __syncthreads();  // every thread is done with red, s_unit and s_flag of this unit
@@ -502,13 +541,19 @@ int fail_chain(int code, const char* fmt, int i, int a = 0, int b = 0) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Validates the jobs and computes the plan layout (and, if `jobs_out`, the descriptors).
+//
+// Unit length: each wave of a unit folds RING steps of 32 K rows (the shortest unit, KU
+// = 512 rows per unit) or, for W8 levels with many units, a multiple of that streamed
+// through the ring: r = (the level's shortest units) / (kLongFactor * kPlanSlots), at
+// most a tile's whole K.  Within a level, jobs are laid out longest unit first, so the
+// queues hand out the long units early and the short ones fill the end.
 int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::vector<ChainJob>* jobs_out,
                  std::vector<int>* unit_job, std::vector<unsigned>* need) {
   if (!jobs || njobs <= 0) return set_error(QLIN_ERR_INVALID, "qlin_chain: no jobs");
   if (M < 1 || M > 16) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: M=%d (1-16 rows)", M);
-  long long units = 0, ncnt = 0, parts = 0;
   int prev_level = 0;
   const bool w4_chain = jobs[0].group != 0;
+  std::vector<long long> level_units;  // units per level at the shortest unit length
   for (int i = 0; i < njobs; ++i) {
     const qlin_chain_job& q = jobs[i];
     const bool w4 = q.group != 0;
@@ -538,12 +583,39 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
     // byte offsets within 32-bit buffer ranges
     if (((long long)(M - 1) * q.ldx + q.K) * 2 >= (1LL << 31) || ((long long)(M - 1) * q.ldo + q.N) * 2 >= (1LL << 31))
       return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: activation or output too large", i);
+    const int ntiles = (q.N + TNC - 1) / TNC;
+    if ((long long)ntiles * ((q.K + KU - 1) / KU) * M * TNC * 4 >= (1LL << 31))
+      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: partials too large", i);
     prev_level = q.level;
-    const int ku = w4 ? KU_W4 : KU_W8;
+    if ((int)level_units.size() <= q.level) level_units.resize(q.level + 1, 0);
+    level_units[q.level] += (long long)ntiles * ((q.K + KU - 1) / KU);
+  }
+  const int nlevels = prev_level + 1;
+  // per job: steps per wave, and the layout order (level, then longest unit first)
+  std::vector<int> wsteps(njobs), order(njobs);
+  for (int i = 0; i < njobs; ++i) {
+    const qlin_chain_job& q = jobs[i];
+    int r = 1;
+    if (!w4_chain) {
+      const long long lr = level_units[q.level] / ((long long)kLongFactor * kPlanSlots);
+      r = (int)std::max<long long>(1, std::min<long long>(lr, (q.K + KU - 1) / KU));
+    }
+    wsteps[i] = RING * r;
+    order[i] = i;
+  }
+  auto unit_rows = [&](int i) { return std::min(jobs[i].K, CW * wsteps[i] * 32); };
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+    if (jobs[a].level != jobs[b].level) return jobs[a].level < jobs[b].level;
+    return unit_rows(a) > unit_rows(b);
+  });
+  long long units = 0, ncnt = 0, parts = 0;
+  for (int oi = 0; oi < njobs; ++oi) {
+    const int i = order[oi];
+    const qlin_chain_job& q = jobs[i];
+    const bool w4 = q.group != 0;
+    const int ku = CW * wsteps[i] * 32;
     const int splits = (q.K + ku - 1) / ku;
     const int ntiles = (q.N + TNC - 1) / TNC;
-    if ((long long)ntiles * splits * M * TNC * 4 >= (1LL << 31))
-      return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d: partials too large", i);
     if (jobs_out) {
       ChainJob d;
       memset(&d, 0, sizeof(d));
@@ -568,10 +640,11 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
       d.cnt0 = (int)ncnt;
       d.level = q.level;
       d.index = i;
+      d.wsteps = wsteps[i];
       jobs_out->push_back(d);
-      for (long long t = 0; t < (long long)ntiles * splits; ++t) unit_job->push_back(i);
+      for (long long t = 0; t < (long long)ntiles * splits; ++t) unit_job->push_back(oi);
       if ((int)need->size() <= q.level) need->resize(q.level + 1, 0u);
-      (*need)[q.level] += 1u;  // jobs of the level
+      (*need)[q.level] += (unsigned)ntiles;  // tiles of the level
     }
     units += (long long)ntiles * splits;
     if (splits > 1) {
@@ -581,7 +654,7 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
     if (units > (1LL << 30)) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: too many work units (job %d)", i);
   }
   L->nunits = (int)units;
-  L->nlevels = prev_level + 1;
+  L->nlevels = nlevels;
   L->ncnt = (int)(kLevel0 + 32LL * L->nlevels + 16LL * njobs + ncnt);
   L->part_floats = parts;
   L->jobs_off = align256(sizeof(ChainHdr));
