@@ -60,9 +60,9 @@ constexpr int RING = 4;            // 32-wide K steps a wave has in flight (its 
 constexpr int KU = CW * RING * 32; // K rows of the shortest unit: 512 (W4: one group of 128 per wave)
 constexpr int kSpinLimit = 1 << 22;        // polls of a dependency before giving up
 // Levels whose units at the shortest length outnumber the workgroups that fit the chip
-// this many times over (kPlanSlots: 3 workgroups on each of 256 CUs) take longer W8
-// units -- up to a tile's whole K -- streamed through the same register ring: fewer
-// split-K exchanges, the same parallelism.
+// this many times over (kPlanSlots: 3 workgroups on each of 256 CUs) take longer units
+// -- up to a tile's whole K -- streamed through the same register ring: fewer split-K
+// exchanges, the same parallelism.
 constexpr int kPlanSlots = 768;
 constexpr int kLongFactor = 2;
 
@@ -80,7 +80,7 @@ struct alignas(16) ChainJob {
   long long part;   // first float of this job's partials within the partial region
   int K, N, wk, sdt, odt;
   int ntiles, splits, unit0, cnt0, level, index;
-  int wsteps;       // 32-wide K steps per wave per unit (a multiple of RING; W4: RING)
+  int wsteps;       // 32-wide K steps per wave per unit (a multiple of RING)
   int pad_[3];
 };
 
@@ -127,7 +127,7 @@ struct UnitRegs {
   static constexpr int NR = W4 ? 4 : 8;  // weight rows per lane per step
   uint32_t w[STEPS][NR][2];
   u32x4 sraw[2];  // W4: raw group scales of the lane's 8 columns
-  uint32_t zr[2];  // W4: their zeros
+  uint32_t zr[2];  // W4: their zeros (read when the job has a zeros tensor)
 };
 
 // A unit's place: job descriptor (uniform), tile, K split.
@@ -177,6 +177,23 @@ __device__ __forceinline__ void load_w_step(const UnitPos& P, int k0, int nsteps
   for (int r = 0; r < NR; ++r) ld8<8>(base + (long long)r * N, w[r]);
 }
 
+// Issues the W4 scale and zero loads of group `grp` of the wave's range (clamped to the
+// matrix's last group).  Jobs without zeros read the scales' address instead, and the
+// fold uses z = 8: no load is merged at a control-flow join.
+__device__ __forceinline__ void load_group(const UnitPos& P, int k0, int grp, UnitRegs<true>& R) {
+  const int lane = threadIdx.x & 63, j = lane & 15;
+  const int K = P.J.K, N = P.J.N;
+  const int col = P.tile * TNC + j * 8;
+  const int ccl = col < N ? col : 0;
+  const int gi = min(k0 / 128 + grp, K / 128 - 1);
+  const long long idx = (long long)gi * N + ccl;
+  const bool f32 = P.J.sdt == DT_F32;
+  const uint8_t* sb = (const uint8_t*)P.J.s + idx * (f32 ? 4 : 2);
+  R.sraw[0] = *(const u32x4*)sb;
+  R.sraw[1] = *(const u32x4*)(sb + (f32 ? 16 : 0));
+  ld8<8>(P.J.z ? P.J.z + idx : sb, R.zr);
+}
+
 // Issues every load of a unit's first RING steps (weights, W4 scales and zeros; nothing
 // waits for them here).
 template <bool W4>
@@ -190,16 +207,9 @@ __device__ __forceinline__ void issue_loads(const UnitPos& P, UnitRegs<W4>& R) {
   const int ccl = col < N ? col : 0;
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) load_w_step<W4>(P, k0, nsteps, s, R.w[s]);
-  if constexpr (W4) {
-    const int gi = min(k0 / 128, K / 128 - 1);
-    const long long idx = (long long)gi * N + ccl;
-    const bool f32 = P.J.sdt == DT_F32;
-    const uint8_t* sb = (const uint8_t*)P.J.s + idx * (f32 ? 4 : 2);
-    R.sraw[0] = *(const u32x4*)sb;
-    R.sraw[1] = *(const u32x4*)(sb + (f32 ? 16 : 0));
-    if (P.J.z) ld8<8>(P.J.z + idx, R.zr);
-    else R.zr[0] = R.zr[1] = 0x08080808u;
-  }
+  if constexpr (W4) load_group(P, k0, 0, R);
+  (void)K;
+  (void)ccl;
 }
 
 // Activations of step i of the wave's range, device-coherent (an earlier job may have
@@ -259,7 +269,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
   constexpr int STEPS = UnitRegs<W4>::STEPS;
   const ChainHdr H = *(const ChainHdr*)plan;
   unsigned* const cnt = (unsigned*)(plan + H.cnt_off);
-  __shared__ float red[CW * 16 * TNP];
+  __shared__ __attribute__((aligned(16))) float red[CW * 16 * TNP];
   __shared__ int s_unit, s_flag;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int j = lane & 15, g = lane >> 4;
@@ -339,47 +349,77 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) w8_step(R.w[s], xv[s], acc);
     } else {
-      // (1024 + lo, 64 + hi) operands; the wave's K range is one group of 128, folded
-      // once at its end: scale * (acc - (c1 + z c2))
-      f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f}, c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+      // (1024 + lo, 64 + hi) operands.  One ring cycle of RING steps is one group of
+      // 128; at its end the group folds scale * (acc - (c1 + z c2)) into the wave's LDS
+      // slot (tot = fma(scale, d, tot), the first group a plain product), which the
+      // workgroup sum below reads, and the next group's scales are loaded.
       const f16x8 boff = f16x8{(_Float16)1024.0f, (_Float16)64.0f, (_Float16)1024.0f, (_Float16)64.0f,
                                (_Float16)1024.0f, (_Float16)64.0f, (_Float16)1024.0f, (_Float16)64.0f};
       const f16x8 bone = f16x8{(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
                                (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+      const int ncyc = J.wsteps / RING;
+      const bool hz = J.z != nullptr;
+      const __amdgpu_buffer_rsrc_t xr = x_rsrc(P, M);
+      float* const slot = red + wave * 16 * TNP;
+      auto cycle = [&](int cyc, auto wl) {
+        constexpr bool LOADS = decltype(wl)::value;
+        f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f}, c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+        static_for<0, RING>([&](auto scc) {
+          constexpr int st = decltype(scc)::value;
+          const f16x8 av = bitcast<f16x8>(xv[st]);
 #pragma unroll
-      for (int s = 0; s < STEPS; ++s) {
-        const f16x8 av = bitcast<f16x8>(xv[s]);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int q = t >> 2, b = t & 3;
-          u32x4 bw;
-          bw.x = w4_pair_offset(R.w[s][0][q], b);
-          bw.y = w4_pair_offset(R.w[s][1][q], b);
-          bw.z = w4_pair_offset(R.w[s][2][q], b);
-          bw.w = w4_pair_offset(R.w[s][3][q], b);
-          acc[t] = mfma_f16(av, bitcast<f16x8>(bw), acc[t]);
+          for (int t = 0; t < 8; ++t) {
+            const int qq = t >> 2, b = t & 3;
+            u32x4 bw;
+            bw.x = w4_pair_offset(R.w[st][0][qq], b);
+            bw.y = w4_pair_offset(R.w[st][1][qq], b);
+            bw.z = w4_pair_offset(R.w[st][2][qq], b);
+            bw.w = w4_pair_offset(R.w[st][3][qq], b);
+            acc[t] = mfma_f16(av, bitcast<f16x8>(bw), acc[t]);
+          }
+          c1 = mfma_f16(av, boff, c1);
+          c2 = mfma_f16(av, bone, c2);
+          if constexpr (LOADS) {
+            const int nx = RING * (cyc + 1) + st;
+            load_w_step<true>(P, k0, nsteps, nx, R.w[st]);
+            xv[st] = load_x_step(P, xr, M, true, k0, nsteps, nx);
+          }
+        });
+        float sc[8];
+        cvt_scale4(R.sraw[0], J.sdt, sc);
+        if (J.sdt == DT_F32) {
+          cvt_scale4(R.sraw[1], J.sdt, sc + 4);
+        } else {
+          const u32x4 hi = u32x4{R.sraw[0].z, R.sraw[0].w, 0u, 0u};
+          cvt_scale4(hi, J.sdt, sc + 4);
         }
-        c1 = mfma_f16(av, boff, c1);
-        c2 = mfma_f16(av, bone, c2);
-      }
-      float sc[8];
-      cvt_scale4(R.sraw[0], J.sdt, sc);
-      if (J.sdt == DT_F32) {
-        cvt_scale4(R.sraw[1], J.sdt, sc + 4);
-      } else {
-        const u32x4 hi = u32x4{R.sraw[0].z, R.sraw[0].w, 0u, 0u};
-        cvt_scale4(hi, J.sdt, sc + 4);
-      }
+        if (4 * g < R4) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const float z = (float)((R.zr[t >> 2] >> (8 * (t & 3))) & 0xFFu);
+          for (int r = 0; r < 4; ++r) {
+            f32x4* const row = (f32x4*)(slot + (4 * g + r) * TNP + j * 8);
+            f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            if (cyc > 0) o[0] = row[0], o[1] = row[1];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] = sc[t] * (acc[t][r] - fmaf(z, c2[r], c1[r]));
-      }
+            for (int t = 0; t < 8; ++t) {
+              const float z = hz ? (float)((R.zr[t >> 2] >> (8 * (t & 3))) & 0xFFu) : 8.0f;
+              const float d = acc[t][r] - fmaf(z, c2[r], c1[r]);
+              o[t >> 2][t & 3] = (cyc > 0) ? fmaf(sc[t], d, o[t >> 2][t & 3]) : sc[t] * d;
+            }
+            row[0] = o[0];
+            row[1] = o[1];
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (LOADS) load_group(P, k0, cyc + 1, R);
+      };
+      for (int cyc = 0; cyc + 1 < ncyc; ++cyc) cycle(cyc, std::integral_constant<bool, true>{});
+      cycle(ncyc - 1, std::integral_constant<bool, false>{});
     }
 
     // ---------------- workgroup sum over the 4 waves (wave order) ----------------
-    if (4 * g < R4) {
+    // (W4 waves have folded their groups into their slots already)
+    if (!W4 && 4 * g < R4) {
 #pragma unroll
       for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -543,7 +583,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Validates the jobs and computes the plan layout (and, if `jobs_out`, the descriptors).
 //
 // Unit length: each wave of a unit folds RING steps of 32 K rows (the shortest unit, KU
-// = 512 rows per unit) or, for W8 levels with many units, a multiple of that streamed
+// = 512 rows per unit) or, for levels with many units, a multiple of that streamed
 // through the ring: r = (the level's shortest units) / (kLongFactor * kPlanSlots), at
 // most a tile's whole K.  Within a level, jobs are laid out longest unit first, so the
 // queues hand out the long units early and the short ones fill the end.
@@ -595,11 +635,8 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
   std::vector<int> wsteps(njobs), order(njobs);
   for (int i = 0; i < njobs; ++i) {
     const qlin_chain_job& q = jobs[i];
-    int r = 1;
-    if (!w4_chain) {
-      const long long lr = level_units[q.level] / ((long long)kLongFactor * kPlanSlots);
-      r = (int)std::max<long long>(1, std::min<long long>(lr, (q.K + KU - 1) / KU));
-    }
+    const long long lr = level_units[q.level] / ((long long)kLongFactor * kPlanSlots);
+    const int r = (int)std::max<long long>(1, std::min<long long>(lr, (q.K + KU - 1) / KU));
     wsteps[i] = RING * r;
     order[i] = i;
   }
