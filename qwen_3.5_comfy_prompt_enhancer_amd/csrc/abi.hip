@@ -122,29 +122,52 @@ long long tiles128(const Problem& P, const SkArgs& a) {
   return t;
 }
 
-// Split count of the K order (store calls; gate/up calls are never split).  Time
-// model of the tiled int8 kernel, fitted to MI355X measurements (M = 512, W8 and W4,
-// K x N = 2048 x 2048, 6144 x 2048, 2048 x 8192, every plan forced), evaluated at the
-// engine's 512-row chunk:
-//   7 us + rounds of 256 workgroups x 128-wide K stages x 1.1 us (x 1.4 W4)
-//   + split-K exchange: 1.45 us per split + 12 ns per workgroup + 0.1 us per MB of
-//     partial tiles; a split level is tried only while the level below leaves CUs idle
+// Time models of the two kernel families for an engine call of M rows split S ways,
+// fitted to MI355X measurements (both families forced, M = 17-512, W8 and W4-g128, the
+// layer shapes 2048x2048, 6144x2048, 2048x8192 and gate/up 2048x6144, weights rotated
+// over 600 MB so they stream from HBM):
+//   tiled: 7 us + rounds of 256 workgroups x 128-wide K stages x weight sets x t_stage,
+//          t_stage = 1.05 us + 2.5 ns per workgroup in the round (W4: 1.8 us + 1.6 ns),
+//          + the split-K exchange (1.45 us per split, 12 ns per workgroup, 0.1 us per MB
+//          of partial tiles)
+//   rows:  5 us + 0.125 us (W4 0.17) per 16-row tile per million weight elements,
+//          + 1.45 us per split
+// t_tiled is negative where the tiled kernel does not cover the call.
+void engine_times(const Problem& P, const SkArgs& a, int M, int S, double* t_tiled, double* t_rows) {
+  const int nb = P.K / 64;
+  *t_tiled = -1.0;
+  SkArgs probe = a;
+  probe.M = M;
+  if (prefill_i8_ok(probe, P.wk, P.epi)) {
+    const long long tiles = (long long)((M + 127) / 128) * tiles128(P, a);
+    const long long wgs = tiles * S;
+    const double occ = (double)std::min<long long>(wgs, 256);
+    const double t_stage = (P.wk == WK_W4 ? 1.8e-6 + 1.6e-9 * occ : 1.05e-6 + 2.5e-9 * occ) * P.nsets;
+    double t = 7e-6 + (double)((wgs + 255) / 256) * ((nb / S + 1) / 2) * t_stage;
+    if (S > 1) t += 1.45e-6 * S + 12e-9 * wgs + 0.1e-12 * (double)wgs * P.nsets * 128 * 128 * sizeof(float);
+    *t_tiled = t;
+  }
+  const double elems = (double)P.K * P.ncols * P.nsets / 1e6;
+  *t_rows = 5e-6 + (P.wk == WK_W4 ? 0.17e-6 : 0.125e-6) * ((M + 15) / 16) * elems + (S > 1 ? 1.45e-6 * S : 0.0);
+}
+
+// Split count of the K order: the S (1, 2, 4 or 8, dividing K into ranges of at least
+// two 64-wide blocks) whose faster family is fastest at the engine's 512-row chunk.
 // QLIN_ENGINE_SPLITS overrides it (tuning; it changes the K order).
 int engine_splits(const Problem& P, const SkArgs& a) {
-  if (P.epi != EPI_STORE) return 1;
   const int nb = P.K / 64;
   const char* es = getenv("QLIN_ENGINE_SPLITS");
   if (es && *es) return atoi(es);
-  const long long tiles = (long long)((kRefChunkM + 127) / 128) * tiles128(P, a);
-  const double t_stage = (P.wk == WK_W4 ? 1.4 : 1.0) * 1.1e-6;
-  double best = 7e-6 + (double)((tiles + 255) / 256) * ((nb + 1) / 2) * t_stage;
+  double best = 0.0;
   int S = 1;
-  for (int s = 2; s <= 8; s *= 2) {
-    if (nb % s != 0 || nb / s < 2 || tiles * (s / 2) >= 256) break;
-    const long long wgs = tiles * s;
-    const double t = 7e-6 + (double)((wgs + 255) / 256) * ((nb / s + 1) / 2) * t_stage + 1.45e-6 * s +
-                     12e-9 * wgs + 0.1e-12 * (double)wgs * 128 * 128 * sizeof(float);
-    if (t < best) best = t, S = s;
+  SkArgs b = a;
+  b.x = nullptr;  // the choice must not depend on where the activations sit
+  for (int s = 1; s <= 8; s *= 2) {
+    if (nb % s != 0 || (s > 1 && nb / s < 2)) break;
+    double tt, tr;
+    engine_times(P, b, kRefChunkM, s, &tt, &tr);
+    const double t = (tt >= 0.0 && tt < tr) ? tt : tr;
+    if (s == 1 || t < best) best = t, S = s;
   }
   return S;
 }
@@ -214,33 +237,17 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
   const int nb = P.K / 64;
   if (S < 1 || S > 64 || nb % S != 0 || (S > 1 && nb / S < 2))
     return fail(QLIN_ERR_UNSUPPORTED, "%s: %d K splits do not divide K=%d into ranges of at least 128", fn, S, P.K);
-  if (P.epi != EPI_STORE && S != 1) return fail(QLIN_ERR_UNSUPPORTED, "%s: gate/up calls are not split", fn);
   // family: the tiled int8 kernel where it applies and a time model prefers it to the
   // 16-row tiles; both give the same bits.  QLIN_ENGINE_PREFILL=tiled|skinny forces one.
   const char* e = getenv("QLIN_ENGINE_PREFILL");
   const bool force_rows = e && strcmp(e, "skinny") == 0;
   const bool force_tiled = e && strcmp(e, "tiled") == 0;
-  // Time models fitted to MI355X measurements (both families forced, M = 17-512, W8
-  // and W4-g128, the layer shapes 2048x2048, 6144x2048, 2048x8192 and gate/up
-  // 2048x6144, weights rotated over 600 MB so they stream from HBM):
-  //   tiled: 7 us + rounds of 256 workgroups x 128-wide K stages x weight sets x
-  //          t_stage, t_stage = 1.05 us + 2.5 ns per workgroup in the round (W4:
-  //          1.8 us + 1.6 ns), + the split-K exchange (1.45 us per split, 12 ns per
-  //          workgroup, 0.1 us per MB of partial tiles)
-  //   rows:  5 us + 0.125 us (W4 0.17) per 16-row tile per million weight elements,
-  //          + 1.45 us per split
+  // time models of the two families (engine_times) at this M
   bool tiled = false;
-  if (prefill_i8_ok(a, P.wk, P.epi) && !force_rows) {
-    const long long tiles = (long long)((P.M + 127) / 128) * tiles128(P, a);
-    const long long wgs = tiles * S;
-    const double occ = (double)std::min<long long>(wgs, 256);
-    const double t_stage = (P.wk == WK_W4 ? 1.8e-6 + 1.6e-9 * occ : 1.05e-6 + 2.5e-9 * occ) * P.nsets;
-    double t_tiled = 7e-6 + (double)((wgs + 255) / 256) * ((nb / S + 1) / 2) * t_stage;
-    if (S > 1) t_tiled += 1.45e-6 * S + 12e-9 * wgs + 0.1e-12 * (double)wgs * 128 * 128 * sizeof(float);
-    const double elems = (double)P.K * P.ncols * P.nsets / 1e6;
-    const double t_rows = 5e-6 + (P.wk == WK_W4 ? 0.17e-6 : 0.125e-6) * ((P.M + 15) / 16) * elems +
-                          (S > 1 ? 1.45e-6 * S : 0.0);
-    tiled = force_tiled || t_tiled < t_rows;
+  if (!force_rows) {
+    double t_tiled, t_rows;
+    engine_times(P, a, P.M, S, &t_tiled, &t_rows);
+    tiled = t_tiled >= 0.0 && (force_tiled || t_tiled < t_rows);
   }
   // the tiled kernel has no producer prologue: make the activations first
   if (tiled && a.pro.kind != PRO_NONE) QL_TRY(pro_materialize(fn, a, stream));
@@ -274,6 +281,7 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
     b.part = S > 1 ? (float*)((char*)workspace + kCounterBytes) : nullptr;
     hipError_t err;
     if (tiled) {
+      if (!b.x || !b.xs) return fail(QLIN_ERR_INVALID, "%s: internal error: no activations for the tiled kernel", fn);
       err = launch_prefill_i8(b, P.wk, P.hz, P.epi, stream);
     } else {
       SkLaunch L;
@@ -299,6 +307,7 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
       const int rg0 = ((rows < 16 ? rows : 16) + 3) / 4;
       L.lds = ((size_t)L.waves * P.nsets * rg0 * 4 * (TN + 4) + (size_t)P.nsets * TN) * sizeof(float);
       if (b.pro.kind != PRO_NONE && !pro_plan(L, b, P.K, rows)) QL_TRY(pro_materialize(fn, b, stream));
+      if (!L.pro && (!b.x || !b.xs)) return fail(QLIN_ERR_INVALID, "%s: internal error: no activations", fn);
       err = launch_skinny(L, b, stream);
     }
     if (err != hipSuccess) return hip_status(fn, err);
@@ -425,6 +434,9 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   // activation producer: fused into the prologue of narrow plans; wide plans (every
   // workgroup would redo the whole row) make the activations with a launch of their own
   if (a.pro.kind != PRO_NONE && (wide || !pro_plan(L, a, P.K, P.M))) QL_TRY(pro_materialize(fn, a, stream));
+  // every launch reads its activations from memory unless its prologue makes them
+  if (!L.pro && (!a.x || (P.act == ACT_I8 && !a.xs)))
+    return fail(QLIN_ERR_INVALID, "%s: internal error: no activations", fn);
   if (clear && splits > 1) QL_TRY(hip_status(fn, clear_counters(workspace, (long long)rtiles * ntiles, stream)));
   return hip_status(fn, launch_skinny(L, a, stream));
 }

@@ -27,9 +27,10 @@
 //     explicit zeros add (8 - z) * sum(a) from one more MFMA against all-ones.
 //   * Copies: global -> registers (three stages ahead, two for gate/up) -> LDS (one
 //     stage ahead), one barrier per stage.
-//   * Split-K (store epilogue): `splits` workgroups per tile over equal ranges of
-//     64-wide blocks; each stores its fp32 partial (device-coherent) and counts its
-//     arrival, and the last to arrive sums the partials in split order.
+//   * Split-K: `splits` workgroups per tile over equal ranges of 64-wide blocks; each
+//     stores its fp32 partial tile (both weight sets for gate/up; device-coherent) and
+//     counts its arrival, and the last to arrive sums the partials in split order and
+//     runs the epilogue.
 //   * The K order of every output element is fixed (blocks in order within each K
 //     group, then group 0 + group 1, then splits in order), so rows do not depend on M
 //     or on the chunking for a given split count.
@@ -87,9 +88,9 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   const int j = lane & 15, g = lane >> 4;
   const int kg = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
   const int M = a.M, K = a.K;
-  // split-K (store epilogue): `S` workgroups per output tile, each over nk
-  // consecutive 64-wide blocks from kb0
-  const int S = (EPI == EPI_STORE) ? a.splits : 1;
+  // split-K: `S` workgroups per output tile, each over nk consecutive 64-wide blocks
+  // from kb0
+  const int S = a.splits;
   const int tile = (int)blockIdx.x / S, split = (int)blockIdx.x % S;
   const int nk = K / 64 / S;
   const int kb0 = split * nk;
@@ -373,45 +374,50 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
           for (int r = 0; r < 4; ++r) acc[s][rb][t][r] += red[((rb * 4 + t) * 4 + r) * 64];
     }
   }
-  if constexpr (EPI == EPI_STORE) {
-    if (S > 1) {
-      // Split-K: group 0's partial tile (wave w: the float4 (rb, t) of every lane at
-      // byte ((rb * 4 + t) * 64 + lane) * 16 of its 16 KB slot) goes out through
-      // device-coherent stores; each workgroup's stores complete before it counts its
-      // arrival, and the last to arrive sums the partials in split order.
-      __shared__ int s_last;
-      constexpr unsigned kSlot = 64u * 64u * 4u;
-      const __amdgpu_buffer_rsrc_t rs =
-          part_rsrc(a.part + (long long)tile * S * 4 * (64 * 64), (unsigned)(S * 4) * kSlot);
-      const unsigned lane_off = (unsigned)lane * 16u;
-      if (kg == 0) {
-        const unsigned base = (unsigned)(split * 4 + (wave & 3)) * kSlot + lane_off;
+  if (S > 1) {
+    // Split-K: group 0's partial tile of each weight set (wave w: the float4 (rb, t) of
+    // every lane at byte ((rb * 4 + t) * 64 + lane) * 16 of its 16 KB slot, slots
+    // [split][set][wave]) goes out through device-coherent stores; each workgroup's
+    // stores complete before it counts its arrival, and the last to arrive sums the
+    // partials in split order.
+    __shared__ int s_last;
+    constexpr unsigned kSlot = 64u * 64u * 4u;
+    const __amdgpu_buffer_rsrc_t rs =
+        part_rsrc(a.part + (long long)tile * S * NS * 4 * (64 * 64), (unsigned)(S * NS * 4) * kSlot);
+    const unsigned lane_off = (unsigned)lane * 16u;
+    if (kg == 0) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const unsigned base = (unsigned)((split * NS + s) * 4 + (wave & 3)) * kSlot + lane_off;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) st_coherent(acc[0][rb][t], rs, base + (unsigned)(rb * 4 + t) * 1024u);
+          for (int t = 0; t < 4; ++t) st_coherent(acc[s][rb][t], rs, base + (unsigned)(rb * 4 + t) * 1024u);
       }
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __syncthreads();
-      if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = prev == (unsigned)(S - 1);
-        if (last) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-      }
-      __syncthreads();
-      if (!s_last || kg != 0) return;  // uniform over each wave
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      for (int sp = 0; sp < S; ++sp) {
-        const unsigned base = (unsigned)(sp * 4 + (wave & 3)) * kSlot + lane_off;
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave has completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev == (unsigned)(S - 1);
+      if (last) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last || kg != 0) return;  // uniform over each wave
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    for (int sp = 0; sp < S; ++sp) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const unsigned base = (unsigned)((sp * NS + s) * 4 + (wave & 3)) * kSlot + lane_off;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const f32x4 v = ld_coherent(rs, base + (unsigned)(rb * 4 + t) * 1024u);
-            acc[0][rb][t] = (sp == 0) ? v : acc[0][rb][t] + v;
+            acc[s][rb][t] = (sp == 0) ? v : acc[s][rb][t] + v;
           }
       }
     }
@@ -565,7 +571,7 @@ hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t st)
     tn = a.seg[0].n / BN;
   }
   a.ntiles = tn;
-  if (epi != EPI_STORE || a.splits < 1) a.splits = 1;  // split-K: store epilogue only
+  if (a.splits < 1) a.splits = 1;
   const int tiles = ((a.M + BM - 1) / BM) * tn * a.splits;
   switch (epi) {
     case EPI_STORE: return launch_i8_e<EPI_STORE>(a, wk, hz, tiles, st);

@@ -457,6 +457,37 @@ def test_mlp_gate_up_quant_w4_prefill_tiled(zeros, group, tiled):
     _fused_vs_unfused(96, w4_=True, zeros=zeros, group=group)
 
 
+@pytest.mark.parametrize("splits", [2, 4])
+@pytest.mark.parametrize("w4_,zeros,group", [(False, "none", 128), (True, "random", 128)])
+def test_mlp_gate_up_quant_prefill_tiled_split_k(splits, w4_, zeros, group, tiled):
+    """Split-K on the tiled kernel's gate/up epilogue: each split stores both weight
+    sets' partials and the last to arrive sums them in split order before silu(g) * u
+    and the requantization -- bit-identical to quantizing its own bf16 h, within
+    tolerance of the oracle."""
+    tiled.setenv("QLIN_ENGINE_SPLITS", str(splits))
+    _fused_vs_unfused(200, w4_=w4_, zeros=zeros, group=group)
+
+
+@pytest.mark.parametrize("splits", [1, 2])
+def test_gate_up_quant_tiled_matches_row_tiles(splits, tiled):
+    """gate/up + requant: the tiled kernel and the 16-row tiles give identical codes and
+    scales for the same split count (the K order depends on the split count only)."""
+    gemm, _ = _g()
+    M, K, N = 96, 2048, 1280
+    a, as_ = H.engine_act(M, K, seed=450)
+    (wg, sg), (wu, su) = H.engine_w8(K, N, seed=451), H.engine_w8(K, N, seed=452)
+    cu = lambda t: t.cuda()
+    tiled.setenv("QLIN_ENGINE_SPLITS", str(splits))
+    out = []
+    for fam in ("tiled", "skinny"):
+        tiled.setenv("QLIN_ENGINE_PREFILL", fam)
+        q = torch.empty((M, N), dtype=torch.int8, device="cuda")
+        s = torch.empty((M, N // 64), dtype=torch.float32, device="cuda")
+        gemm.mlp_gate_up_quant(cu(a), cu(as_), cu(wg), cu(sg), cu(wu), cu(su), q, s)
+        out.append((q.cpu(), s.cpu()))
+    assert torch.equal(out[0][0], out[1][0]) and torch.equal(out[0][1], out[1][1])
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 2048, 6144), (4, 2048, 6144), (512, 2048, 6144), (512, 6144, 2048)])
 def test_engine_scale_property_full_size(M, K, N):
     """Doubling the per-64 activation scales doubles every bf16 output exactly (the
