@@ -209,7 +209,11 @@ int pro_materialize(const char* fn, SkArgs& a, hipStream_t stream) {
 
 // Fused prologue for a skinny launch plan: places the code block of the workgroup's
 // rows and K range after the finish layout in dynamic LDS.  False when the plan has
-// no fused instantiation or the block does not fit (the caller then materializes).
+// no fused instantiation, the block does not fit, or the prologue would hold each
+// thread for more than kProItems values (every column tile of a row tile makes the
+// same codes: cheap for decode's short K ranges, slower than one producer launch for
+// 16-row tiles over long ones); the caller then makes the codes with their own launch.
+constexpr long long kProItems = 32;
 bool pro_plan(SkLaunch& L, SkArgs& a, int K, int rows) {
   L.pro = 1;
   if (!skinny_pro_ok(L, a.group)) {
@@ -218,6 +222,11 @@ bool pro_plan(SkLaunch& L, SkArgs& a, int K, int rows) {
   }
   const int kr = (a.lanes == 2) ? a.kchunk : std::min(K, L.waves * a.kchunk);
   const int mt = std::min(16, rows);
+  const long long work = (long long)mt * kr + (a.pro.kind == PRO_RMSNORM ? (long long)mt * K : 0);
+  if (work > kProItems * 64 * L.waves) {
+    L.pro = 0;
+    return false;
+  }
   const size_t off = (L.lds + 15) & ~(size_t)15;
   const int ldq = kr + 16;  // 16 bytes of padding staggers the rows over the LDS banks
   const size_t bytes = (size_t)mt * ldq + (size_t)mt * (kr / 64) * sizeof(float) + (size_t)mt * sizeof(float);
