@@ -37,11 +37,16 @@ CFLAGS = [
 ]
 
 
-# Per-source flags.  prefill.hip keeps its 128 fp32 accumulators per lane in
+# Per-source flags.  The A16 prefill kernel (prefill_kernel.h, instantiated by
+# prefill.hip and prefill_w4_*.hip) keeps its 128 fp32 accumulators per lane in
 # architectural VGPRs (the VGPR form of MFMA): with accumulation registers the
 # compiler rotates the loop-carried accumulators through copies every K tile.
+_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 EXTRA = {
-    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "prefill.hip": _VGPR_FORM,
+    "prefill_w4_f16.hip": _VGPR_FORM,
+    "prefill_w4_bf16.hip": _VGPR_FORM,
+    "prefill_w4_f32.hip": _VGPR_FORM,
 }
 
 

@@ -301,7 +301,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     int nxt = 0;
     if (tid == 0) nxt = (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kQueues + q;
     const ChainJob& J = P.J;
-    const int K = J.K, N = J.N, S = J.splits, tile = P.tile, split = P.split;
+    const int N = J.N, S = J.splits, tile = P.tile, split = P.split;
     int k0, nsteps;
     wave_range<W4>(P, &k0, &nsteps);
 
