@@ -327,6 +327,25 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     // ---------------- activations of a dependent unit, read after its wait ----------------
     if (J.level > 0) load_x<W4>(P, M, true, xv);
 
+    // The next unit is made known before this unit's last ring cycle (its index was
+    // fetched at this unit's start, so that atomic's latency is hidden), and the last
+    // cycle refills each ring slot with the next unit's step as soon as the slot's
+    // MFMAs are issued: the wave's loads stay in flight across the unit boundary,
+    // under this unit's fold, sum, exchange and epilogue.  Past the last unit the
+    // loads re-read this unit's first steps (lines the caches hold), so they need no
+    // branch.
+    int un = 0, k0n = 0, nstepsn = 0;
+    bool xn_now = false;
+    UnitPos Pn;
+    auto publish_next = [&]() {
+      if (tid == 0) s_unit = nxt;
+      __syncthreads();
+      un = (int)__builtin_amdgcn_readfirstlane((uint32_t)s_unit);
+      Pn = decode_unit(jobs, unit_job, un < H.nunits ? un : u);  // past the end: this unit
+      xn_now = un < H.nunits && Pn.J.level == 0;
+      wave_range<W4>(Pn, &k0n, &nstepsn);
+    };
+
     // ---------------- MFMA ----------------
     f32x4 acc[8];
 #pragma unroll
@@ -346,8 +365,14 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           xv[s] = load_x_step(P, xr, M, true, k0, nsteps, nx);
         });
       }
+      publish_next();
+      const __amdgpu_buffer_rsrc_t xrn = x_rsrc(Pn, M);
 #pragma unroll
-      for (int s = 0; s < STEPS; ++s) w8_step(R.w[s], xv[s], acc);
+      for (int s = 0; s < STEPS; ++s) {
+        w8_step(R.w[s], xv[s], acc);
+        load_w_step<false>(Pn, k0n, nstepsn, s, R.w[s]);
+        xv[s] = load_x_step(Pn, xrn, M, xn_now, k0n, nstepsn, s);
+      }
     } else {
       // (1024 + lo, 64 + hi) operands.  One ring cycle of RING steps is one group of
       // 128; at its end the group folds scale * (acc - (c1 + z c2)) into the wave's LDS
@@ -360,9 +385,11 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
       const int ncyc = J.wsteps / RING;
       const bool hz = J.z != nullptr;
       const __amdgpu_buffer_rsrc_t xr = x_rsrc(P, M);
+      __amdgpu_buffer_rsrc_t xrn = xr;
       float* const slot = red + wave * 16 * TNP;
+      // wl: 1 = refill with this unit's next steps, 2 = with the next unit's first steps
       auto cycle = [&](int cyc, auto wl) {
-        constexpr bool LOADS = decltype(wl)::value;
+        constexpr int LOADS = decltype(wl)::value;
         f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f}, c2 = f32x4{0.f, 0.f, 0.f, 0.f};
         static_for<0, RING>([&](auto scc) {
           constexpr int st = decltype(scc)::value;
@@ -379,10 +406,13 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           }
           c1 = mfma_f16(av, boff, c1);
           c2 = mfma_f16(av, bone, c2);
-          if constexpr (LOADS) {
+          if constexpr (LOADS == 1) {
             const int nx = RING * (cyc + 1) + st;
             load_w_step<true>(P, k0, nsteps, nx, R.w[st]);
             xv[st] = load_x_step(P, xr, M, true, k0, nsteps, nx);
+          } else {
+            load_w_step<true>(Pn, k0n, nstepsn, st, R.w[st]);
+            xv[st] = load_x_step(Pn, xrn, M, xn_now, k0n, nstepsn, st);
           }
         });
         float sc[8];
@@ -411,10 +441,13 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (LOADS) load_group(P, k0, cyc + 1, R);
+        if constexpr (LOADS == 1) load_group(P, k0, cyc + 1, R);
+        else load_group(Pn, k0n, 0, R);
       };
-      for (int cyc = 0; cyc + 1 < ncyc; ++cyc) cycle(cyc, std::integral_constant<bool, true>{});
-      cycle(ncyc - 1, std::integral_constant<bool, false>{});
+      for (int cyc = 0; cyc + 1 < ncyc; ++cyc) cycle(cyc, std::integral_constant<int, 1>{});
+      publish_next();
+      xrn = x_rsrc(Pn, M);
+      cycle(ncyc - 1, std::integral_constant<int, 2>{});
     }
 
     // ---------------- workgroup sum over the 4 waves (wave order) ----------------
@@ -451,17 +484,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
       __builtin_amdgcn_s_waitcnt(0);  // every partial store of this thread has completed
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
-    if (tid == 0) s_unit = (int)nxt;
-    __syncthreads();
-
-    // ---------------- the next unit's weights go out now (its registers are free) ----------------
-    const int un = s_unit;
-    UnitPos Pn;
-    if (un < H.nunits) {
-      Pn = decode_unit(jobs, unit_job, un);
-      issue_loads<W4>(Pn, R);
-      load_x<W4>(Pn, M, Pn.J.level == 0, xv);
-    }
+    __syncthreads();  // (split-K: every partial store of the workgroup has completed)
 
     // ---------------- split-K: the last unit of a tile to arrive sums the splits in order ----------------
     bool finish = true;
