@@ -160,8 +160,9 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
                     ch.add(xin(M, K), lw[l][i].w, lw[l][i].s, outs[M][i], level=lvl)
                 if shapes and args.levels == "layer":
                     base += LEVELS_PER_LAYER
-            ch.add(xin(M, head[1]), hw.w, hw.s, hout[M],
-                   level=(base if shapes and args.levels == "layer" else 0))
+            if args.head == "chain":
+                ch.add(xin(M, head[1]), hw.w, hw.s, hout[M],
+                       level=(base if shapes and args.levels == "layer" else 0))
             ch.build()
             chains[M] = ch
         for M in ms:
@@ -169,6 +170,14 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
         torch.cuda.synchronize()
         ev = {M: [] for M in ms}
         record = {"on": False}
+
+        # with --head own the vocabulary head follows the chain as its own launch on the
+        # same stream (the wide GEMV plan; the stream order is its dependency)
+        head_own = args.head == "own"
+        if head_own:
+            for M in ms:
+                hw.run(lin, xin(M, head[1]), hout[M])
+            torch.cuda.synchronize()
 
         def step():
             for M in ms:
@@ -181,8 +190,11 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
                     ev[M].append((e0, e1))
                 else:
                     chains[M].run()
+                if head_own:
+                    hw.run(lin, xin(M, head[1]), hout[M])
 
-        step_bytes = {M: (layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0) + hw.nbytes(M) for M in ms}
+        step_bytes = {M: (layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0)
+                      + (0 if head_own else hw.nbytes(M)) for M in ms}
         return total, step, ev, step_bytes, record, (lw, hw, xs, outs, hout, lin, chains)
 
     # eager warm-up (allocates the workspace outside capture), then capture per M
@@ -650,13 +662,14 @@ def prefill_pmc(args):
 
 
 def decode_pmc(args):
-    """For `rocprofv3 --pmc` runs: `--steps` launches of the W8 decode chain (every
-    linear of 8 layer copies of the 2B-class layer plus the vocab head, M = 1,
-    dependency levels per `--levels`) and the same 1 GiB device copy as the
-    calibration of the byte counters."""
+    """For `rocprofv3 --pmc` runs: `--steps` launches of the decode chain of
+    `--pmc-kind` weights (every linear of 8 layer copies of the 2B-class layer, plus the
+    vocab head unless `--head own` gives it a launch of its own, M = 1, dependency
+    levels per `--levels`) and the same 1 GiB device copy as the calibration of the
+    byte counters."""
     import torch
     args.launch = "chain"
-    total, step, ev, step_bytes, record, ctx = decode_sweep(args, "w8", LAYER_SHAPES, HEAD, [1], args.layers)
+    total, step, ev, step_bytes, record, ctx = decode_sweep(args, args.pmc_kind, LAYER_SHAPES, HEAD, [1], args.layers)
     for _ in range(args.steps):
         step()
     a = torch.empty(1 << 30, dtype=torch.uint8, device=torch.device("cuda", 0))
@@ -664,7 +677,8 @@ def decode_pmc(args):
     for _ in range(2):
         b.copy_(a)
     torch.cuda.synchronize()
-    print(json.dumps({"workload": "decode-pmc", "levels": args.levels, "bytes_per_launch": step_bytes[1],
+    print(json.dumps({"workload": "decode-pmc", "kind": args.pmc_kind, "head": args.head,
+                      "levels": args.levels, "bytes_per_launch": step_bytes[1],
                       "copy_bytes": 1 << 30}), flush=True)
     return 0
 
@@ -747,6 +761,11 @@ def main() -> int:
     ap.add_argument("--levels", default=None, choices=["layer", "flat"],
                     help="chain dependency levels: per decode layer, or all independent (default: flat for "
                          "the decode sweeps, whose shapes are independent; layer for the 9B-class decode chain)")
+    ap.add_argument("--head", default=None, choices=["chain", "own"],
+                    help="chain launches: the vocabulary head inside the chain launch, or as its own launch "
+                         "(the wide GEMV plan) after it (default: own for the W4 workloads, chain for W8, "
+                         "whichever measured faster)")
+    ap.add_argument("--pmc-kind", default="w8", choices=["w8", "w4"], help="decode-pmc: weight format")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--detail", action="store_true", help="per-shape table on stderr")
@@ -766,6 +785,9 @@ def main() -> int:
         return 1
 
     wl = args.workload
+    if args.head is None:
+        w4 = wl in ("decode-w4", "chain-w4") or (wl == "decode-pmc" and args.pmc_kind == "w4")
+        args.head = "own" if w4 else "chain"
     if wl == "head-pmc":
         return head_pmc(args)
     if wl == "prefill-pmc":
@@ -802,8 +824,11 @@ def main() -> int:
         achieved = hb / dur / 1e9
         if args.launch == "chain":
             tag = f"chain-{kind}-{wl}"
-            kname = (f"chain_kernel {kind}: {layers} layer copies x {len(shapes)} linears + vocab head "
-                     f"{head[1]}x{head[2]}, {args.levels} levels, M={'/'.join(map(str, ms))}")
+            kname = (f"chain_kernel {kind}: {layers} layer copies x {len(shapes)} linears"
+                     + (f" + vocab head {head[1]}x{head[2]}" if args.head == "chain" else "")
+                     + f", {args.levels} levels, M={'/'.join(map(str, ms))}")
+            if args.head == "own":
+                tag += "-layers"
         else:
             tag = f"{kind}-{head[1]}x{head[2]}"
             kname = f"skinny_kernel {kind} vocab head {head[1]}x{head[2]}, M={'/'.join(map(str, ms))}"
@@ -839,7 +864,8 @@ def main() -> int:
                   "rows_M": ms, "layer_copies": layers,
                   "shapes_KN": [[K, N] for (_, K, N) in shapes] + [[head[1], head[2]]],
                   "bytes_per_step": total,
-                  "launch": ({"chain": f"one persistent chain launch per M ({args.levels} dependency levels)",
+                  "launch": ({"chain": f"one persistent chain launch per M ({args.levels} dependency levels)"
+                                       + ("" if args.head == "chain" else ", then the vocab head as its own launch"),
                               "graph": "hipgraph per M for layer shapes, eager vocab head"}[args.launch]
                              if not args.no_graph else "eager")}
         if other is not None:

@@ -332,8 +332,9 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     // cycle refills each ring slot with the next unit's step as soon as the slot's
     // MFMAs are issued: the wave's loads stay in flight across the unit boundary,
     // under this unit's fold, sum, exchange and epilogue.  Past the last unit the
-    // loads re-read this unit's first steps (lines the caches hold), so they need no
-    // branch.
+    // loads need no branch either: they all read the first rows of tile 0 of this
+    // unit's job, a few KB that every workgroup shares in L2 (re-reading this unit's
+    // own first steps instead, long evicted, cost 10 % more HBM reads).
     int un = 0, k0n = 0, nstepsn = 0;
     bool xn_now = false;
     UnitPos Pn;
@@ -341,9 +342,12 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
       if (tid == 0) s_unit = nxt;
       __syncthreads();
       un = (int)__builtin_amdgcn_readfirstlane((uint32_t)s_unit);
-      Pn = decode_unit(jobs, unit_job, un < H.nunits ? un : u);  // past the end: this unit
-      xn_now = un < H.nunits && Pn.J.level == 0;
+      const bool more = un < H.nunits;  // uniform
+      Pn = decode_unit(jobs, unit_job, more ? un : u);
+      if (!more) Pn.tile = 0, Pn.split = 0;
+      xn_now = more && Pn.J.level == 0;
       wave_range<W4>(Pn, &k0n, &nstepsn);
+      if (!more) k0n = 0, nstepsn = 0;
     };
 
     // ---------------- MFMA ----------------
@@ -424,19 +428,26 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           cvt_scale4(hi, J.sdt, sc + 4);
         }
         if (4 * g < R4) {
+          float zf[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) zf[t] = hz ? (float)((R.zr[t >> 2] >> (8 * (t & 3))) & 0xFFu) : 8.0f;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            f32x4* const row = (f32x4*)(slot + (4 * g + r) * TNP + j * 8);
-            f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-            if (cyc > 0) o[0] = row[0], o[1] = row[1];
+            // only the rows below M: the sum never reads the others (most of the fold's
+            // instructions at M = 1)
+            if (4 * g + r < M) {
+              f32x4* const row = (f32x4*)(slot + (4 * g + r) * TNP + j * 8);
+              f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+              if (cyc > 0) o[0] = row[0], o[1] = row[1];
+              // the first group: fma with a zero addend, the product rounded once
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              const float z = hz ? (float)((R.zr[t >> 2] >> (8 * (t & 3))) & 0xFFu) : 8.0f;
-              const float d = acc[t][r] - fmaf(z, c2[r], c1[r]);
-              o[t >> 2][t & 3] = (cyc > 0) ? fmaf(sc[t], d, o[t >> 2][t & 3]) : sc[t] * d;
+              for (int t = 0; t < 8; ++t) {
+                const float d = acc[t][r] - fmaf(zf[t], c2[r], c1[r]);
+                o[t >> 2][t & 3] = fmaf(sc[t], d, o[t >> 2][t & 3]);
+              }
+              row[0] = o[0];
+              row[1] = o[1];
             }
-            row[0] = o[0];
-            row[1] = o[1];
           }
         }
 #pragma unroll
