@@ -565,17 +565,22 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           }
         }
       }
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_waitcnt(0);  // the tile's output has reached the coherence point
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __syncthreads();
-      if (tid == 0) {
-        // the tile counts for its level; the level's last tile sets the level's flag (one
-        // atomic on the critical path between levels)
-        const unsigned pl =
-            __hip_atomic_fetch_add(cnt + kLevel0 + 32 * J.level, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (pl + 1 == need[J.level])
-          __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // The tile counts for its level; the level's last tile sets the level's flag (one
+      // atomic on the critical path between levels).  The last level has no reader of its
+      // flag (the kernel's end publishes its outputs), so its tiles skip the count and the
+      // wait for their stores, which on this hardware also waits for the next unit's
+      // ring loads issued before them.
+      if (J.level + 1 < H.nlevels) {  // uniform
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);  // the tile's output has reached the coherence point
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (tid == 0) {
+          const unsigned pl =
+              __hip_atomic_fetch_add(cnt + kLevel0 + 32 * J.level, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (pl + 1 == need[J.level])
+            __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
     __syncthreads();  // every thread is done with red, s_unit and s_flag of this unit
