@@ -174,10 +174,32 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
         # with --head own the vocabulary head follows the chain as its own launch on the
         # same stream (the wide GEMV plan; the stream order is its dependency)
         head_own = args.head == "own"
+        head_graphs = {}
         if head_own:
+            # warm-up (allocates the workspace outside capture), then one HIP graph per M:
+            # replaying it costs the host one call, so the GPU does not wait for the host
+            # between the chain and the head
             for M in ms:
                 hw.run(lin, xin(M, head[1]), hout[M])
             torch.cuda.synchronize()
+            for M in ms:
+                gh = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gh):
+                    hw.run(lin, xin(M, head[1]), hout[M])
+                head_graphs[M] = gh
+            torch.cuda.synchronize()
+
+        # each chain's launch bound once (library function, plan pointer, stream), so
+        # the event interval around a launch holds no Python work beyond the call
+        from qwen35_amd.kernels import qlin as C
+        launch = {M: (C.lib().qlin_chain_run, chains[M].plan.data_ptr(), torch.cuda.current_stream().cuda_stream)
+                  for M in ms}
+
+        def run_chain(M):
+            fn, plan, stream = launch[M]
+            rc = fn(plan, stream)
+            if rc != 0:
+                C.check(rc, "qlin_chain_run")
 
         def step():
             for M in ms:
@@ -185,13 +207,13 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
                     e0 = torch.cuda.Event(enable_timing=True)
                     e1 = torch.cuda.Event(enable_timing=True)
                     e0.record()
-                    chains[M].run()
+                    run_chain(M)
                     e1.record()
                     ev[M].append((e0, e1))
                 else:
-                    chains[M].run()
+                    run_chain(M)
                 if head_own:
-                    hw.run(lin, xin(M, head[1]), hout[M])
+                    head_graphs[M].replay()
 
         step_bytes = {M: (layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0)
                       + (0 if head_own else hw.nbytes(M)) for M in ms}
