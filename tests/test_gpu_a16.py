@@ -416,10 +416,12 @@ def test_prefill_w8(M, K, N, shape, monkeypatch):
 @pytest.mark.parametrize("shape", [0, 1, 2])
 @pytest.mark.parametrize("M", [40, 256])
 @pytest.mark.parametrize("group,zeros,sdt", [(128, "none", torch.float16), (32, "random", torch.float16),
-                                             (64, "random", torch.bfloat16), (128, "eight", torch.float32)])
+                                             (64, "random", torch.bfloat16), (128, "eight", torch.float32),
+                                             (128, "none", torch.bfloat16), (64, "none", torch.float32)])
 def test_prefill_w4(M, group, zeros, sdt, shape, monkeypatch):
     """W4 prefill folds the group scale into the fp16 weight (one fp16 rounding per
-    weight), so it is held to the GEMM tolerance, not bit-exactness."""
+    weight), so it is held to the GEMM tolerance, not bit-exactness.  The kernels are
+    built per scale dtype, each with and without a zeros tensor: all six are run."""
     _force_tiled(monkeypatch, shape)
     K, N = 1024, 1280
     x = H.act_f16(M, K, seed=310 + M)
