@@ -786,6 +786,32 @@ PfPlan plan_prefill(int wk, int M, int K, int N, size_t part_cap) {
   return best;
 }
 
+// Tile order of a plan with one tile per workgroup (or its K splits): each XCD runs one
+// contiguous eighth of the order, and the order goes down gm row tiles before the next
+// column tile, so an XCD's run covers about gm row tiles x (run / gm) column tiles.
+// gm minimises what one run reads into its XCD's L2: rows x (BM x K fp16 activations)
+// + columns x (the weights of BN columns).  QLIN_PREFILL_GM overrides it (0: the order
+// in groups of 8 row tiles with workgroups in launch order).
+int prefill_tile_group(int wk, int M, int K, int N, int shape) {
+  const char* e = getenv("QLIN_PREFILL_GM");
+  if (e && *e) return std::max(0, atoi(e));
+  int bm, bn, waves;
+  prefill_geometry(shape, &bm, &bn, &waves);
+  const long long tm = (M + bm - 1) / bm, tn = (N + bn - 1) / bn;
+  const long long run = std::max<long long>(1, (tm * tn + 7) / 8);
+  const double arow = (double)bm * K * 2.0, wcol = (double)K * bn * (wk == WK_W4 ? 0.5 : 1.0);
+  int best = 1;
+  double best_c = 0.0;
+  for (int gm = 1; gm <= 64; gm *= 2) {
+    const long long h = std::min<long long>(gm, tm);
+    const long long rows = std::min(h, run), cols = (run + h - 1) / h;
+    const double c = (double)rows * arow + (double)cols * wcol;
+    if (gm == 1 || c < best_c) best_c = c, best = gm;
+    if (gm >= tm) break;
+  }
+  return best;
+}
+
 int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K, int64_t ldx, const void* w,
                const void* scale, int s_dtype, const uint8_t* zero, int group, int N, void* out, int out_dtype,
                int64_t ldo, const void* residual, int64_t ldr, void* ws, size_t wsb, void* stream) {
@@ -834,6 +860,7 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
     t.part = nullptr;
     t.cnt = nullptr;
     t.sk = 0;
+    t.gm = 0;
     if (fits32) {
       PfPlan p = plan_prefill(wk, M, K, N, part_cap);
       if (getenv("QLIN_PREFILL_VERBOSE"))
@@ -864,6 +891,7 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
       if (p.tiled || force_tiled) {
         t.splits = p.splits;
         t.sk = p.sk;
+        if (p.sk == 0) t.gm = prefill_tile_group(wk, M, K, N, p.shape);
         if (p.splits > 1 || p.sk > 0) {
           t.cnt = (unsigned*)ws;
           t.part = (float*)((char*)ws + kCounterBytes);

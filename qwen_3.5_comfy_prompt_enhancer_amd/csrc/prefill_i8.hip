@@ -34,6 +34,10 @@
 //   * The K order of every output element is fixed (blocks in order within each K
 //     group, then group 0 + group 1, then splits in order), so rows do not depend on M
 //     or on the chunking for a given split count.
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include "qlin_dev.h"
 #include "qlin_internal.h"
 
@@ -90,17 +94,23 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   const int M = a.M, K = a.K;
   // split-K: `S` workgroups per output tile, each over nk consecutive 64-wide blocks
   // from kb0
+  // Workgroups go to the 8 XCDs in turn; with a.gm set, XCD x's workgroups (b = x,
+  // x + 8, ...) take one contiguous run of the tile order (a tile's splits included).
   const int S = a.splits;
-  const int tile = (int)blockIdx.x / S, split = (int)blockIdx.x % S;
+  const int b = (int)blockIdx.x, W = (int)gridDim.x;
+  const int v = a.gm > 0 ? (b & 7) * (W >> 3) + min(b & 7, W & 7) + (b >> 3) : b;
+  const int tile = v / S, split = v % S;
   const int nk = K / 64 / S;
   const int kb0 = split * nk;
 
-  // grouped tile order
+  // grouped tile order: runs of consecutive tiles cover gm row tiles x a few column
+  // tiles, so the workgroups of one XCD share activation and weight tiles in its L2
   const int tiles_m = (M + BM - 1) / BM, tiles_n = a.ntiles;
-  const int per_group = GROUP_M * tiles_n;
+  const int gm = a.gm > 0 ? a.gm : GROUP_M;
+  const int per_group = gm * tiles_n;
   const int grp = tile / per_group;
-  const int first_m = grp * GROUP_M;
-  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int first_m = grp * gm;
+  const int gsize = min(tiles_m - first_m, gm);
   const int tm = first_m + (tile % per_group) % gsize;
   const int tn = (tile % per_group) / gsize;
   int si = 0;
@@ -573,6 +583,26 @@ hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t st)
   a.ntiles = tn;
   if (a.splits < 1) a.splits = 1;
   const int tiles = ((a.M + BM - 1) / BM) * tn * a.splits;
+  // Tile order: each XCD runs one contiguous eighth of it, going down gm row tiles
+  // before the next column tile; gm minimises what a run reads into its XCD's L2: rows
+  // x (128 x K int8 activations) + columns x (the weights of 128 columns, every set).
+  // QLIN_I8_GM overrides it (0: groups of 8 row tiles, workgroups in launch order).
+  const char* eg = getenv("QLIN_I8_GM");
+  if (eg && *eg) {
+    a.gm = atoi(eg) > 0 ? atoi(eg) : 0;
+  } else {
+    const long long tm = (a.M + BM - 1) / BM;
+    const long long run = std::max<long long>(1, (tm * tn + 7) / 8);
+    const double arow = (double)BM * a.K, wcol = (double)a.K * BN * (wk == WK_W4 ? 0.5 : 1.0) * (epi == EPI_STORE ? 1 : 2);
+    double best_c = 0.0;
+    for (int gm = 1; gm <= 64; gm *= 2) {
+      const long long h = std::min<long long>(gm, tm);
+      const long long rows = std::min(h, run), cols = (run + h - 1) / h;
+      const double c = (double)rows * arow + (double)cols * wcol;
+      if (gm == 1 || c < best_c) best_c = c, a.gm = gm;
+      if (gm >= tm) break;
+    }
+  }
   switch (epi) {
     case EPI_STORE: return launch_i8_e<EPI_STORE>(a, wk, hz, tiles, st);
     case EPI_GATEUP: return launch_i8_e<EPI_GATEUP>(a, wk, hz, tiles, st);

@@ -169,13 +169,15 @@ void prefill_kernel(const TlArgs a) {
   const int kg = wave / (WM * WN);  // K group: with KG = 2, group kg computes substep kg
   const int wl = wave % (WM * WN);  // wave within its group
   const int wm = wl / WN, wn = wl % WN;
-  // grouped tile order: consecutive workgroups share weight column tiles in L2
+  // grouped tile order: runs of consecutive tiles cover gm row tiles x a few column
+  // tiles, so the workgroups of one XCD share activation and weight tiles in its L2
   // (the balanced schedule numbers tiles row by row: its workgroups already run
   // consecutive tiles on one XCD)
   const int pid = tile;
-  const int per_group = GROUP_M * tiles_n;
-  const int first_m = (pid / per_group) * GROUP_M;
-  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int gm = a.gm > 0 ? a.gm : GROUP_M;
+  const int per_group = gm * tiles_n;
+  const int first_m = (pid / per_group) * gm;
+  const int gsize = min(tiles_m - first_m, gm);
   const int tm = pair ? pid / tiles_n : first_m + (pid % per_group) % gsize;
   const int tn = pair ? pid % tiles_n : (pid % per_group) / gsize;
   const int m0 = tm * G::BM, n0 = tn * BN;
@@ -597,10 +599,14 @@ void prefill_kernel(const TlArgs a) {
 
   const int nkt = K / BK;  // K tiles of one output tile
   if constexpr (!BAL) {
-    // one tile per workgroup, or `splits` workgroups per tile over equal K ranges
+    // one tile per workgroup, or `splits` workgroups per tile over equal K ranges.
+    // Workgroups go to the 8 XCDs in turn; with a.gm set, XCD x's workgroups (b = x,
+    // x + 8, ...) take one contiguous run of the order (a tile's splits included).
     const int S = a.splits;
     const int nk = nkt / S;
-    run((int)blockIdx.x / S, ((int)blockIdx.x % S) * nk, nk, S, (int)blockIdx.x % S, false);
+    const int b = (int)blockIdx.x, W = (int)gridDim.x;
+    const int v = a.gm > 0 ? (b & 7) * (W >> 3) + min(b & 7, W & 7) + (b >> 3) : b;
+    run(v / S, (v % S) * nk, nk, S, v % S, false);
     return;
   }
   // Balanced schedule: the (tile, K tile) units in order, a.sk consecutive units per

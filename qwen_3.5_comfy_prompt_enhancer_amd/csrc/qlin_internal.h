@@ -74,6 +74,9 @@ struct SkArgs {
                        // the alternate 64-wide blocks of [s*kchunk, (s+1)*kchunk) (wave w:
                        // block offsets w, w+2, ...), the K order of the tiled int8 kernel
   ProArgs pro;         // fused prologue (launches with SkLaunch::pro set); x / xs unused
+  int gm;              // tiled int8 kernel: row tiles per group of the tile order; > 0 also
+                       // gives each XCD a contiguous run of the order (0: groups of 8,
+                       // workgroups in order)
 };
 
 struct SkLaunch {
@@ -119,6 +122,9 @@ struct TlArgs {
   unsigned* cnt;      // split-K arrival counters [tiles], zero between calls
   int sk;             // balanced schedule: K tiles per workgroup over all tiles (0 = off);
                       // partials [tiles][2][waves][128 * 64]
+  int gm;             // one tile per workgroup: row tiles per group of the tile order; > 0
+                      // also gives each XCD a contiguous run of the order (0: groups of 8,
+                      // workgroups in order)
 };
 
 // LDS-DMA prefill kernel; `shape` picks the workgroup tile (rows x columns):

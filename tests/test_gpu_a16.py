@@ -498,6 +498,29 @@ def test_prefill_balanced(shape, sk, monkeypatch):
     assert torch.equal(_run_w4(x, packed, s4, z, out_dtype=torch.bfloat16), y4)
 
 
+@pytest.mark.parametrize("shape,splits", [(0, 1), (1, 1), (1, 4), (2, 2)])
+def test_prefill_tile_order_does_not_change_results(shape, splits, monkeypatch):
+    """The XCD-aware tile order (each XCD runs a contiguous run of the order, gm row
+    tiles per group) only places workgroups: every gm, and the earlier order
+    (QLIN_PREFILL_GM=0), gives the same bits, with and without split-K (W8 with
+    residual, W4 with zeros).  M = 300 gives a partial last row tile and a
+    workgroup count that is not a multiple of 8 for some shapes."""
+    _force_tiled(monkeypatch, shape)
+    monkeypatch.setenv("QLIN_PREFILL_SPLITS", str(splits))
+    M, K, N = 300, 1024, 1280
+    x = H.act_f16(M, K, seed=390 + shape)
+    w, s = H.w8(K, N, seed=391)
+    res = torch.randn((M, N), generator=H.gen(392)).to(torch.float16)
+    packed, s4, z = H.w4(K, N, seed=393, group=128, zeros="random")
+    outs = []
+    for gm in ("0", "1", "2", "8", ""):
+        monkeypatch.setenv("QLIN_PREFILL_GM", gm)
+        outs.append((_run_w8(x, w, s, residual=res), _run_w4(x, packed, s4, z, out_dtype=torch.bfloat16)))
+    H.assert_out_close(outs[0][0], H.linear_w8_ref_cols(x, w, s, np.arange(N), residual=res))
+    for o in outs[1:]:
+        assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1])
+
+
 def test_prefill_balanced_rejects_three_way_tiles(monkeypatch):
     """sk=12 would spread a 32-K-tile output tile over three workgroups: refused."""
     _force_tiled(monkeypatch, 1)

@@ -405,6 +405,33 @@ def test_prefill_tiled_split_k_rows_independent_of_chunking(tiled):
     assert torch.equal(y[100:200], yc)
 
 
+@pytest.mark.parametrize("splits", [1, 4])
+def test_prefill_tiled_tile_order_does_not_change_results(splits, tiled):
+    """The XCD-aware tile order of the tiled int8 kernel only places workgroups: every
+    gm, and the earlier order (QLIN_I8_GM=0), gives the same bits for gemm_i8 with the
+    residual and for gate/up + requant (codes and scales), with and without split-K."""
+    gemm, _ = _g()
+    tiled.setenv("QLIN_ENGINE_SPLITS", str(splits))
+    M, K, N = 300, 2048, 1280
+    a, as_ = H.engine_act(M, K, seed=495 + splits)
+    b, bs = H.engine_w8(K, N, seed=496)
+    (wg, sg), (wu, su) = H.engine_w8(K, N, seed=497), H.engine_w8(K, N, seed=498)
+    hid = torch.randn((M, N), generator=H.gen(499)).to(torch.bfloat16).cuda()
+    outs = []
+    for gm in ("0", "1", "2", "8", ""):
+        tiled.setenv("QLIN_I8_GM", gm)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y, residual=hid)
+        q = torch.empty((M, N), dtype=torch.int8, device="cuda")
+        s = torch.empty((M, N // 64), dtype=torch.float32, device="cuda")
+        gemm.mlp_gate_up_quant(a.cuda(), as_.cuda(), wg.cuda(), sg.cuda(), wu.cuda(), su.cuda(), q, s)
+        outs.append((y.cpu(), q.cpu(), s.cpu()))
+    ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy(), bs.numpy(), residual=_bf16(hid.cpu()))
+    H.assert_out_close(outs[0][0], ref)
+    for o in outs[1:]:
+        assert all(torch.equal(u, v) for u, v in zip(o, outs[0]))
+
+
 def test_prefill_tiled_bad_split_raises(tiled):
     gemm, _ = _g()
     tiled.setenv("QLIN_ENGINE_SPLITS", "3")  # 32 blocks of 64 do not split three ways
