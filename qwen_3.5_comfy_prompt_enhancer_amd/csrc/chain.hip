@@ -59,6 +59,7 @@ constexpr int TNP = TNC + 4;       // padded LDS row
 constexpr int RING = 4;            // 32-wide K steps a wave has in flight (its register ring)
 constexpr int KU = CW * RING * 32; // K rows of the shortest unit: 512 (W4: one group of 128 per wave)
 constexpr int kSpinLimit = 1 << 22;        // polls of a dependency before giving up
+constexpr int kWaitVm0 = 0x0F70;           // s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima)
 // Levels whose units at the shortest length outnumber the workgroups that fit the chip
 // this many times over (kPlanSlots: 3 workgroups on each of 256 CUs) take longer units
 // -- up to a tile's whole K -- streamed through the same register ring: fewer split-K
@@ -114,7 +115,7 @@ __device__ __forceinline__ u32x4 ld_x_coherent(__amdgpu_buffer_rsrc_t r, unsigne
 
 template <int COLS>
 __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t d[2]) {
-  const u32x2 v = *(const u32x2*)p;
+  const u32x2 v = ld_global<u32x2>(p);
   d[0] = v.x;
   d[1] = v.y;
 }
@@ -189,8 +190,8 @@ __device__ __forceinline__ void load_group(const UnitPos& P, int k0, int grp, Un
   const long long idx = (long long)gi * N + ccl;
   const bool f32 = P.J.sdt == DT_F32;
   const uint8_t* sb = (const uint8_t*)P.J.s + idx * (f32 ? 4 : 2);
-  R.sraw[0] = *(const u32x4*)sb;
-  R.sraw[1] = *(const u32x4*)(sb + (f32 ? 16 : 0));
+  R.sraw[0] = ld_global<u32x4>(sb);
+  R.sraw[1] = ld_global<u32x4>(sb + (f32 ? 16 : 0));
   ld8<8>(P.J.z ? P.J.z + idx : sb, R.zr);
 }
 
@@ -237,6 +238,13 @@ __device__ __forceinline__ void load_x(const UnitPos& P, int M, bool now, u32x4 
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) xv[s] = load_x_step(P, xr, M, now, k0, nsteps, s);
 }
+
+// Keeps a ring slot's refill where the source puts it: right after the slot's MFMAs,
+// activations first.  Left to itself the scheduler sinks every refill of a ring cycle
+// below the cycle's last MFMA, and the first step of the next cycle then waits for all
+// of them (the counter is in order), so a wave had no loads in flight while it
+// computed.
+__device__ __forceinline__ void refill_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // One 32-wide W8 step: 8 MFMAs of the lane's 8 columns against the step's activations.
 __device__ __forceinline__ void w8_step(const uint32_t (&w)[8][2], u32x4 x, f32x4 (&acc)[8]) {
@@ -295,6 +303,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     P = decode_unit(jobs, unit_job, u);
     issue_loads<W4>(P, R);
     load_x<W4>(P, M, P.J.level == 0, xv);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // see the reload of a dependent unit's activations
   }
   while (u < H.nunits) {
     // the next unit's index, fetched now and read after this unit's partial stores
@@ -325,7 +334,14 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     }
 
     // ---------------- activations of a dependent unit, read after its wait ----------------
-    if (J.level > 0) load_x<W4>(P, M, true, xv);
+    // The wait makes this path enter the ring cycles with nothing in flight.  Otherwise
+    // these activations, loaded after the whole ring of weights, would make the wait
+    // insertion assume that order at the top of every ring cycle (where it merges with
+    // the cycles' own in-order refills, activations first) and drain the ring there.
+    if (J.level > 0) {
+      load_x<W4>(P, M, true, xv);
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    }
 
     // The next unit is made known before this unit's last ring cycle (its index was
     // fetched at this unit's start, so that atomic's latency is hidden), and the last
@@ -365,8 +381,10 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           constexpr int s = decltype(sc)::value;
           w8_step(R.w[s], xv[s], acc);
           const int nx = RING * (cyc + 1) + s;
-          load_w_step<false>(P, k0, nsteps, nx, R.w[s]);
+          refill_fence();
           xv[s] = load_x_step(P, xr, M, true, k0, nsteps, nx);
+          load_w_step<false>(P, k0, nsteps, nx, R.w[s]);
+          refill_fence();
         });
       }
       publish_next();
@@ -374,8 +392,10 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) {
         w8_step(R.w[s], xv[s], acc);
-        load_w_step<false>(Pn, k0n, nstepsn, s, R.w[s]);
+        refill_fence();
         xv[s] = load_x_step(Pn, xrn, M, xn_now, k0n, nstepsn, s);
+        load_w_step<false>(Pn, k0n, nstepsn, s, R.w[s]);
+        refill_fence();
       }
     } else {
       // (1024 + lo, 64 + hi) operands.  One ring cycle of RING steps is one group of
@@ -410,14 +430,16 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           }
           c1 = mfma_f16(av, boff, c1);
           c2 = mfma_f16(av, bone, c2);
+          refill_fence();
           if constexpr (LOADS == 1) {
             const int nx = RING * (cyc + 1) + st;
-            load_w_step<true>(P, k0, nsteps, nx, R.w[st]);
             xv[st] = load_x_step(P, xr, M, true, k0, nsteps, nx);
+            load_w_step<true>(P, k0, nsteps, nx, R.w[st]);
           } else {
-            load_w_step<true>(Pn, k0n, nstepsn, st, R.w[st]);
             xv[st] = load_x_step(Pn, xrn, M, xn_now, k0n, nstepsn, st);
+            load_w_step<true>(Pn, k0n, nstepsn, st, R.w[st]);
           }
+          refill_fence();
         });
         float sc[8];
         cvt_scale4(R.sraw[0], J.sdt, sc);

@@ -184,7 +184,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
         const int blk = kb0 + min(2 * st + k2, nk - 1);
         const long long gi = (long long)(blk * 64 / a.group) * n + ncol0 + c;
         rg.bs = ld_scale1_raw(sset[s], a.sdt, gi);  // converted at the LDS store
-        if constexpr (HZ) rg.bz = zset[s][gi];
+        if constexpr (HZ) rg.bz = ld_global<uint8_t>(zset[s] + gi);
       }
     }
   };

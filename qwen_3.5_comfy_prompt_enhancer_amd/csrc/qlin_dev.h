@@ -43,6 +43,15 @@ __device__ __forceinline__ T bitcast(F f) {
   return __builtin_bit_cast(T, f);
 }
 
+// Load of a T from global memory through a generic pointer.  A plain dereference of a
+// pointer the compiler cannot place (one read from a descriptor in memory) becomes a
+// flat load, which counts on the LDS counter as well: every later wait for an LDS
+// access then also waits for it, draining a register ring of weight loads.
+template <typename T>
+__device__ __forceinline__ T ld_global(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+
 // f(std::integral_constant<int, I>{}) for I = B .. E-1, unrolled at compile time.
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -185,8 +194,8 @@ __device__ __forceinline__ float load_scale(const void* p, int dt, long long i) 
 __device__ __forceinline__ u32x4 ld_scale4_raw(const void* p, int dt, long long idx) {
   const bool f32 = dt == DT_F32;
   const uint8_t* base = (const uint8_t*)p + idx * (f32 ? 4 : 2);
-  const u32x2 v0 = *(const u32x2*)base;
-  const u32x2 v1 = *(const u32x2*)(base + (f32 ? 8 : 0));
+  const u32x2 v0 = ld_global<u32x2>(base);
+  const u32x2 v1 = ld_global<u32x2>(base + (f32 ? 8 : 0));
   return u32x4{v0.x, v0.y, v1.x, v1.y};
 }
 
@@ -208,7 +217,7 @@ __device__ __forceinline__ void cvt_scale4(const u32x4 raw, int dt, float out[4]
 // dword holding element idx (for 16-bit types it also holds the neighbour).
 __device__ __forceinline__ uint32_t ld_scale1_raw(const void* p, int dt, long long idx) {
   const long long byte = (dt == DT_F32) ? idx * 4 : ((idx * 2) & ~3LL);
-  return *(const uint32_t*)((const uint8_t*)p + byte);
+  return ld_global<uint32_t>((const uint8_t*)p + byte);
 }
 
 // The value of ld_scale1_raw's dword for element idx (only idx's parity is used).

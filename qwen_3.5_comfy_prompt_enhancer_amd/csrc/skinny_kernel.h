@@ -97,13 +97,13 @@ __device__ __forceinline__ void ld_scales_raw_nb(const void* p, int dt, long lon
   const bool f32 = dt == DT_F32;
   const uint8_t* base = (const uint8_t*)p + idx * (f32 ? 4 : 2);
   if constexpr (COLS == 4) {
-    const u32x2 v0 = *(const u32x2*)base;
-    const u32x2 v1 = *(const u32x2*)(base + (f32 ? 8 : 0));
+    const u32x2 v0 = ld_global<u32x2>(base);
+    const u32x2 v1 = ld_global<u32x2>(base + (f32 ? 8 : 0));
     raw[0] = u32x4{v0.x, v0.y, v1.x, v1.y};
   } else {
     const int last16 = COLS / 8 - 1;  // last vector of 16-bit scales
 #pragma unroll
-    for (int c = 0; c < COLS / 4; ++c) raw[c] = *(const u32x4*)(base + 16 * (f32 ? c : min(c, last16)));
+    for (int c = 0; c < COLS / 4; ++c) raw[c] = ld_global<u32x4>(base + 16 * (f32 ? c : min(c, last16)));
   }
 }
 
