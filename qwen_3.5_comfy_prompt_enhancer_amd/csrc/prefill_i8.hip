@@ -326,20 +326,26 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   // sets, the loop written for even and odd st so their indices are static) and two
   // iterations ahead with two (one register set: the gate/up accumulators need the
   // registers).
+  // Every copy and LDS store is issued unconditionally: stages past the last one read
+  // the last block again (fetch clamps the block index) and are stored to the buffer
+  // no one reads any more.  A copy issued under a condition made the wait insertion
+  // assume, at the join, that its registers were the most recent loads: it waited for
+  // every copy in flight (vmcnt(0)) before each stage's LDS stores and again before
+  // the next copy, so a stage waited a whole memory round trip.
   const int nst = (nk + 1) / 2;
   if constexpr (NS == 1) {
     Regs rg0, rg1;
     fetch(rg0, 0);
     store(rg0, 0);
-    if (nst > 1) fetch(rg1, 1);
-    if (nst > 2) fetch(rg0, 2);
+    fetch(rg1, 1);
+    fetch(rg0, 2);
     __syncthreads();
     // next: the registers holding stage st+1, stored now and refilled with stage st+3
     auto iter = [&](int st, Regs& next) {
       if (2 * st + kg < nk) compute(st & 1);
-      if (st + 1 < nst) store(next, (st + 1) & 1);
+      store(next, (st + 1) & 1);
       __syncthreads();
-      if (st + 3 < nst) fetch(next, st + 3);
+      fetch(next, st + 3);
     };
     int st = 0;
     for (; st + 1 < nst; st += 2) {
@@ -351,13 +357,13 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
     Regs rg;
     fetch(rg, 0);
     store(rg, 0);
-    if (nst > 1) fetch(rg, 1);
+    fetch(rg, 1);
     __syncthreads();
     for (int st = 0; st < nst; ++st) {
       if (2 * st + kg < nk) compute(st & 1);
-      if (st + 1 < nst) store(rg, (st + 1) & 1);
+      store(rg, (st + 1) & 1);
       __syncthreads();
-      if (st + 2 < nst) fetch(rg, st + 2);
+      fetch(rg, st + 2);
     }
   }
 
