@@ -281,9 +281,17 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
         tr4(hi[4], hi[5], hi[6], hi[7], o1);
 #pragma unroll
         for (int t = 0; t < 4; ++t) bv[t] = u32x4{e0[t], e1[t], o0[t], o1[t]};
-        const f32x4 bsv = *(const f32x4*)(base + G::BS_OFF + (s * 256 + kg * BN + cb) * 4);
-        uint32_t zw = 0;
-        if constexpr (HZ) zw = *(const uint32_t*)(base + G::BZ_OFF + s * 256 + kg * BN + cb);
+        // The MFMA sums 16 * (nibble - 8) * a: the dot is p / 16, exactly.  Rather than
+        // shifting every p, the fold takes float(p) (exact: |p| < 2^24) against the scale
+        // product divided by 16 (exact): fma(float(p), fl(a_s * b_s) / 16, acc) is
+        // fma(float(p / 16), fl(a_s * b_s), acc) bit for bit, one instruction less.
+        const f32x4 bsv = *(const f32x4*)(base + G::BS_OFF + (s * 256 + kg * BN + cb) * 4) * 0.0625f;
+        int zc[4] = {0, 0, 0, 0};  // 16 * (8 - z): explicit zeros add (8 - z) * sum(a), times 16
+        if constexpr (HZ) {
+          const uint32_t zw = *(const uint32_t*)(base + G::BZ_OFF + s * 256 + kg * BN + cb);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) zc[t] = (8 - (int)((zw >> (8 * t)) & 0xFFu)) * 16;
+        }
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -291,8 +299,8 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
             const i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              int v = p[r] >> 4;  // exact: the MFMA summed 16 * (nibble - 8)
-              if constexpr (HZ) v += (8 - (int)((zw >> (8 * t)) & 0xFFu)) * sx[rb][r];
+              int v = p[r];  // 16 * the dot
+              if constexpr (HZ) v += zc[t] * sx[rb][r];
               acc[s][rb][t][r] = fmaf((float)v, asv[rb][r] * bsv[t], acc[s][rb][t][r]);
             }
           }
