@@ -638,14 +638,19 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
         } else {
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
+            // The MFMA summed 16 * (nibble - 8) * a: float(16 * dot) (exact, |.| < 2^24)
+            // against the scale product divided by 16 (exact) is fma(float(dot), a_s *
+            // b_s, acc) bit for bit, without a shift per output.
             float ws[COLS];
             cvt_scales<COLS>(st.sraw[s], a.sdt, ws);
+#pragma unroll
+            for (int t = 0; t < COLS; ++t) ws[t] *= 0.0625f;
 #pragma unroll
             for (int t = 0; t < COLS; ++t) {
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
-                int v = iacc[s][t][r] >> 4;  // exact: the MFMA summed 16 * (nibble - 8)
-                if constexpr (HZ) v += (8 - (int)byte_of(st.z[s].d[t >> 2], t & 3)) * sx[r];
+                int v = iacc[s][t][r];  // 16 * the dot
+                if constexpr (HZ) v += (8 - (int)byte_of(st.z[s].d[t >> 2], t & 3)) * 16 * sx[r];
                 acc[s][t][r] = fmaf((float)v, as_[r] * ws[t], acc[s][t][r]);
               }
               iacc[s][t] = i32x4{0, 0, 0, 0};
