@@ -659,10 +659,44 @@ def head_pmc(args):
     return 0
 
 
+def prefill_w4_cases(args):
+    """For `rocprofv3` runs comparing the W4 and W8 prefill kernels: for each of the
+    three M = 2048 prefill shapes (2048x6144, 6144x2048, 2048x2048), 3 eager launches of
+    W8 (fp16 column scales), then 3 of W4 group 128 with fp16 scales, and on 2048x6144
+    also 3 each with bf16 and fp32 group scales (random fp16 x)."""
+    import torch
+    dev = torch.device("cuda", 0)
+    lin = importlib.import_module(f"{ALIAS}.kernels.linear")
+    g = torch.Generator().manual_seed(3)
+    M = 2048
+    for (K, N) in [(2048, 6144), (6144, 2048), (2048, 2048)]:
+        x = torch.randn(M, K, generator=g).to(torch.float16).to(dev)
+        w8 = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8).to(dev)
+        s8 = (torch.rand(N, generator=g) * 1e-3).to(torch.float16).to(dev)
+        p4 = torch.randint(0, 256, (K // 2, N), generator=g, dtype=torch.uint8).to(dev)
+        s4 = (torch.rand(K // 128, N, generator=g) * 1e-3).to(torch.float16).to(dev)
+        y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        for _ in range(3):
+            lin.linear_w8(x, w8, s8, y)
+        for _ in range(3):
+            lin.linear_w4(x, p4, s4, y)
+        if (K, N) == (2048, 6144):
+            for dt in (torch.bfloat16, torch.float32):
+                sx = s4.to(dt)
+                for _ in range(3):
+                    lin.linear_w4(x, p4, sx, y)
+        torch.cuda.synchronize()
+    print(json.dumps({"workload": "prefill-pmc", "cases": "w4"}), flush=True)
+    return 0
+
+
 def prefill_pmc(args):
     """For `rocprofv3 --pmc` runs: a few launches of the dominant prefill GEMM (W8,
-    M=2048, K=2048, N=6144) and the same 1 GiB device copy as the calibration."""
+    M=2048, K=2048, N=6144) and the same 1 GiB device copy as the calibration; with
+    `--pmc-cases w4`, the W4 / W8 comparison of prefill_w4_cases instead."""
     import torch
+    if args.pmc_cases == "w4":
+        return prefill_w4_cases(args)
     dev = torch.device("cuda", 0)
     lin = importlib.import_module(f"{ALIAS}.kernels.linear")
     gen = torch.Generator().manual_seed(8)
@@ -788,6 +822,8 @@ def main() -> int:
                          "(the wide GEMV plan) after it (default: own for the W4 workloads, chain for W8, "
                          "whichever measured faster)")
     ap.add_argument("--pmc-kind", default="w8", choices=["w8", "w4"], help="decode-pmc: weight format")
+    ap.add_argument("--pmc-cases", default="dominant", choices=["dominant", "w4"],
+                    help="prefill-pmc: the dominant W8 GEMM, or the W4 / W8 comparison on the three shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--detail", action="store_true", help="per-shape table on stderr")
