@@ -115,7 +115,7 @@ __device__ __forceinline__ u32x4 ld_x_coherent(__amdgpu_buffer_rsrc_t r, unsigne
 
 template <int COLS>
 __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t d[2]) {
-  const u32x2 v = ld_global<u32x2>(p);
+  const u32x2 v = ld_global_nt<u32x2>(p);
   d[0] = v.x;
   d[1] = v.y;
 }
