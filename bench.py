@@ -819,8 +819,8 @@ def main() -> int:
                          "the decode sweeps, whose shapes are independent; layer for the 9B-class decode chain)")
     ap.add_argument("--head", default=None, choices=["chain", "own"],
                     help="chain launches: the vocabulary head inside the chain launch, or as its own launch "
-                         "(the wide GEMV plan) after it (default: own for the W4 workloads, chain for W8, "
-                         "whichever measured faster)")
+                         "(the wide GEMV plan) after it (default: own for the 9B-class W4 chain, chain "
+                         "otherwise, whichever measured faster)")
     ap.add_argument("--pmc-kind", default="w8", choices=["w8", "w4"], help="decode-pmc: weight format")
     ap.add_argument("--pmc-cases", default="dominant", choices=["dominant", "w4"],
                     help="prefill-pmc: the dominant W8 GEMM, or the W4 / W8 comparison on the three shapes")
@@ -844,8 +844,7 @@ def main() -> int:
 
     wl = args.workload
     if args.head is None:
-        w4 = wl in ("decode-w4", "chain-w4") or (wl == "decode-pmc" and args.pmc_kind == "w4")
-        args.head = "own" if w4 else "chain"
+        args.head = "own" if wl == "chain-w4" else "chain"
     if wl == "head-pmc":
         return head_pmc(args)
     if wl == "prefill-pmc":

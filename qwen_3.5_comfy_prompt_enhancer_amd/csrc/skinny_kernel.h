@@ -47,11 +47,14 @@ struct Row {
   uint32_t d[COLS / 4];
 };
 
+// COLS = 16 is the wide plan of the decode GEMV (one row tile: every weight byte is
+// read once), whose rows are loaded non-temporally; the narrower plans also serve row
+// tiles that re-read the weights from L2.
 template <int COLS>
 __device__ __forceinline__ Row<COLS> ld_row(const uint8_t* p, bool valid) {
   Row<COLS> r;
   if constexpr (COLS == 16) {
-    const u32x4 v = *(const u32x4*)p;
+    const u32x4 v = ld_global_nt<u32x4>(p);
     r.d[0] = valid ? v.x : 0u;
     r.d[1] = valid ? v.y : 0u;
     r.d[2] = valid ? v.z : 0u;
