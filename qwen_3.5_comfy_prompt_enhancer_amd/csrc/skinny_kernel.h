@@ -47,24 +47,26 @@ struct Row {
   uint32_t d[COLS / 4];
 };
 
-// COLS = 16 is the wide plan of the decode GEMV (one row tile: every weight byte is
-// read once), whose rows are loaded non-temporally; the narrower plans also serve row
-// tiles that re-read the weights from L2.
-template <int COLS>
+// Weight rows, loaded non-temporally where that measured faster: W8 rows of 8 or 16
+// columns (decode plans read each byte once; the 16-row prefill tiles of 8 columns lost
+// nothing) and the wide W4 plan (16 columns, decode only).  W4 rows of 4 or 8 columns
+// (decode and 16-row tiles: 5-14 % slower non-temporal), the 4-column W8 tiles (the
+// 512-row o-projection's 16-row tiles: slower) and the zeros keep plain loads.
+template <int COLS, bool NT>
 __device__ __forceinline__ Row<COLS> ld_row(const uint8_t* p, bool valid) {
   Row<COLS> r;
   if constexpr (COLS == 16) {
-    const u32x4 v = ld_global_nt<u32x4>(p);
+    const u32x4 v = NT ? ld_global_nt<u32x4>(p) : ld_global<u32x4>(p);
     r.d[0] = valid ? v.x : 0u;
     r.d[1] = valid ? v.y : 0u;
     r.d[2] = valid ? v.z : 0u;
     r.d[3] = valid ? v.w : 0u;
   } else if constexpr (COLS == 8) {
-    const u32x2 v = *(const u32x2*)p;
+    const u32x2 v = NT ? ld_global_nt<u32x2>(p) : ld_global<u32x2>(p);
     r.d[0] = valid ? v.x : 0u;
     r.d[1] = valid ? v.y : 0u;
   } else {
-    const uint32_t v = *(const uint32_t*)p;
+    const uint32_t v = NT ? ld_global_nt<uint32_t>(p) : ld_global<uint32_t>(p);
     r.d[0] = valid ? v : 0u;
   }
   return r;
@@ -365,14 +367,14 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
     for (int s = 0; s < NS; ++s) {
       const uint8_t* base = wp[s] + r0 * n + ccl;
 #pragma unroll
-      for (int r = 0; r < NR; ++r) st.w[s][r] = ld_row<COLS>(base + (long long)r * n, true);
+      for (int r = 0; r < NR; ++r) st.w[s][r] = ld_row<COLS, (!W4 && COLS >= 8) || COLS == 16>(base + (long long)r * n, true);
       if constexpr (W4) {
         const long long gi = (long long)(k / G) * n + ccl;
         // measured: the fp16-activation loops run best with the dtype branch (the
         // compiler unswitches them), the int8-activation ones without it
         if constexpr (F16) ld_scales_raw<COLS>(sp[s], a.sdt, gi, st.sraw[s]);
         else ld_scales_raw_nb<COLS>(sp[s], a.sdt, gi, st.sraw[s]);
-        if constexpr (HZ) st.z[s] = ld_row<COLS>(zp[s] + gi, true);
+        if constexpr (HZ) st.z[s] = ld_row<COLS, false>(zp[s] + gi, true);
       }
     }
   };
