@@ -292,18 +292,33 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) zc[t] = (8 - (int)((zw >> (8 * t)) & 0xFFu)) * 16;
         }
+        auto fold4 = [&](const i32x4& p, int rb, int t) {
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              int v = p[r];  // 16 * the dot
-              if constexpr (HZ) v += zc[t] * sx[rb][r];
-              acc[s][rb][t][r] = fmaf((float)v, asv[rb][r] * bsv[t], acc[s][rb][t][r]);
-            }
+          for (int r = 0; r < 4; ++r) {
+            int v = p[r];  // 16 * the dot
+            if constexpr (HZ) v += zc[t] * sx[rb][r];
+            acc[s][rb][t][r] = fmaf((float)v, asv[rb][r] * bsv[t], acc[s][rb][t][r]);
           }
+        };
+        if constexpr (NS == 1) {
+          // all 16 dots first, then their folds (as for W8 below)
+          i32x4 p[4][4];
+#pragma unroll
+          for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              p[rb][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0);
+#pragma unroll
+          for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) fold4(p[rb][t], rb, t);
+        } else {
+#pragma unroll
+          for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              fold4(__builtin_amdgcn_mfma_i32_16x16x64_i8(av[rb], bitcast<i32x4>(bv[t]), izero, 0, 0, 0), rb, t);
+        }
       } else {
         uint32_t d[16];
 #pragma unroll
