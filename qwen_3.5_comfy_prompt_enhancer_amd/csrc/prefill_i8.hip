@@ -45,13 +45,17 @@ namespace qlin {
 
 namespace {
 
-constexpr int BM = 128, BN = 128;
-constexpr int WAVES = 8;
-constexpr int THREADS = 64 * WAVES;
+constexpr int BM = 128;
 constexpr int GROUP_M = 8;  // tile order: 8 row tiles per group share weight column tiles in L2
 
-template <int WK, int NS>
+// WNW: 64-column wave tiles per workgroup row.  2: the 128 x 128 tile of 8 waves with
+// copies through registers; 1: the 128 x 64 tile of 4 waves with LDS DMA copies (W8 store
+// calls), small enough in registers and LDS for three workgroups per CU.
+template <int WK, int NS, int WNW = 2>
 struct Gi8 {
+  static constexpr int BN = 64 * WNW;
+  static constexpr int WAVES = 4 * WNW;
+  static constexpr int THREADS = 64 * WAVES;
   static constexpr bool W4 = WK == WK_W4;
   static constexpr int A_BLK = BM * 64;                 // activation bytes of one block
   static constexpr int B_ROWS = W4 ? 32 : 64;           // weight rows of one block
@@ -68,7 +72,7 @@ struct Gi8 {
   static constexpr int BS_OFF = AS_OFF + 2 * BM * 4;    // W4 group scales: [set][2][128] fp32
   static constexpr int BZ_OFF = BS_OFF + (W4 ? NS * 2 * BN * 4 : 0);  // W4 zeros: [set][2][128] bytes
   static constexpr int STAGE = BZ_OFF + (W4 ? NS * 2 * BN : 0);
-  static constexpr int RED = 4 * 64 * 64 * 4;  // one set of group 1's accumulators at the end
+  static constexpr int RED = 2 * WNW * 64 * 64 * 4;  // one set of group 1's accumulators at the end
   static constexpr int LDS = (2 * STAGE > RED) ? 2 * STAGE : RED;
 };
 
@@ -80,17 +84,30 @@ __device__ __forceinline__ int a_off(int r, int c) { return r * 64 + 16 * (c ^ (
 
 }  // namespace
 
-template <int WK, bool HZ, int EPI>
-__global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
+// 16-byte / 4-byte LDS DMA: lane i copies from vaddr to LDS m0 + 16 i (4 i).  Issued from
+// inline assembly; the loop waits for them explicitly (vmcnt) before its barrier.
+__device__ __forceinline__ void i8_dma16(const void* vaddr, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(vaddr), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void i8_dma4(const void* vaddr, uint32_t m0) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(vaddr), "{m0}"(m0) : "memory");
+}
+constexpr int kWaitVm0 = 0x0F70;  // s_waitcnt vmcnt(0) (expcnt, lgkmcnt at their maxima)
+
+template <int WK, bool HZ, int EPI, int WNW>
+__global__ __launch_bounds__(256 * WNW) __attribute__((amdgpu_waves_per_eu(WNW == 1 ? 3 : 2)))
+void prefill_i8_kernel(const SkArgs a) {
   constexpr int NS = (EPI == EPI_STORE) ? 1 : 2;  // weight sets feeding one tile
-  using G = Gi8<WK, NS>;
+  using G = Gi8<WK, NS, WNW>;
+  constexpr int BN = G::BN, THREADS = G::THREADS;
+  static_assert(WNW == 2 || (WK == WK_W8 && NS == 1), "the DMA tile serves W8 store calls");
   constexpr bool W4 = G::W4;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   const int tid = threadIdx.x;
   const int wave = (int)rfl((uint32_t)tid >> 6), lane = tid & 63;
   const int j = lane & 15, g = lane >> 4;
-  const int kg = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
+  const int kg = wave / (2 * WNW), wm = (wave / WNW) & 1, wn = wave % WNW;
   const int M = a.M, K = a.K;
   // split-K: `S` workgroups per output tile, each over nk consecutive 64-wide blocks
   // from kb0
@@ -330,7 +347,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
         tr4(d[12], d[13], d[14], d[15], x3);
 #pragma unroll
         for (int t = 0; t < 4; ++t) bv[t] = u32x4{x0[t], x1[t], x2[t], x3[t]};
-        if constexpr (NS == 1) {
+        if constexpr (NS == 1 && WNW == 2) {
           // all 16 dots first, then their folds: the folds run back to back instead of each
           // waiting on its MFMA (a block's compute measured 1029 instead of 1397 cycles for a
           // wave alone, 650 instead of 789 per block with two waves on a SIMD)
@@ -376,7 +393,46 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   // every copy in flight (vmcnt(0)) before each stage's LDS stores and again before
   // the next copy, so a stage waited a whole memory round trip.
   const int nst = (nk + 1) / 2;
-  if constexpr (NS == 1) {
+  if constexpr (WNW == 1) {
+    // Two LDS stages; the copy of stage st+1 goes out (LDS DMA, no registers) while stage st
+    // is computed, into the buffer the barrier that ended stage st-1 freed.  Stages past the
+    // last read the last block again (the index is clamped) into a buffer no one reads.
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+    auto dma_stage = [&](int st, int buf) {
+      const uint32_t sbase = lds0 + (uint32_t)(buf * G::STAGE);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {  // activations: 16 x 1 KB per stage, 4 per wave
+        const int q = wave * 4 + q4, k2 = q >> 3;
+        const int r = (q & 7) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);  // the chunk a_off(r, c) places at this slot
+        const int blk = kb0 + min(2 * st + k2, nk - 1);
+        const int row = min(m0 + r, M - 1);
+        i8_dma16(xq + (long long)row * K + blk * 64 + 16 * c, sbase + (uint32_t)(k2 * G::A_BLK + (q & 7) * 1024));
+      }
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) {  // weights: 8 groups of 16 rows x 64 bytes, 2 per wave
+        const int q = wave * 2 + q2, k2 = q >> 2, grp = q & 3;
+        const int blk = kb0 + min(2 * st + k2, nk - 1);
+        const uint8_t* src = wset[0] + (long long)(blk * 64 + 16 * grp + (lane >> 2)) * n + ncol0 + 16 * (lane & 3);
+        i8_dma16(src, sbase + (uint32_t)(G::B_OFF + k2 * G::B_BLK + G::b_row(16 * grp)));
+      }
+      {  // activation scales: [2 blocks][128 rows] fp32, 64 per wave
+        const int k2 = wave >> 1, r = (wave & 1) * 64 + lane;
+        const int blk = kb0 + min(2 * st + k2, nk - 1);
+        i8_dma4(a.xs + (long long)min(m0 + r, M - 1) * NG + blk,
+                sbase + (uint32_t)(G::AS_OFF + (k2 * BM + (wave & 1) * 64) * 4));
+      }
+    };
+    dma_stage(0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    for (int st = 0; st < nst; ++st) {
+      dma_stage(st + 1, (st + 1) & 1);
+      if (2 * st + kg < nk) compute(st & 1);
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      __syncthreads();
+    }
+  } else if constexpr (NS == 1) {
     Regs rg0, rg1;
     fetch(rg0, 0);
     store(rg0, 0);
@@ -411,7 +467,9 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   }
 
   // ---------------- K groups: group 0 + group 1 (fixed order), one set at a time ----------------
-  float* red = (float*)lds + (wave & 3) * (64 * 64) + lane;
+  constexpr int WT = 2 * WNW;  // wave tiles (wm, wn) of one K group
+  const int wt = wave % WT;
+  float* red = (float*)lds + wt * (64 * 64) + lane;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     if (s > 0) __syncthreads();  // group 0 has read the previous set
@@ -442,12 +500,12 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
     __shared__ int s_last;
     constexpr unsigned kSlot = 64u * 64u * 4u;
     const __amdgpu_buffer_rsrc_t rs =
-        part_rsrc(a.part + (long long)tile * S * NS * 4 * (64 * 64), (unsigned)(S * NS * 4) * kSlot);
+        part_rsrc(a.part + (long long)tile * S * NS * WT * (64 * 64), (unsigned)(S * NS * WT) * kSlot);
     const unsigned lane_off = (unsigned)lane * 16u;
     if (kg == 0) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const unsigned base = (unsigned)((split * NS + s) * 4 + (wave & 3)) * kSlot + lane_off;
+        const unsigned base = (unsigned)((split * NS + s) * WT + wt) * kSlot + lane_off;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -470,7 +528,7 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
     for (int sp = 0; sp < S; ++sp) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const unsigned base = (unsigned)((sp * NS + s) * 4 + (wave & 3)) * kSlot + lane_off;
+        const unsigned base = (unsigned)((sp * NS + s) * WT + wt) * kSlot + lane_off;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -588,46 +646,63 @@ __global__ __launch_bounds__(THREADS) void prefill_i8_kernel(const SkArgs a) {
   }
 }
 
-template <int WK, bool HZ, int EPI>
+template <int WK, bool HZ, int EPI, int WNW>
 static hipError_t launch_i8_t(const SkArgs& a, int tiles, hipStream_t st) {
-  using G = Gi8<WK, (EPI == EPI_STORE) ? 1 : 2>;
+  using G = Gi8<WK, (EPI == EPI_STORE) ? 1 : 2, WNW>;
   static bool attr_set = false;  // benign race: every caller sets the same value
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)prefill_i8_kernel<WK, HZ, EPI>,
+    const hipError_t e = hipFuncSetAttribute((const void*)prefill_i8_kernel<WK, HZ, EPI, WNW>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((prefill_i8_kernel<WK, HZ, EPI>), dim3(tiles), dim3(THREADS), (size_t)G::LDS, st, a);
+  hipLaunchKernelGGL((prefill_i8_kernel<WK, HZ, EPI, WNW>), dim3(tiles), dim3(G::THREADS), (size_t)G::LDS, st, a);
   return hipGetLastError();
 }
 
 template <int EPI>
 static hipError_t launch_i8_e(const SkArgs& a, int wk, bool hz, int tiles, hipStream_t st) {
-  if (wk == WK_W8) return launch_i8_t<WK_W8, false, EPI>(a, tiles, st);
-  if (hz) return launch_i8_t<WK_W4, true, EPI>(a, tiles, st);
-  return launch_i8_t<WK_W4, false, EPI>(a, tiles, st);
+  if (wk == WK_W8) return launch_i8_t<WK_W8, false, EPI, 2>(a, tiles, st);
+  if (hz) return launch_i8_t<WK_W4, true, EPI, 2>(a, tiles, st);
+  return launch_i8_t<WK_W4, false, EPI, 2>(a, tiles, st);
 }
 
+// Column tile of a call: 64 (the 4-wave DMA tile, three workgroups per CU) or 128.  Both
+// give the same bits.  W8 store calls split over K take the DMA tile: it measured faster
+// there (the 6144-deep down projection at M = 512 over 4 splits: 28.8 against 30.5 us;
+// with one split the 2048 -> 8192 proj3 was slower on it, 28.7-29.5 against 27.2-27.6).
+// QLIN_I8_DMA=1|0 forces it on or off for every W8 store call (tuning; same bits).
+static int i8_bn(int wk, int epi, int splits) {
+  if (wk != WK_W8 || epi != EPI_STORE) return 128;
+  const char* e = getenv("QLIN_I8_DMA");
+  if (e && *e) return atoi(e) == 1 ? 64 : 128;
+  return splits > 1 ? 64 : 128;
+}
+
+// Whether the tiled kernel covers a call; the 128-column condition holds for both tiles
+// (the DMA tile is only forced where it covers the call).
 bool prefill_i8_ok(const SkArgs& a, int wk, int epi) {
   if (a.M <= 16 || a.K % 64 != 0 || ((uintptr_t)a.x & 15) != 0) return false;
   if (wk == WK_W4 && a.group < 64) return false;
+  const char* e = getenv("QLIN_I8_DMA");
+  const int bn = (e && atoi(e) == 1 && wk == WK_W8 && epi == EPI_STORE) ? 64 : 128;
   const int nsets = (epi == EPI_STORE) ? a.nseg : 1;  // gate/up: one column range, two weight sets
   for (int s = 0; s < nsets; ++s)
-    if (a.seg[s].n % BN != 0) return false;
+    if (a.seg[s].n % bn != 0) return false;
   return true;
 }
 
 hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t st) {
+  const int bn = i8_bn(wk, epi, a.splits);
   int tn = 0;
   if (epi == EPI_STORE) {
     for (int s = 0; s < a.nseg; ++s) {
       a.seg[s].tile0 = tn;
-      tn += a.seg[s].n / BN;
+      tn += a.seg[s].n / bn;
     }
   } else {
     a.seg[0].tile0 = a.seg[1].tile0 = 0;
-    tn = a.seg[0].n / BN;
+    tn = a.seg[0].n / bn;
   }
   a.ntiles = tn;
   if (a.splits < 1) a.splits = 1;
@@ -642,7 +717,7 @@ hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t st)
   } else {
     const long long tm = (a.M + BM - 1) / BM;
     const long long run = std::max<long long>(1, (tm * tn + 7) / 8);
-    const double arow = (double)BM * a.K, wcol = (double)a.K * BN * (wk == WK_W4 ? 0.5 : 1.0) * (epi == EPI_STORE ? 1 : 2);
+    const double arow = (double)BM * a.K, wcol = (double)a.K * bn * (wk == WK_W4 ? 0.5 : 1.0) * (epi == EPI_STORE ? 1 : 2);
     double best_c = 0.0;
     for (int gm = 1; gm <= 64; gm *= 2) {
       const long long h = std::min<long long>(gm, tm);
@@ -653,7 +728,9 @@ hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t st)
     }
   }
   switch (epi) {
-    case EPI_STORE: return launch_i8_e<EPI_STORE>(a, wk, hz, tiles, st);
+    case EPI_STORE:
+      if (bn == 64) return launch_i8_t<WK_W8, false, EPI_STORE, 1>(a, tiles, st);
+      return launch_i8_e<EPI_STORE>(a, wk, hz, tiles, st);
     case EPI_GATEUP: return launch_i8_e<EPI_GATEUP>(a, wk, hz, tiles, st);
     default: return launch_i8_e<EPI_GATEUP_Q>(a, wk, hz, tiles, st);
   }

@@ -432,6 +432,31 @@ def test_prefill_tiled_tile_order_does_not_change_results(splits, tiled):
         assert all(torch.equal(u, v) for u, v in zip(o, outs[0]))
 
 
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_prefill_tiled_dma_tile_same_bits(splits, tiled):
+    """The 4-wave 128 x 64 DMA tile (QLIN_I8_DMA=1; the default for W8 store calls split
+    over K) and the 8-wave 128 x 128 tile fold every output in the same order: gemm_i8 with
+    the residual and proj3 (three column segments) give the same bits on both."""
+    gemm, _ = _g()
+    tiled.setenv("QLIN_ENGINE_SPLITS", str(splits))
+    M, K = 300, 2048
+    a, as_ = H.engine_act(M, K, seed=520 + splits)
+    b, bs = H.engine_w8(K, 1280, seed=521)
+    ws = [H.engine_w8(K, n, seed=522 + i) for i, n in enumerate((1024, 256, 256))]
+    hid = torch.randn((M, 1280), generator=H.gen(525)).to(torch.bfloat16).cuda()
+    outs = []
+    for dma in ("1", "0"):
+        tiled.setenv("QLIN_I8_DMA", dma)
+        y = torch.empty((M, 1280), dtype=torch.bfloat16, device="cuda")
+        gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), y, residual=hid)
+        p3 = torch.empty((M, 1536), dtype=torch.bfloat16, device="cuda")
+        gemm.proj3(a.cuda(), as_.cuda(), *(t.cuda() for w in ws for t in w), p3)
+        outs.append((y.cpu(), p3.cpu()))
+    ref = R.gemm_i8_ref(a.numpy(), as_.numpy(), b.numpy(), bs.numpy(), residual=_bf16(hid.cpu()))
+    H.assert_out_close(outs[0][0], ref)
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
 def test_prefill_tiled_bad_split_raises(tiled):
     gemm, _ = _g()
     tiled.setenv("QLIN_ENGINE_SPLITS", "3")  # 32 blocks of 64 do not split three ways
