@@ -667,16 +667,16 @@ static hipError_t launch_i8_e(const SkArgs& a, int wk, bool hz, int tiles, hipSt
   return launch_i8_t<WK_W4, false, EPI, 2>(a, tiles, st);
 }
 
-// Column tile of a call: 64 (the 4-wave DMA tile, three workgroups per CU) or 128.  Both
-// give the same bits.  W8 store calls split over K take the DMA tile: it measured faster
-// there (the 6144-deep down projection at M = 512 over 4 splits: 28.8 against 30.5 us;
-// with one split the 2048 -> 8192 proj3 was slower on it, 28.7-29.5 against 27.2-27.6).
-// QLIN_I8_DMA=1|0 forces it on or off for every W8 store call (tuning; same bits).
+// Column tile of a call: 128, or 64 (the 4-wave DMA tile, three workgroups per CU) for
+// W8 store calls with QLIN_I8_DMA=1 (same bits).  The DMA tile is not the default: timed
+// alone, the 6144-deep down projection at M = 512 over 4 splits ran 28.8 us on it against
+// 30.5, but inside a layer's sequence of calls 32.7 against about 31, and proj3 (one
+// split) was slower on it either way.
 static int i8_bn(int wk, int epi, int splits) {
+  (void)splits;
   if (wk != WK_W8 || epi != EPI_STORE) return 128;
   const char* e = getenv("QLIN_I8_DMA");
-  if (e && *e) return atoi(e) == 1 ? 64 : 128;
-  return splits > 1 ? 64 : 128;
+  return (e && atoi(e) == 1) ? 64 : 128;
 }
 
 // Whether the tiled kernel covers a call; the 128-column condition holds for both tiles

@@ -434,8 +434,8 @@ def test_prefill_tiled_tile_order_does_not_change_results(splits, tiled):
 
 @pytest.mark.parametrize("splits", [1, 2, 4])
 def test_prefill_tiled_dma_tile_same_bits(splits, tiled):
-    """The 4-wave 128 x 64 DMA tile (QLIN_I8_DMA=1; the default for W8 store calls split
-    over K) and the 8-wave 128 x 128 tile fold every output in the same order: gemm_i8 with
+    """The 4-wave 128 x 64 DMA tile (QLIN_I8_DMA=1) and the 8-wave 128 x 128 tile (the
+    default) fold every output in the same order: gemm_i8 with
     the residual and proj3 (three column segments) give the same bits on both."""
     gemm, _ = _g()
     tiled.setenv("QLIN_ENGINE_SPLITS", str(splits))
