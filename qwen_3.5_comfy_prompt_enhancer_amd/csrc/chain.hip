@@ -190,8 +190,8 @@ __device__ __forceinline__ void load_group(const UnitPos& P, int k0, int grp, Un
   const long long idx = (long long)gi * N + ccl;
   const bool f32 = P.J.sdt == DT_F32;
   const uint8_t* sb = (const uint8_t*)P.J.s + idx * (f32 ? 4 : 2);
-  R.sraw[0] = ld_global<u32x4>(sb);
-  R.sraw[1] = ld_global<u32x4>(sb + (f32 ? 16 : 0));
+  R.sraw[0] = ld_global_nt<u32x4>(sb);
+  R.sraw[1] = ld_global_nt<u32x4>(sb + (f32 ? 16 : 0));
   ld8<8>(P.J.z ? P.J.z + idx : sb, R.zr);
 }
 
