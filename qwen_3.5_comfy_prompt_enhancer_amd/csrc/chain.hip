@@ -239,6 +239,41 @@ __device__ __forceinline__ void load_x(const UnitPos& P, int M, bool now, u32x4 
   for (int s = 0; s < STEPS; ++s) xv[s] = load_x_step(P, xr, M, now, k0, nsteps, s);
 }
 
+// W8 with M <= 4: the activations of one ring cycle (RING steps, 128 K rows of rows 0-3)
+// in one 64-lane load, lane 16 r + c holding row r, K rows k0 + 128 cyc + 8 c .. + 7 (two
+// whole 128-byte lines per row), instead of RING loads with 4 M of 64 lanes active and
+// half a line per row each.  Rows past M, steps past the wave's range and any step when
+// `now` is false read zeros, as in load_x_step.
+__device__ __forceinline__ u32x4 load_x_cycle(const UnitPos& P, __amdgpu_buffer_rsrc_t xr, int M, bool now, int k0,
+                                              int nsteps, int cyc) {
+  const int lane = threadIdx.x & 63, r = lane >> 4, c = lane & 15;
+  const int step = RING * cyc + (c >> 2);
+  const unsigned off = (unsigned)(((long long)r * P.J.ldx + k0 + 128 * cyc + 8 * c) * 2);
+  return ld_x_coherent(xr, (now && step < nsteps && r < M) ? off : 0xFFFFFFF0u);
+}
+
+// The first ring cycle's activations of a unit (one load per lane).
+__device__ __forceinline__ u32x4 load_x_first_cycle(const UnitPos& P, int M, bool now) {
+  int k0, nsteps;
+  wave_range<false>(P, &k0, &nsteps);
+  return load_x_cycle(P, x_rsrc(P, M), M, now, k0, nsteps, 0);
+}
+
+// Step s's MFMA operand from a cycle's activations: lane (j, g) takes row j, K rows
+// 32 s + 8 g .. + 7, which lane 16 j + 4 s + g holds.  Rows 4-15 take a copy of row j & 3
+// (no select: it would put each permute under a branch); MFMA rows are independent and
+// the workgroup sum reads rows below M only.
+__device__ __forceinline__ u32x4 x_of_step(const u32x4 xc, int s) {
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int src = ((j & 3) * 16 + 4 * s + g) * 4;
+  u32x4 v;
+  v.x = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xc.x);
+  v.y = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xc.y);
+  v.z = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xc.z);
+  v.w = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)xc.w);
+  return v;
+}
+
 // Keeps a ring slot's refill where the source puts it: right after the slot's MFMAs,
 // activations first.  Left to itself the scheduler sinks every refill of a ring cycle
 // below the cycle's last MFMA, and the first step of the next cycle then waits for all
@@ -270,7 +305,7 @@ __device__ __forceinline__ unsigned* level_flag(uint8_t* plan, const ChainHdr& H
 // The read-only parts of the plan (job descriptors, unit table, level sizes) come as
 // separate restrict-qualified arguments so that the compiler reads them with scalar
 // loads: the descriptors' pointers then stay in scalar registers.
-template <bool W4>
+template <bool W4, bool XC>
 __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void chain_kernel(uint8_t* plan, const ChainJob* __restrict__ jobs,
                                                    const int* __restrict__ unit_job,
                                                    const unsigned* __restrict__ need) {
@@ -298,11 +333,14 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
   UnitRegs<W4> R;
   UnitPos P;
   u32x4 xv[STEPS];
+  u32x4 xc = u32x4{0u, 0u, 0u, 0u};  // XC: the current ring cycle's activations
+  static_assert(!(W4 && XC), "one-load activation cycles are built for W8");
   // a level-0 unit's activations go out with its weights; a later level's after its wait
   if (u < H.nunits) {
     P = decode_unit(jobs, unit_job, u);
     issue_loads<W4>(P, R);
-    load_x<W4>(P, M, P.J.level == 0, xv);
+    if constexpr (XC) xc = load_x_first_cycle(P, M, P.J.level == 0);
+    else load_x<W4>(P, M, P.J.level == 0, xv);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // see the reload of a dependent unit's activations
   }
   while (u < H.nunits) {
@@ -339,7 +377,8 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     // insertion assume that order at the top of every ring cycle (where it merges with
     // the cycles' own in-order refills, activations first) and drain the ring there.
     if (J.level > 0) {
-      load_x<W4>(P, M, true, xv);
+      if constexpr (XC) xc = load_x_first_cycle(P, M, true);
+      else load_x<W4>(P, M, true, xv);
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
     }
 
@@ -370,7 +409,37 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     f32x4 acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (!W4) {
+    if constexpr (XC) {
+      // as below, with each cycle's activations in one register per lane: the cycle's
+      // step operands are permuted out of it at the cycle's start, and the next cycle's
+      // load goes out with the refill of the first slot
+      const int ncyc = J.wsteps / RING;
+      const __amdgpu_buffer_rsrc_t xr = x_rsrc(P, M);
+      for (int cyc = 0; cyc + 1 < ncyc; ++cyc) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) xv[s] = x_of_step(xc, s);
+        static_for<0, RING>([&](auto sc) {
+          constexpr int s = decltype(sc)::value;
+          w8_step(R.w[s], xv[s], acc);
+          refill_fence();
+          if constexpr (s == 0) xc = load_x_cycle(P, xr, M, true, k0, nsteps, cyc + 1);
+          load_w_step<false>(P, k0, nsteps, RING * (cyc + 1) + s, R.w[s]);
+          refill_fence();
+        });
+      }
+      publish_next();
+      const __amdgpu_buffer_rsrc_t xrn = x_rsrc(Pn, M);
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) xv[s] = x_of_step(xc, s);
+      static_for<0, RING>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        w8_step(R.w[s], xv[s], acc);
+        refill_fence();
+        if constexpr (s == 0) xc = load_x_cycle(Pn, xrn, M, xn_now, k0n, nstepsn, 0);
+        load_w_step<false>(Pn, k0n, nstepsn, s, R.w[s]);
+        refill_fence();
+      });
+    } else if constexpr (!W4) {
       // the wave's steps through the RING-deep register ring: each step's slot is
       // refilled with the step RING ahead as soon as its MFMAs are issued; the last
       // RING steps issue no loads
@@ -767,28 +836,41 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
 }
 
 std::mutex g_mu;
-int g_grid[64][2];                       // resident workgroups per device and weight kind
+int g_grid[64][3];                       // resident workgroups per device and kernel variant
 struct PlanInfo {
   const void* plan;
-  int w4;
+  int w4, M;
   long long jobs_off, unit_off, need_off;
 };
+
+// Kernel variant of a plan: 0 W8, 1 W4, 2 W8 with one activation load per ring cycle
+// (M = 2-4; QLIN_CHAIN_XC=0 turns it off).  Every variant gives the same bits.  At
+// M = 1 the per-step loads have only 4 lanes active anyway, and the permutes' latency
+// at each cycle's start made the one-load form 1 % slower there (measured).
+int chain_variant(const PlanInfo& pi) {
+  if (pi.w4) return 1;
+  const char* e = getenv("QLIN_CHAIN_XC");
+  return (pi.M >= 2 && pi.M <= 4 && !(e && strcmp(e, "0") == 0)) ? 2 : 0;
+}
 std::vector<PlanInfo> g_plans;  // plans initialized in this process
 
-int chain_grid(int w4, int* grid) {
+int chain_grid(int variant, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= 64) return set_error(QLIN_ERR_HIP, "qlin_chain_run: hipGetDevice failed");
   std::lock_guard<std::mutex> lk(g_mu);
-  if (g_grid[dev][w4] == 0) {
+  if (g_grid[dev][variant] == 0) {
     int cus = 0, per = 0;
     e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess)
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, w4 ? chain_kernel<true> : chain_kernel<false>, CT, 0);
+    if (e == hipSuccess) {
+      if (variant == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<true, false>, CT, 0);
+      else if (variant == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<false, true>, CT, 0);
+      else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<false, false>, CT, 0);
+    }
     if (e != hipSuccess || cus <= 0 || per <= 0) return set_error(QLIN_ERR_HIP, "qlin_chain_run: occupancy query failed");
-    g_grid[dev][w4] = cus * per;
+    g_grid[dev][variant] = cus * per;
   }
-  *grid = g_grid[dev][w4];
+  *grid = g_grid[dev][variant];
   return QLIN_OK;
 }
 
@@ -863,7 +945,7 @@ extern "C" int qlin_chain_init(const qlin_chain_job* jobs, int njobs, int M, voi
     snprintf(msg, sizeof(msg), "qlin_chain_init: copy: HIP error %d (%s)", (int)e, hipGetErrorString(e));
     return set_error(QLIN_ERR_HIP, msg);
   }
-  remember_plan(PlanInfo{plan, L.w4, L.jobs_off, L.unit_off, L.need_off});
+  remember_plan(PlanInfo{plan, L.w4, M, L.jobs_off, L.unit_off, L.need_off});
   return QLIN_OK;
 }
 
@@ -875,14 +957,17 @@ extern "C" int qlin_chain_run(void* plan, void* stream) {
   if (!find_plan(plan, &pi))
     return set_error(QLIN_ERR_INVALID, "qlin_chain_run: plan not initialized by qlin_chain_init in this process");
   int grid = 0;
-  const int rc = chain_grid(pi.w4, &grid);
+  const int variant = chain_variant(pi);
+  const int rc = chain_grid(variant, &grid);
   if (rc != QLIN_OK) return rc;
   uint8_t* const p = (uint8_t*)plan;
   const ChainJob* jobs = (const ChainJob*)(p + pi.jobs_off);
   const int* units = (const int*)(p + pi.unit_off);
   const unsigned* need = (const unsigned*)(p + pi.need_off);
-  if (pi.w4) hipLaunchKernelGGL(chain_kernel<true>, dim3(grid), dim3(CT), 0, (hipStream_t)stream, p, jobs, units, need);
-  else hipLaunchKernelGGL(chain_kernel<false>, dim3(grid), dim3(CT), 0, (hipStream_t)stream, p, jobs, units, need);
+  const hipStream_t st = (hipStream_t)stream;
+  if (variant == 1) hipLaunchKernelGGL((chain_kernel<true, false>), dim3(grid), dim3(CT), 0, st, p, jobs, units, need);
+  else if (variant == 2) hipLaunchKernelGGL((chain_kernel<false, true>), dim3(grid), dim3(CT), 0, st, p, jobs, units, need);
+  else hipLaunchKernelGGL((chain_kernel<false, false>), dim3(grid), dim3(CT), 0, st, p, jobs, units, need);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     char msg[160];
