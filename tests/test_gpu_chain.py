@@ -191,3 +191,37 @@ def test_bad_levels_rejected():
     ch.add(x, w.cuda(), s.cuda(), o, level=2)
     with pytest.raises(ValueError, match="level"):
         ch.build()
+
+
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_w8_one_load_activation_cycles_same_bits(M, monkeypatch):
+    """W8 chains at M = 2-4 load a ring cycle's activations with one load and permute
+    them to the MFMA lanes; QLIN_CHAIN_XC=0 takes one load per step instead.  The same
+    plan gives the same bits both ways: whole-K units (2048 deep), K-split units (6144
+    deep) and a dependent level that reads a level-0 output.  The first output is also
+    checked against the oracle."""
+    shapes = [(2048, 2048), (6144, 2048), (2048, 6144)]
+    ws = [_weights("w8", K, N, 870 + i) for i, (K, N) in enumerate(shapes)]
+    X = {K: H.act_f16(M, K, seed=875 + K).cuda() for K, _ in shapes}
+    outs = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _, N in shapes]
+    w4k, s4k, _ = _weights("w8", 6144, 2048, 879)
+    s4k = (s4k.float() / 64).to(torch.float16)
+    dep = torch.empty((M, 2048), dtype=torch.float16, device="cuda")
+    ch = _chain(M)
+    for (K, N), (w, s, _), o in zip(shapes, ws, outs):
+        ch.add(X[K], _cu(w), _cu(s), o, level=0)
+    ch.add(outs[2], _cu(w4k), _cu(s4k), dep, level=1)
+    ch.build()
+    res = {}
+    for xc in ("1", "0"):
+        monkeypatch.setenv("QLIN_CHAIN_XC", xc)
+        for o in outs + [dep]:
+            o.zero_()
+        ch.run()
+        torch.cuda.synchronize()
+        assert ch.wait_error() == 0
+        res[xc] = [o.cpu() for o in outs + [dep]]
+    for a, b in zip(res["1"], res["0"]):
+        assert torch.equal(a, b)
+    w0, s0, _ = ws[0]
+    H.assert_out_close(res["1"][0], _ref("w8", X[2048].cpu(), w0, s0, None, np.arange(2048)))
