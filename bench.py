@@ -93,6 +93,12 @@ def bytes_w4(M, K, N, G=128):
     return K * N // 2 + 2 * (K // G) * N + 2 * M * K + 2 * M * N
 
 
+def _capture(g):
+    """HIP graph capture on a stream that has a split-K workspace (kernels/qlin.py)."""
+    from qwen35_amd.kernels import qlin
+    return qlin.capture(g)
+
+
 # ------------------------------------------------------------------ weights
 
 class Weights:
@@ -132,7 +138,10 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
         hw = Weights(kind, head[1], head[2], dev, gen)
         kmax = max([K for _, K, _ in shapes] + [head[1]])
         xs = {M: torch.randn((M, kmax), generator=gen).to(torch.float16).to(dev) for M in ms}
-        outs = {M: [torch.empty((M, N), dtype=torch.float16, device=dev) for (_, _, N) in shapes] for M in ms}
+        # every job writes an output of its own (layer copy l, shape i), so a launch of
+        # the whole sweep is a valid computation whose results are checked below
+        outs = {M: [[torch.empty((M, N), dtype=torch.float16, device=dev) for (_, _, N) in shapes]
+                    for _ in range(layers)] for M in ms}
         hout = {M: torch.empty((M, head[2]), dtype=torch.float16, device=dev) for M in ms}
 
     def xin(M, K):
@@ -141,7 +150,7 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
     def run_layers(M):
         for l in range(layers):
             for i, (_, K, _) in enumerate(shapes):
-                lw[l][i].run(lin, xin(M, K), outs[M][i])
+                lw[l][i].run(lin, xin(M, K), outs[M][l][i])
 
     total = sum((layers * sum(w.nbytes(M) for w in lw[0]) if lw else 0) + hw.nbytes(M) for M in ms)
     if args.launch == "chain":
@@ -157,7 +166,7 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
                 for i in order:
                     _, K, _ = shapes[i]
                     lvl = base + LAYER_LEVEL.get(shapes[i][0], 0) if args.levels == "layer" else 0
-                    ch.add(xin(M, K), lw[l][i].w, lw[l][i].s, outs[M][i], level=lvl)
+                    ch.add(xin(M, K), lw[l][i].w, lw[l][i].s, outs[M][l][i], level=lvl)
                 if shapes and args.levels == "layer":
                     base += LEVELS_PER_LAYER
             if args.head == "chain":
@@ -184,7 +193,7 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
             torch.cuda.synchronize()
             for M in ms:
                 gh = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(gh):
+                with _capture(gh):
                     hw.run(lin, xin(M, head[1]), hout[M])
                 head_graphs[M] = gh
             torch.cuda.synchronize()
@@ -228,7 +237,7 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
     if not args.no_graph:
         for M in ms:
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            with _capture(g):
                 run_layers(M)
             graphs[M] = g
         torch.cuda.synchronize()
@@ -288,11 +297,11 @@ def detail_table(ctx, kind, shapes, head, ms, reps=40):
             def body():
                 for r in range(n):
                     w = hw if is_head else lw[r % layers][i]
-                    w.run(lin, xs[M][:, :K], hout[M] if is_head else outs[M][i])
+                    w.run(lin, xs[M][:, :K], hout[M] if is_head else outs[M][r % layers][i])
             body()
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            with _capture(g):
                 body()
             g.replay()
             torch.cuda.synchronize()
@@ -356,7 +365,7 @@ def prefill_bench(args, shapes=PREFILL_SHAPES):
         pair = []
         for part in (its[:dom], its[dom + 1:]):
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            with _capture(g):
                 for (_, _, _, _, _, w, x, o) in part:
                     w.run(lin, x, o)
             pair.append(g)
@@ -443,7 +452,7 @@ def engine_bench(args, kind):
         return K * N if kind == "w8" else K * N // 2 + (K // 128) * N * 2
 
     layer_wbytes = wbytes(2048, 8192) + wbytes(2048, 2048) + 2 * wbytes(2048, 6144) + wbytes(6144, 2048)
-    res, pro_res = {}, {}
+    res, pro_res, chain_res = {}, {}, {}
     fused = importlib.import_module(f"{ALIAS}.kernels.fused")
     normk = importlib.import_module(f"{ALIAS}.kernels.norm")
     nw_in = (torch.rand(2048, generator=gen) * 0.1).to(torch.bfloat16).to(dev)
@@ -453,7 +462,7 @@ def engine_bench(args, kind):
         run()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with _capture(g):
             run()
         for _ in range(args.warmup):
             g.replay()
@@ -521,6 +530,33 @@ def engine_bench(args, kind):
         pro_res[M] = (timed(run_unfused), timed(run_fused))
         log(f"engine {kind} layer with producers M={M:4d}: {pro_res[M][0] * 1e6:7.1f} us as producer + linear "
             f"launches, {pro_res[M][1] * 1e6:7.1f} us fused")
+        if M <= 8:
+            # the same layer body as ONE engine-chain launch per layer (kernels/echain.py):
+            # o-projection with its gate_mul producer, gate/up + quant with the post-norm,
+            # down, the next layer's proj3 with its in-norm (keeping the codes, as the
+            # engine's gate_proj reads them); levels 0-3
+            echain = importlib.import_module(f"{ALIAS}.kernels.echain")
+            chains = []
+            for L in lw:
+                ch = echain.EngineChain(M)
+                ch.gemm_i8(None, None, L["o"][0], L["o"][1], hid, residual=hid,
+                           pro=fused.Producer.gate_mul(aout, qkvz, hd=256), level=0)
+                ch.mlp_gate_up_quant(None, None, L["g"][0], L["g"][1], L["u"][0], L["u"][1], hq, hs,
+                                     pro=fused.Producer.rmsnorm(hid, nw_post, 1e-6), level=1)
+                ch.gemm_i8(hq, hs, L["d"][0], L["d"][1], hid, residual=hid, level=2)
+                ch.proj3(None, None, L["qkv"][0], L["qkv"][1], L["z"][0], L["z"][1], None, None, qkvz,
+                         pro=fused.Producer.rmsnorm(hid, nw_in, 1e-6, q=xq, s=xs), level=3)
+                chains.append(ch.build())
+
+            def run_chain():
+                for ch in chains:
+                    ch.run()
+
+            chain_res[M] = timed(run_chain)
+            if any(ch.wait_error() for ch in chains):
+                raise RuntimeError("engine chain: a dependency wait gave up")
+            log(f"engine {kind} layer with producers M={M:4d}: {chain_res[M] * 1e6:7.1f} us as one engine-chain "
+                f"launch per layer")
     act_bytes = lambda M: M * (2048 * 3 + 6144) + M * 4 * (32 * 3 + 96)
     out_bytes = lambda M: M * 2 * (8192 + 2048 * 2 * 2) + M * (6144 + 96 * 4)
     dec_bytes = {M: layer_wbytes + act_bytes(M) + out_bytes(M) for M in (1, 4)}
@@ -529,7 +565,39 @@ def engine_bench(args, kind):
         extra = (f"{dec_bytes[M] / res[M] / 1e9:7.0f} GB/s" if M in dec_bytes
                  else f"{flops / res[M] / 1e12:7.1f} TOPS")
         log(f"engine {kind} layer M={M:4d}: {res[M] * 1e6:8.1f} us per layer  {extra}")
-    return dec_bytes, flops, res, pro_res
+    for M in (1, 4):
+        log(f"engine {kind} layer chain M={M}: {dec_bytes[M] / chain_res[M] / 1e9:7.0f} GB/s")
+    return dec_bytes, flops, res, pro_res, chain_res
+
+
+def check_sweep(ctx, kind, shapes, head, ms, layers, max_cols=4096):
+    """Checks the outputs the timed decode steps left: every shape of the last layer
+    copy and sampled columns of the vocabulary head, at every M, against the fp32 CPU
+    path (torch_dequant + fp32 matmul of the same fp16 activations).  Returns the
+    worst normalized error max|y - ref| / max|ref| and whether it is within the 2e-3
+    tolerance plus the fp16 output rounding (2**-11 relative)."""
+    import torch
+    lw, hw, xs, outs, hout = ctx[:5]
+    worst = 0.0
+    gen = torch.Generator().manual_seed(17)
+    jobs = [(lw[layers - 1][i], (lambda M, i=i: outs[M][layers - 1][i]), None) for i in range(len(shapes))]
+    cols = torch.randperm(head[2], generator=gen)[:max_cols].sort().values
+    jobs.append((hw, (lambda M: hout[M]), cols))
+    for w, out_of, cols_ in jobs:
+        wd = torch_dequant(kind, w.w.cpu(), w.s.cpu())
+        if cols_ is not None:
+            wd = wd[:, cols_]
+        for M in ms:
+            x = xs[M][:, :w.K].float().cpu()
+            ref = x @ wd
+            y = out_of(M).float().cpu()
+            if cols_ is not None:
+                y = y[:, cols_]
+            err = float((y - ref).abs().max() / ref.abs().max())
+            worst = max(worst, err)
+    return {"max_rel_err": round(worst, 6), "ok": worst <= 2e-3 + 2.0 ** -11,
+            "checked": (f"every shape of layer copy {layers - 1} and {max_cols} sampled vocab-head columns, "
+                        f"M={'/'.join(map(str, ms))}, against dequantize + fp32 matmul on the CPU")}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -927,10 +995,16 @@ def main() -> int:
                              if not args.no_graph else "eager")}
         if other is not None:
             config["other_levels"] = other
+        if layers > 0 and wl != "chain-w4":
+            config["output_check"] = check_sweep(ctx, kind, shapes, head, ms, layers)
+            log(f"output check: {config['output_check']}")
+            if not config["output_check"]["ok"]:
+                print(json.dumps({"error": "decode sweep outputs out of tolerance", **config["output_check"]}))
+                return 1
         dtype = "f16 x int8" if kind == "w8" else "f16 x int4"
     elif wl in ("engine-w8", "engine-w4"):
         kind = wl.split("-")[1]
-        dec_bytes, pf_flops, res, pro_res = engine_bench(args, kind)
+        dec_bytes, pf_flops, res, pro_res, chain_res = engine_bench(args, kind)
         # value: decode rows M = 1 and 4 through the engine's calls, weight-streaming GB/s
         t = (res[1] + res[4]) / 2
         value = (dec_bytes[1] + dec_bytes[4]) / (res[1] + res[4]) / 1e9
@@ -942,8 +1016,10 @@ def main() -> int:
                   "prefill_chunk_M512_us_per_layer": round(res[512] * 1e6, 1),
                   "prefill_chunk_M512_tops": round(pf_flops / res[512] / 1e12, 1),
                   "with_producers_us_per_layer": {
-                      str(M): {"producer_then_linear": round(u * 1e6, 1), "fused": round(f * 1e6, 1)}
+                      str(M): {"producer_then_linear": round(u * 1e6, 1), "fused": round(f * 1e6, 1),
+                               **({"engine_chain": round(chain_res[M] * 1e6, 1)} if M in chain_res else {})}
                       for M, (u, f) in pro_res.items()},
+                  "engine_chain_GB_per_s": {str(M): round(dec_bytes[M] / chain_res[M] / 1e9, 1) for M in (1, 4)},
                   "launch": "hipgraph of all layers per M"}
         dtype = "i8 x int8" if kind == "w8" else "i8 x int4"
     else:

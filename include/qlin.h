@@ -323,6 +323,71 @@ int qlin_chain_init(const qlin_chain_job* jobs, int njobs, int M, void* plan, si
 int qlin_chain_run(void* plan, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Engine decode chains: the engine-signature linears and their activation producers
+ * between two mixer kernels, in one persistent launch
+ *
+ * The engine's decode step calls, between the attention / delta-rule kernels of two
+ * layers (engine.py:236-279, 265-268, 272-279, 218-226):
+ *   norm_gated_quant | gate_mul_quant -> gemm_i8 (o-projection, += hidden)
+ *   -> rmsnorm_quant -> mlp_gate_up_quant -> gemm_i8 (down, += hidden)
+ *   -> rmsnorm_quant -> proj3
+ * A chain job is one of those linears -- what qlin_gemm_i8 / qlin_gemm_w4,
+ * qlin_mlp_gate_up(_quant)_i8/_w4 or one column range of qlin_proj3_i8/_w4 computes --
+ * with its activations either read from memory (a_q, a_s) or made by its producer
+ * (`pro`, as the qlin_pro_* calls make them; the producer's input may be written by
+ * an earlier level of the same chain).  Levels start at 0 and rise by at most 1 along
+ * the list; level L > 0 starts only after every job of level L - 1 has written its
+ * outputs.  Every job gives the same bits as the corresponding single call with 1-8
+ * rows (those run the same work units as a one-job launch), and row m of an M-row
+ * chain equals an M = 1 chain.  No reference counterpart as a function: the reference
+ * launches a producer and a linear per projection and names whole-step capture as its
+ * next step (ENGINEERING.md:383-399); each job replaces one such pair of launches.
+ * ------------------------------------------------------------------------- */
+#define QLIN_EJ_GEMM 1           /* out = a . W (+ residual), bf16 */
+#define QLIN_EJ_GATE_UP 2        /* out = bf16(silu(a . Wg) * (a . Wu)) */
+#define QLIN_EJ_GATE_UP_QUANT 3  /* out_q / out_s = per-64 int8 codes of that */
+
+typedef struct qlin_echain_job {
+  int kind;               /* QLIN_EJ_* */
+  const int8_t* a_q;      /* int8 [M][K] (row stride K), or NULL with a producer */
+  const float* a_s;       /* fp32 [M][K/64] */
+  qlin_producer pro;      /* pro.kind 0: none; else as for the qlin_pro_* calls (pro.q /
+                             pro.s, if given, receive the codes too) */
+  int K, N;               /* K % 64 == 0, N % 16 == 0 (gate/up + quant: N % 64 == 0) */
+  int group;              /* 0 = W8 (int8 [K][N], scale [N]); else the W4 group (a
+                             multiple of 64 dividing K; packed [K/2][N], scale [K/G][N]) */
+  const void* w;          /* the weight (gate for gate/up) */
+  const void* scale;
+  const uint8_t* zero;    /* W4 zeros [K/G][N] or NULL (z = 8) */
+  const void* w2;         /* gate/up: the up weight, scale and zeros */
+  const void* scale2;
+  const uint8_t* zero2;
+  int scale_dtype;        /* QLIN_F16, QLIN_BF16 or QLIN_F32 */
+  void* out;              /* bf16 [M][ldo] (QLIN_EJ_GEMM, QLIN_EJ_GATE_UP) */
+  int64_t ldo;
+  const void* residual;   /* bf16 [M][ldr] or NULL; may alias out (QLIN_EJ_GEMM) */
+  int64_t ldr;
+  int8_t* out_q;          /* QLIN_EJ_GATE_UP_QUANT: codes [M][N], scales [M][N/64] */
+  float* out_s;
+  int level;              /* dependency level */
+} qlin_echain_job;
+
+/* Bytes of device memory an engine chain plan needs (0 if the jobs are invalid). */
+size_t qlin_echain_bytes(const qlin_echain_job* jobs, int njobs, int M);
+
+/* Validates the jobs (M = 1-8 rows; W8 jobs or W4 jobs, not both) and writes the plan
+ * into `plan` (caller-owned device memory, qlin_echain_bytes() bytes, 16-byte
+ * aligned), as qlin_chain_init does. */
+int qlin_echain_init(const qlin_echain_job* jobs, int njobs, int M, void* plan, size_t plan_bytes,
+                     void* stream);
+
+/* Runs every job of the plan in one launch on `stream`, asynchronously; capturable in
+ * a HIP graph.  Launches of one plan must not overlap in time.  The int at byte offset
+ * 20 of the plan is 1 after a launch in which a dependency wait gave up (it polls about
+ * 4 M times), 0 otherwise; it describes the last finished launch. */
+int qlin_echain_run(void* plan, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Layout entry points (bit-exactness checks of the unpack / dequant)
  * ------------------------------------------------------------------------- */
 

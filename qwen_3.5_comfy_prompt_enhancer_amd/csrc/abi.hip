@@ -33,24 +33,18 @@ int hip_status(const char* fn, hipError_t e) {
   return fail(QLIN_ERR_HIP, "%s: HIP error %d (%s)", fn, (int)e, hipGetErrorString(e));
 }
 
+// Fill kernel behind clear_counters (a kernel node, not a memset, so a call that clears
+// its counters can be captured in a graph).
+__global__ void zero_u32(unsigned* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
 #define QL_TRY(expr)              \
   do {                            \
     const int rc_ = (expr);       \
     if (rc_ != QLIN_OK) return rc_; \
   } while (0)
 
-__global__ void zero_u32(unsigned* p, int n) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
-}
-
-// Zero the first n arrival counters of a scratch with a fill kernel on `stream` (a
-// kernel node, not a memset, so the call can be captured in a graph).
-hipError_t clear_counters(void* ws, long long n, hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_u32, dim3((unsigned)std::min<long long>(256, (n + 255) / 256)), dim3(256), 0, stream,
-                     (unsigned*)ws, (int)n);
-  return hipGetLastError();
-}
 
 // Workspace: [counters | partial sums].  Counters must be zero between calls.
 constexpr size_t kWorkspaceBytes = size_t(256) << 20;
@@ -110,9 +104,12 @@ void plan_override(const Problem& P, int& cols, int& waves, int& upw) {
 // ((v0 + v1) + v2) + ...; then the W8 column scale (and residual, one rounding).
 // The 16-row skinny tiles reproduce it with two waves per split (lanes == 2).
 // S is chosen for the engine's 512-row chunk and then held for every M.
-// Calls with fewer rows (decode: one sequence or up to four best-of rows) keep the
-// decode plans, whose results depend on (K, N) only, so batch rows equal single rows.
-constexpr int kRowsM = 5;
+// Calls with fewer rows (decode: one sequence, or up to eight best-of candidates,
+// engine.py:392) run the engine decode work units (echain.hip), whose results depend
+// on (K, N) and the call kind only, so batch rows equal single rows; a chunk remainder
+// of 1-8 rows therefore agrees with the unchunked prefill to the tolerance, not bit
+// for bit.
+constexpr int kRowsM = kDecodeRowsMax + 1;
 constexpr int kRefChunkM = 512;
 
 // Column tiles of 128 over the call's column ranges.
@@ -332,6 +329,15 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
 // are not known to be zero).
 int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace, size_t ws_bytes,
                     hipStream_t stream, bool clear = false) {
+  // decode rows (one sequence or up to eight best-of rows) run on the engine decode
+  // work units, the units an engine chain runs: a call equals its chain job bit for bit
+  // (QLIN_ENGINE_DECODE=skinny keeps such calls on the skinny decode plans below, for
+  // comparisons; it changes the K order)
+  if (P.act == ACT_I8 && P.M <= kDecodeRowsMax && echain_covers(a, P.wk, P.M)) {
+    const char* ed = getenv("QLIN_ENGINE_DECODE");
+    if (!(ed && strcmp(ed, "skinny") == 0))
+      return echain_engine_call(fn, a, P.wk, P.epi, P.M, workspace, ws_bytes, kCounterBytes, stream, clear);
+  }
   if (P.act == ACT_I8 && P.M >= kRowsM) return engine_rows(fn, P, a, workspace, ws_bytes, stream, clear);
   SkLaunch L;
   L.act = P.act;
@@ -478,6 +484,28 @@ int check_engine_act(const char* fn, const int8_t* a_q, const float* a_s, int M,
 // codes go to q / s or, without them, to the end of the workspace, which is taken off
 // *wsb so no split-K partial reaches it.
 int setup_pro(const char* fn, ProArgs& p, int M, int K, void* ws, size_t* wsb) {
+  QL_TRY(check_producer(fn, p, M, K));
+  if (p.q) {
+    p.tq = p.q;
+    p.ts = p.s;
+  } else {
+    const size_t qb = ((size_t)M * K + 255) & ~(size_t)255;
+    const size_t sb = ((size_t)M * (K / 64) * sizeof(float) + 255) & ~(size_t)255;
+    if (!ws || *wsb < kCounterBytes + qb + sb)
+      return fail(QLIN_ERR_WORKSPACE, "%s: no room in the workspace for the activation codes", fn);
+    *wsb -= qb + sb;
+    p.tq = (int8_t*)ws + *wsb;
+    p.ts = (float*)((char*)ws + *wsb + qb);
+  }
+  p.lds_off = 0;
+  p.ldq = 0;
+  return QLIN_OK;
+}
+
+}  // namespace
+
+int qlin::check_producer(const char* fn, ProArgs& p, int M, int K) {
+  (void)M;
   if (p.kind != PRO_RMSNORM && p.kind != PRO_GATE_MUL && p.kind != PRO_NORM_GATED)
     return fail(QLIN_ERR_INVALID, "%s: unknown producer kind %d", fn, p.kind);
   if (K % 64 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 64", fn, K);
@@ -511,22 +539,17 @@ int setup_pro(const char* fn, ProArgs& p, int M, int K, void* ws, size_t* wsb) {
   if ((p.q == nullptr) != (p.s == nullptr)) return fail(QLIN_ERR_INVALID, "%s: give both q and s, or neither", fn);
   if (p.q && (!aligned(p.q, 8) || !aligned(p.s, 4)))
     return fail(QLIN_ERR_UNSUPPORTED, "%s: q must be 8-byte aligned", fn);
-  if (p.q) {
-    p.tq = p.q;
-    p.ts = p.s;
-  } else {
-    const size_t qb = ((size_t)M * K + 255) & ~(size_t)255;
-    const size_t sb = ((size_t)M * (K / 64) * sizeof(float) + 255) & ~(size_t)255;
-    if (!ws || *wsb < kCounterBytes + qb + sb)
-      return fail(QLIN_ERR_WORKSPACE, "%s: no room in the workspace for the activation codes", fn);
-    *wsb -= qb + sb;
-    p.tq = (int8_t*)ws + *wsb;
-    p.ts = (float*)((char*)ws + *wsb + qb);
-  }
-  p.lds_off = 0;
-  p.ldq = 0;
   return QLIN_OK;
 }
+
+hipError_t qlin::clear_counters(void* ws, long long n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_u32, dim3((unsigned)std::min<long long>(256, (n + 255) / 256)), dim3(256), 0, stream,
+                     (unsigned*)ws, (int)n);
+  return hipGetLastError();
+}
+
+namespace {
 
 int check_out16(const char* fn, const void* p, int64_t ld, int N, const char* what) {
   if (!p) return fail(QLIN_ERR_INVALID, "%s: null %s", fn, what);

@@ -89,25 +89,63 @@ __device__ __forceinline__ float pro_quant8(const float y[8], uint32_t& lo, uint
 // [rows][ng] after it) and/or the global code and scale matrices.
 struct ProOut {
   uint8_t* lq;  // LDS codes [rows][ldq bytes] for the K range [kb, ke), or nullptr
-  float* ls;    // LDS scales [rows][lng]
+  float* ls;    // LDS scales: row r, 64-column group b of the range at ls[r * lng + b * lsb]
   int ldq;
-  int lng;      // (ke - kb) / 64
+  int lng;      // row stride of ls ((ke - kb) / 64 for a [rows][groups] block)
+  int lsb;      // group stride of ls (1 for a [rows][groups] block)
   bool emit;    // also write p.q / p.s
 };
 
+// Loads of the producer's 16-bit inputs: plain, or (COH) device-coherent buffer loads
+// for inputs that an earlier part of the same launch may have written (the decode
+// chain), which plain loads could read stale from another XCD's L2.
+// The thread index; under COH (inside the decode chain's persistent loop) as a value
+// the compiler cannot hoist out of the loop, so what derives from it is not kept live
+// across the loop.
+template <bool COH>
+__device__ __forceinline__ int pro_tid() {
+  int t = (int)threadIdx.x;
+  if constexpr (COH) asm volatile("" : "+v"(t));
+  return t;
+}
+
+template <bool COH>
+__device__ __forceinline__ u32x4 pro_ld(const void* p, long long idx16) {
+  if constexpr (COH) {
+    return __builtin_amdgcn_raw_buffer_load_b128(part_rsrc(p, 0x7FFFFFF0u), (unsigned)(idx16 * 2), 0, kCpolSc1);
+  } else {
+    return *(const u32x4*)((const uint16_t*)p + idx16);
+  }
+}
+
+// The global copies of the codes (emit): device-coherent stores under COH, so a later
+// part of the same launch may read them.
+template <bool COH>
+__device__ __forceinline__ void pro_emit(const ProArgs& p, int K, int row, int k, uint32_t lo, uint32_t hi,
+                                         bool scale, float s) {
+  if constexpr (COH) {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, part_rsrc(p.q, 0x7FFFFFF0u),
+                                          (unsigned)((long long)row * K + k), 0, kCpolSc1);
+    if (scale)
+      __builtin_amdgcn_raw_buffer_store_b32(bitcast<uint32_t>(s), part_rsrc(p.s, 0x7FFFFFF0u),
+                                            (unsigned)(((long long)row * (K / 64) + k / 64) * 4), 0, kCpolSc1);
+  } else {
+    *(u32x2*)(p.q + (long long)row * K + k) = u32x2{lo, hi};
+    if (scale) p.s[(long long)row * (K / 64) + k / 64] = s;
+  }
+}
+
 // One (row, 64-column group) item of an 8-lane team: the lane's 8 columns start at k.
+template <bool COH>
 __device__ __forceinline__ void pro_put(const ProArgs& p, const ProOut& o, int K, int row0, int r, int kb, int k,
                                         int t8, const float y[8]) {
   uint32_t lo, hi;
   const float s = pro_quant8(y, lo, hi);
   if (o.lq) {
     *(u32x2*)(o.lq + (long long)r * o.ldq + (k - kb)) = u32x2{lo, hi};
-    if (t8 == 0) o.ls[r * o.lng + (k - kb) / 64] = s;
+    if (t8 == 0) o.ls[r * o.lng + ((k - kb) / 64) * o.lsb] = s;
   }
-  if (o.emit) {
-    *(u32x2*)(p.q + (long long)(row0 + r) * K + k) = u32x2{lo, hi};
-    if (t8 == 0) p.s[(long long)(row0 + r) * (K / 64) + k / 64] = s;
-  }
+  if (o.emit) pro_emit<COH>(p, K, row0 + r, k, lo, hi, t8 == 0, s);
 }
 
 // Chunks of a row's sum of squares a lane loads ahead (K <= 64 * 8 * kProSumPre);
@@ -117,11 +155,15 @@ constexpr int kProSumPre = 8;
 // The loads of a producer block that go out before the linear's first weight loads.
 // A wave's memory loads complete in issue order, so loads issued after the weights
 // would wait for them: issued first, they return while the weights stream in.
-struct ProPre {
-  u32x4 xs[kProSumPre];  // rmsnorm: this lane's first chunks of its wave's first row
+// PRE: chunks prefetched (any count gives the same sums: a lane folds its chunks in
+// increasing order either way); fewer hold fewer registers while weights stream.
+template <int PRE>
+struct ProPreN {
+  u32x4 xs[PRE];         // rmsnorm: this lane's first chunks of its wave's first row
   u32x4 x, g;            // the thread's first item: 8 activations, 8 gates / z values
   u32x4 w0, w1;          // and 8 norm-weight values (w1: the second half of fp32 ones)
 };
+using ProPre = ProPreN<kProSumPre>;
 
 __device__ __forceinline__ u32x4 pro_raw(const void* p, long long idx16) {
   return *(const u32x4*)((const uint16_t*)p + idx16);
@@ -185,15 +227,16 @@ __device__ __forceinline__ ProGeo pro_geo(const ProArgs& p, int row0, int rows, 
 // in-bounds addresses, and pro_block uses only the applicable ones (a load whose
 // result is merged at a control-flow join is waited for at the join, which would
 // hold the weight loads behind it).
-__device__ __forceinline__ void pro_issue(const ProArgs& p, int K, const ProGeo& G, ProPre& pp) {
-  const int tid = threadIdx.x;
+template <bool COH = false, int PRE = kProSumPre>
+__device__ __forceinline__ void pro_issue(const ProArgs& p, int K, const ProGeo& G, ProPreN<PRE>& pp) {
+  const int tid = pro_tid<COH>();
   const int wave = tid >> 6, lane = tid & 63;
   const bool ng_kind = p.kind == PRO_NORM_GATED;
   // rmsnorm's chunks (other kinds read the same in-bounds addresses and ignore them)
   const long long soff = (long long)(G.row0 + min(wave, G.rows - 1)) * p.ldx;
   const int nc = K >> 3;
 #pragma unroll
-  for (int i = 0; i < kProSumPre; ++i) pp.xs[i] = pro_raw(p.x, soff + 8LL * min(lane + 64 * i, nc - 1));
+  for (int i = 0; i < PRE; ++i) pp.xs[i] = pro_ld<COH>(p.x, soff + 8LL * min(lane + 64 * i, nc - 1));
   // the first item
   long long xi, gi, wi;
   if (ng_kind) {
@@ -214,8 +257,8 @@ __device__ __forceinline__ void pro_issue(const ProArgs& p, int K, const ProGeo&
   // kinds without gates or norm weight read fixed addresses of x instead (distinct from
   // the item's own, so the compiler cannot turn them into copies behind a branch)
   const bool has_g = p.kind != PRO_RMSNORM, has_w = p.kind != PRO_GATE_MUL;
-  pp.x = pro_raw(p.x, xi);
-  pp.g = pro_raw(has_g ? p.g : p.x, has_g ? gi : 0);
+  pp.x = pro_ld<COH>(p.x, xi);
+  pp.g = pro_ld<COH>(has_g ? p.g : p.x, has_g ? gi : 0);
   const bool f32w = has_w && p.wdt == DT_F32;
   const uint8_t* wb = has_w ? (const uint8_t*)p.w + wi * (f32w ? 4 : 2) : (const uint8_t*)p.x + 16;
   pp.w0 = *(const u32x4*)wb;
@@ -225,10 +268,11 @@ __device__ __forceinline__ void pro_issue(const ProArgs& p, int K, const ProGeo&
 // Codes and scales of the block (pro_issue's loads first, then the rest), into LDS
 // and / or the global code matrices.  Called by every thread of the workgroup (it
 // holds barriers); `lr` is LDS for `rows` floats.
-__device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo& G, const ProPre& pp,
+template <bool COH = false, int PRE = kProSumPre>
+__device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo& G, const ProPreN<PRE>& pp,
                                           const ProOut& o, float* lr) {
 #pragma clang fp contract(off)
-  const int tid = threadIdx.x;
+  const int tid = pro_tid<COH>();
   const int nthr = blockDim.x;
   const int rows = G.rows, row0 = G.row0, kb = G.kb, ke = G.ke, ng = G.ng;
   if (p.kind == PRO_RMSNORM || p.kind == PRO_GATE_MUL) {
@@ -243,7 +287,7 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo&
         int c0 = lane;
         if (r == wave) {
 #pragma unroll
-          for (int i = 0; i < kProSumPre; ++i) {
+          for (int i = 0; i < PRE; ++i) {
             if (lane + 64 * i < nc) {
               float v[8];
               pro_cvt8(pp.xs[i], p.xdt, v);
@@ -251,11 +295,11 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo&
               for (int e = 0; e < 8; ++e) acc = acc + v[e] * v[e];
             }
           }
-          c0 = lane + 64 * kProSumPre;
+          c0 = lane + 64 * PRE;
         }
         for (int c = c0; c < nc; c += 64) {
           float v[8];
-          pro_cvt8(pro_raw(p.x, off + 8LL * c), p.xdt, v);
+          pro_cvt8(pro_ld<COH>(p.x, off + 8LL * c), p.xdt, v);
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc = acc + v[e] * v[e];
         }
@@ -270,7 +314,7 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo&
       const int k = kb + (it - r * ng) * 64 + 8 * t8;
       const bool first = it == (tid >> 3);
       float x[8], y[8];
-      pro_cvt8(first ? pp.x : pro_raw(p.x, (long long)(row0 + r) * p.ldx + k), p.xdt, x);
+      pro_cvt8(first ? pp.x : pro_ld<COH>(p.x, (long long)(row0 + r) * p.ldx + k), p.xdt, x);
       if (p.kind == PRO_RMSNORM) {
         float w[8];
         u32x4 w0 = pp.w0, w1 = pp.w1;
@@ -286,11 +330,11 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo&
         // gates of head h sit at [h * 2 hd + hd, (h + 1) * 2 hd) of the gate row
         float gv[8];
         const long long gc = (long long)(k / p.hd) * (2 * p.hd) + p.hd + (k % p.hd);
-        pro_cvt8(first ? pp.g : pro_raw(p.g, (long long)(row0 + r) * p.ldg + gc), p.xdt, gv);
+        pro_cvt8(first ? pp.g : pro_ld<COH>(p.g, (long long)(row0 + r) * p.ldg + gc), p.xdt, gv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = x[e] * pro_sigmoid(gv[e]);
       }
-      pro_put(p, o, K, row0, r, kb, k, t8, y);
+      pro_put<COH>(p, o, K, row0, r, kb, k, t8, y);
     }
   } else {
     // PRO_NORM_GATED: teams of hd / 8 lanes, one (row, head) each; a head's groups are
@@ -304,13 +348,13 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo&
       const bool first = it == tid / T;
       const long long off = (long long)(row0 + r) * K + (long long)h * p.hd;
       float x[8], zv[8], w[8], y[8];
-      pro_cvt8(first ? pp.x : pro_raw(p.x, off + 8 * tl), p.xdt, x);
+      pro_cvt8(first ? pp.x : pro_ld<COH>(p.x, off + 8 * tl), p.xdt, x);
       float acc = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = acc + x[e] * x[e];
       const float ri = pro_rms_inv(pro_team_sum(acc, T), p.hd, p.eps);
-      pro_cvt8(first ? pp.g : pro_raw(p.g, (long long)(row0 + r) * p.ldg + (long long)h * p.hd + 8 * tl), p.xdt,
-               zv);
+      pro_cvt8(first ? pp.g : pro_ld<COH>(p.g, (long long)(row0 + r) * p.ldg + (long long)h * p.hd + 8 * tl),
+               p.xdt, zv);
       pro_cvt_w(pp.w0, pp.w1, p.wdt, w);  // the same 8 weights for every head
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -325,12 +369,9 @@ __device__ __forceinline__ void pro_block(const ProArgs& p, int K, const ProGeo&
       if (k >= kb && k < ke) {
         if (o.lq) {
           *(u32x2*)(o.lq + (long long)r * o.ldq + (k - kb)) = u32x2{lo, hi};
-          if ((tl & 7) == 0) o.ls[r * o.lng + (k - kb) / 64] = s;
+          if ((tl & 7) == 0) o.ls[r * o.lng + ((k - kb) / 64) * o.lsb] = s;
         }
-        if (o.emit) {
-          *(u32x2*)(p.q + (long long)(row0 + r) * K + k) = u32x2{lo, hi};
-          if ((tl & 7) == 0) p.s[(long long)(row0 + r) * (K / 64) + k / 64] = s;
-        }
+        if (o.emit) pro_emit<COH>(p, K, row0 + r, k, lo, hi, (tl & 7) == 0, s);
       }
     }
   }

@@ -20,6 +20,7 @@ __global__ __launch_bounds__(kProThreads) void producer_kernel(const ProArgs p, 
   o.ls = nullptr;
   o.ldq = 0;
   o.lng = 0;
+  o.lsb = 1;
   o.emit = true;
   const ProGeo G = pro_geo(p, blockIdx.x, 1, 0, K);
   ProPre pp;

@@ -149,6 +149,20 @@ int gemm_i8_scratch(const char* fn, const int8_t* a_q, const float* a_s, int M, 
                     int64_t ldr, void* scratch, size_t scratch_bytes, void* stream);
 size_t counter_bytes();
 
+// Validates an activation producer for M rows of K columns (norm_gated's input row
+// stride becomes K); returns a status with the message set.
+int check_producer(const char* fn, ProArgs& p, int M, int K);
+// Zeroes the first n arrival counters of a scratch with a fill kernel on `stream`.
+hipError_t clear_counters(void* ws, long long n, hipStream_t stream);
+// Engine decode work units (echain.hip): whether an engine-signature call of M rows
+// runs on them (M <= 8, W8 or W4 groups that are multiples of 64, 16-byte aligned
+// activations), and the call as a one-level launch of them.  The workspace holds
+// `counter_bytes` of arrival counters, then split-K partials.
+constexpr int kDecodeRowsMax = 8;
+bool echain_covers(const SkArgs& a, int wk, int M);
+int echain_engine_call(const char* fn, const SkArgs& a, int wk, int epi, int M, void* ws, size_t ws_bytes,
+                       size_t counter_bytes, hipStream_t stream, bool clear);
+
 // Standalone producer launch: codes and scales of all M rows into p.q / p.s.
 hipError_t launch_producer(const ProArgs& p, int M, int K, hipStream_t st);
 // Evaluates the producers' exp on n values (a test entry point).

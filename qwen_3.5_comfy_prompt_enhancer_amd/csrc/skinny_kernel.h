@@ -413,6 +413,7 @@ __attribute__((amdgpu_waves_per_eu(SkOcc<ACT, WK, EPI, COLS>::value))) void skin
       o.ls = pls;
       o.ldq = a.pro.ldq;
       o.lng = plng;
+      o.lsb = 1;
       o.emit = a.pro.q != nullptr && tile == 0;
       pro_block(a.pro, K, pgeo, ppre, o, plr);
     }

@@ -76,10 +76,12 @@ _SIGS = {
     "qlin_pro_exp_f32": [_P, _P, _I, _P],
 }
 
-# the decode-chain entry points are declared in kernels/chain.py (they take a struct array),
+# the decode-chain entry points are declared in kernels/chain.py and kernels/echain.py (they
+# take a struct array),
 # the fused-producer linears in kernels/fused.py (they take a struct)
 EXPORTS = ("qlin_version", "qlin_last_error", "qlin_workspace_bytes", *_SIGS,
            "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run",
+           "qlin_echain_bytes", "qlin_echain_init", "qlin_echain_run",
            "qlin_pro_gemm_i8", "qlin_pro_gemm_w4", "qlin_pro_proj3_i8", "qlin_pro_proj3_w4",
            "qlin_pro_mlp_gate_up_quant_i8", "qlin_pro_mlp_gate_up_quant_w4")
 
@@ -137,8 +139,8 @@ def check(status: int, name: str) -> None:
 
 
 _ws: dict[tuple[int, int], torch.Tensor] = {}
-_ws_first: dict[int, torch.Tensor] = {}
 _ws_lock = threading.Lock()
+_capture_streams: dict[int, torch.cuda.Stream] = {}
 
 
 def workspace(device: torch.device, stream: int | None = None) -> torch.Tensor:
@@ -146,11 +148,12 @@ def workspace(device: torch.device, stream: int | None = None) -> torch.Tensor:
     arrival counters at zero after every call, so it is never cleared again.
 
     Each stream gets its own, so calls running at the same time on two streams never
-    share arrival counters or partial sums.  A call made while a stream is being
-    captured into a HIP graph, on a stream that has no workspace yet, uses the
-    device's first workspace (a zero-fill cannot go into the graph): call once
-    outside capture first, and do not replay such a graph concurrently with other
-    calls on the device."""
+    share arrival counters or partial sums.  A call under HIP graph capture uses the
+    workspace of the capturing stream, which must exist before capture starts (a
+    zero-fill cannot go into the graph): capture with `capture()` below, or call
+    `bind_workspace(stream)` first.  A graph replays with the workspace it was captured
+    with, so graphs captured on one stream must not be replayed at the same time as each
+    other or as calls on that stream."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     if stream is None:
         stream = torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream
@@ -162,16 +165,34 @@ def workspace(device: torch.device, stream: int | None = None) -> torch.Tensor:
         w = _ws.get(key)
         if w is None:
             if torch.cuda.is_current_stream_capturing():
-                w = _ws_first.get(idx)
-                if w is None:
-                    raise RuntimeError("the first quantized-linear call on a device must run outside HIP graph "
-                                       "capture (it allocates the split-K workspace)")
-                return w
+                raise RuntimeError(
+                    "quantized-linear call under HIP graph capture on a stream without a workspace: capture "
+                    "with kernels.qlin.capture(graph), or call kernels.qlin.bind_workspace(stream) before "
+                    "capturing")
             nbytes = lib().qlin_workspace_bytes()
             w = torch.zeros(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
             _ws[key] = w
-            _ws_first.setdefault(idx, w)
     return w
+
+
+def bind_workspace(stream: torch.cuda.Stream) -> torch.Tensor:
+    """Allocate (once) the workspace of `stream`, outside graph capture, so that calls
+    captured on it later find it."""
+    return workspace(stream.device, stream.cuda_stream)
+
+
+def capture(graph: torch.cuda.CUDAGraph, stream: torch.cuda.Stream | None = None, **kw):
+    """`torch.cuda.graph(graph, stream=...)` on a stream that has a workspace: `stream`
+    (bound here if it has none), or a capture stream of the current device's own.
+    Graphs captured on the same stream share its workspace (see `workspace`)."""
+    if stream is None:
+        idx = torch.cuda.current_device()
+        stream = _capture_streams.get(idx)
+        if stream is None:
+            stream = torch.cuda.Stream(device=idx)
+            _capture_streams[idx] = stream
+    bind_workspace(stream)
+    return torch.cuda.graph(graph, stream=stream, **kw)
 
 
 def require_cuda(*ts) -> torch.device:

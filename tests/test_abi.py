@@ -27,8 +27,8 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 36
-    for n in ("qlin_rmsnorm_quant", "qlin_gate_mul_quant", "qlin_norm_gated_quant", "qlin_pro_exp_f32",
+    assert len(names) == 39
+    for n in ("qlin_echain_bytes", "qlin_echain_init", "qlin_echain_run","qlin_rmsnorm_quant", "qlin_gate_mul_quant", "qlin_norm_gated_quant", "qlin_pro_exp_f32",
               "qlin_pro_gemm_i8", "qlin_pro_gemm_w4", "qlin_pro_proj3_i8", "qlin_pro_proj3_w4",
               "qlin_pro_mlp_gate_up_quant_i8", "qlin_pro_mlp_gate_up_quant_w4",
               "qlin_gemm_i8", "qlin_gemm_i8_noalloc", "qlin_chain_bytes", "qlin_chain_init", "qlin_chain_run",
@@ -181,6 +181,43 @@ def test_chain_validation_without_gpu():
     assert L.qlin_chain_bytes((CH._Job * 1)(job(x=0x10008)), 1, 1) == 0
     assert b"aligned" in L.qlin_last_error()
     assert L.qlin_chain_bytes((CH._Job * 1)(job()), 1, 17) == 0
+
+
+def test_echain_validation_without_gpu():
+    """qlin_echain_bytes validates an engine chain on the host: the struct layout the
+    Python binding declares, the level rule, W8 and W4 jobs not mixed, rows 1-8, a W4
+    group that is not a multiple of 64, gate/up + quant needing N % 64 == 0, a producer
+    job that also names activations, and a bad producer (head size)."""
+    qlin, L = _lib()
+    from qwen35_amd.kernels import echain as EC
+    from qwen35_amd.kernels import fused as FU
+    EC._bind(L)
+
+    def job(kind=EC.QLIN_EJ_GEMM, level=0, group=0, K=2048, N=512, aq=0x10000, pro=None):
+        j = EC._EJob(kind=kind, a_q=aq, a_s=0x11000 if aq else None, K=K, N=N, group=group, w=0x20000,
+                     scale=0x30000, scale_dtype=qlin.QLIN_BF16, out=0x40000, ldo=N, level=level)
+        if kind != EC.QLIN_EJ_GEMM:
+            j.w2, j.scale2, j.out_q, j.out_s = 0x50000, 0x60000, 0x70000, 0x80000
+        if pro is not None:
+            j.pro = pro
+        return j
+
+    def nbytes(*jobs, M=4):
+        return L.qlin_echain_bytes((EC._EJob * len(jobs))(*jobs), len(jobs), M)
+
+    assert nbytes(job(), job(EC.QLIN_EJ_GATE_UP_QUANT, level=1, N=6144), job(level=2)) > 0
+    assert nbytes(job(), job(level=2)) == 0 and b"levels" in L.qlin_last_error()
+    assert nbytes(job(), job(group=128, level=1)) == 0 and b"W8 jobs or W4" in L.qlin_last_error()
+    assert nbytes(job(), M=9) == 0 and b"1-8" in L.qlin_last_error()
+    assert nbytes(job(group=96, K=2880)) == 0 and b"group" in L.qlin_last_error()
+    assert nbytes(job(EC.QLIN_EJ_GATE_UP_QUANT, N=528)) == 0 and b"N % 64" in L.qlin_last_error()
+    rms = FU._CProducer(kind=1, x=0x90000, ldx=2048, x_dtype=qlin.QLIN_BF16, g=None, ldg=0, w=0xA0000,
+                        w_dtype=qlin.QLIN_BF16, hd=0, one_plus=1, eps=1e-6, q=None, s=None)
+    assert nbytes(job(aq=None, pro=rms)) > 0
+    assert nbytes(job(pro=rms)) == 0 and b"a_q" in L.qlin_last_error()
+    ng = FU._CProducer(kind=3, x=0x90000, ldx=2048, x_dtype=qlin.QLIN_BF16, g=0xB0000, ldg=8192, w=0xA0000,
+                       w_dtype=qlin.QLIN_BF16, hd=64, one_plus=0, eps=1e-6, q=None, s=None)
+    assert nbytes(job(aq=None, pro=ng)) == 0 and b"head size 64" in L.qlin_last_error()
 
 
 def test_producer_validation_without_gpu():

@@ -7,8 +7,10 @@ a 700-token prompt runs as chunks of 512 + 188 (prefill_chunk = 512,
 engine.py:540-545), and a cached prefix ends on a multiple of 32 tokens
 (engine.py:567-570).  Every row of a call with at least 5 rows must therefore not
 depend on M, on the chunking, or on which kernel family the library picks for that
-M.  Calls with 1-4 rows are decode (one sequence, or up to four best-of rows,
-nodes.py:325-327) and have their own plans.
+M.  Calls with 1-8 rows are decode (one sequence, or up to eight best-of rows,
+engine.py:392) and run the decode work units, whose rows equal single-row calls
+instead (tests/test_gpu_echain.py): a chunk remainder of 1-8 rows agrees with the
+unchunked prefill within the GEMM tolerance, not bit for bit (tested below).
 """
 from __future__ import annotations
 
@@ -44,11 +46,11 @@ def _cu(t):
     return None if t is None else t.cuda()
 
 
-# (total rows, chunks): a 700-token prompt in chunks of 512, a 520-token one (its
-# remainder of 8 rows still above the decode sizes), and a cached 160-token prefix
-# (a multiple of 32) followed by the rest of the prompt
-CASES = [(700, ((0, 512), (512, 700))), (520, ((0, 512), (512, 520))), (700, ((0, 160), (160, 700)))]
-CASE_IDS = ["512+188", "512+8", "160+540"]
+# (total rows, chunks): a 700-token prompt in chunks of 512, a 521-token one (its
+# remainder of 9 rows the smallest above the decode sizes), and a cached 160-token
+# prefix (a multiple of 32) followed by the rest of the prompt
+CASES = [(700, ((0, 512), (512, 700))), (521, ((0, 512), (512, 521))), (700, ((0, 160), (160, 700)))]
+CASE_IDS = ["512+188", "512+9", "160+540"]
 
 
 def _run_gemm(a, as_, b, bs, bz, hid, m0, m1):
@@ -130,8 +132,8 @@ def test_gate_up_quant_chunked_equals_whole(kind, total, case):
 
 @pytest.mark.parametrize("kind", ["w8", "w4"])
 @pytest.mark.parametrize("K,N", [(2048, 2048), (6144, 2048), (2048, 6144)])
-def test_every_row_count_from_5_agrees(kind, K, N):
-    """Rows 0-4 of calls with M = 5, 8, 16, 17, 64, 130, 300 and 512 rows are the same
+def test_every_row_count_from_9_agrees(kind, K, N):
+    """Rows 0-8 of calls with M = 9, 16, 17, 64, 130, 300 and 512 rows are the same
     bits: the 16-row tiles (M <= 16 always, larger M where the time model prefers
     them) and the tiled int8 kernel fold K in one order."""
     gemm = _g()
@@ -139,12 +141,35 @@ def test_every_row_count_from_5_agrees(kind, K, N):
     a, as_ = H.engine_act(Mmax, K, seed=630 + K + N)
     b, bs, bz = _weights(kind, K, N, seed=631)
     ref = None
-    for M in (5, 8, 16, 17, 64, 130, 300, 512):
+    for M in (9, 16, 17, 64, 130, 300, 512):
         out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         gemm.gemm_i8(a[:M].cuda(), as_[:M].cuda(), b.cuda(), bs.cuda(), out, b_z=_cu(bz))
         if ref is None:
-            ref = out[:5].clone()
-        assert torch.equal(out[:5], ref), f"M={M}"
+            ref = out[:9].clone()
+        assert torch.equal(out[:9], ref), f"M={M}"
+
+
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+@pytest.mark.parametrize("rem", [1, 4, 8])
+def test_decode_sized_remainder_within_tolerance(kind, rem):
+    """A chunk remainder of 1-8 rows runs the decode work units (so that best-of rows
+    equal single rows): its rows agree with the unchunked call within the GEMM
+    tolerance, and both agree with the oracle."""
+    gemm = _g()
+    K, N, total = 2048, 2048, 512 + rem
+    a, as_ = H.engine_act(total, K, seed=640 + rem)
+    b, bs, bz = _weights(kind, K, N, seed=641)
+    whole = torch.empty((total, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), whole, b_z=_cu(bz))
+    tail = torch.empty((rem, N), dtype=torch.bfloat16, device="cuda")
+    gemm.gemm_i8(a[512:].contiguous().cuda(), as_[512:].contiguous().cuda(), b.cuda(), bs.cuda(), tail,
+                 b_z=_cu(bz))
+    if kind == "w8":
+        ref = R.gemm_i8_ref(a[512:].numpy(), as_[512:].numpy(), b.numpy(), bs.numpy())
+    else:
+        ref = R.gemm_w4_ref(a[512:].numpy(), as_[512:].numpy(), b.numpy(), H.np_(bs), bz.numpy())
+    H.assert_out_close(tail.cpu(), ref)
+    H.assert_out_close(whole[512:].cpu(), ref)
 
 
 @pytest.mark.parametrize("kind", ["w8", "w4"])

@@ -195,10 +195,11 @@ def test_mlp_gate_up_quant_w4(M, zeros, group):
 @pytest.mark.parametrize("plan", ["4,8,0", "8,4,0"])
 @pytest.mark.parametrize("M", [1, 2, 4])
 def test_engine_decode_forced_plans(plan, M, monkeypatch):
-    """One-pass 64-column tiles and split-K 128-column tiles for every engine call
-    kind (store + residual, proj3, gate/up + quant; W8 and W4), whatever the
-    default plan is for the shape (decode sizes: the plan override applies to calls
-    of at most 4 rows)."""
+    """The skinny decode plans (QLIN_ENGINE_DECODE=skinny; by default decode-sized
+    engine calls run the engine decode work units): one-pass 64-column tiles and
+    split-K 128-column tiles for every engine call kind (store + residual, proj3,
+    gate/up + quant; W8 and W4), whatever the default plan is for the shape."""
+    monkeypatch.setenv("QLIN_ENGINE_DECODE", "skinny")
     monkeypatch.setenv("QLIN_SKINNY_PLAN", plan)
     gemm, w4 = _g()
     K, N = 2048, 2048

@@ -5,9 +5,9 @@ the linears that run them in their own launch.
   producers' exp must equal the oracle bit for bit: int8 codes and fp32 scales.
 * A fused call (`kernels/fused.py`) must equal the two-call sequence it replaces --
   the standalone producer, then the engine-signature linear -- bit for bit, for every
-  plan family: decode plans (M = 1-4: one-pass 64-column tiles, split-K), two-wave
-  row tiles (M = 5-16), the tiled prefill kernel and wide launches (the producer then
-  runs as a launch of its own), with and without the optional code outputs.
+  plan family: the decode work units (M = 1-8, the producer in every unit's
+  prologue), two-wave row tiles (M = 9-16), the tiled prefill kernel (the producer
+  then runs as a launch of its own), with and without the optional code outputs.
 * The fused result is also within the GEMM tolerance of the oracle's fp32 result on
   the oracle's codes.
 Shapes are the engine's 2B-class layer (hidden 2048; engine.py:218-279).
