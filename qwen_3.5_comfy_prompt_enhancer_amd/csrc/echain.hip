@@ -39,7 +39,7 @@
 //     dependency wait; its weights come through a register ring of 2 blocks per wave
 //     issued before the wait, and the last ring cycle of a unit already loads the next
 //     unit's first blocks, so weights stream across unit boundaries.
-//   * Scheduling (persistent form): 8 queues hand out units in increasing order, and a
+//   * Scheduling (persistent form): 64 queues hand out units in increasing order, and a
 //     unit waits only for units of lower levels (bounded polls; a wait that gives up
 //     sets an error word), so every wait ends whether or not all workgroups are
 //     resident.  The last workgroup to leave resets the queues, counters and flags.
@@ -76,11 +76,11 @@ constexpr int KU_MAX = 2048;         // longest unit K range (its codes are stag
 constexpr int LDQ = KU_MAX + 16;     // LDS code row stride (16 bytes stagger the rows over banks)
 constexpr int kSpinLimit = 1 << 22;  // polls of a dependency before giving up
 constexpr int kWaitVm0 = 0x0F70;     // s_waitcnt vmcnt(0)
-constexpr int kQueues = 8;
+constexpr int kQueues = 64;             // unit queues, one counter per 128-byte line
 constexpr int kLevel0 = 32 * (kQueues + 1);
 constexpr int kPlanSlots = 768;      // resident workgroups the unit plan assumes (3 per CU x 256 CUs)
 constexpr int kLongFactor = 2;
-constexpr int kEPre = 2;             // producer: row chunks a lane loads ahead (registers are short)
+constexpr int kEPre = 4;             // producer: row chunks a lane loads ahead (all of a 2048-wide row)
 
 enum EEpi { EE_STORE = 0, EE_GATEUP = 1, EE_GATEUP_Q = 2 };
 
@@ -123,7 +123,8 @@ struct ESh {
   uint8_t q[EMAXM * LDQ];              // the unit's codes [row][K range]
   float s[(KU_MAX / 64) * 16];         // the unit's activation scales [block][row (16)]
   float lr[EMAXM];                     // producer: per-row inverse RMS
-  int unit, flag;
+  float cs[2 * TNC];                   // the tile's W8 column scales [set][column]
+  int unit, unit2, flag;
 };
 
 // Register ring of one wave: RB blocks of weights (W8: 16 K rows x 8 columns; W4: 8
@@ -173,21 +174,41 @@ __device__ __forceinline__ const uint8_t* set_w(const EJob& J, int set) {
   return set ? J.w[1] : J.w[0];
 }
 
+// What the ring loads of a unit need: its weight set and the wave's K range.  The
+// persistent form computes it for the next unit while the current one runs.
+struct ELoad {
+  const uint8_t* w;
+  const void* s;
+  const uint8_t* z;
+  int N, group, sdt, col0, k0, nblk;
+};
+
+__device__ __forceinline__ ELoad make_load(const EJob& J, const EPos& P) {
+  ELoad L;
+  L.w = P.set ? J.w[1] : J.w[0];
+  L.s = P.set ? J.s[1] : J.s[0];
+  L.z = P.set ? J.z[1] : J.z[0];
+  L.N = J.N;
+  L.group = J.group;
+  L.sdt = J.sdt;
+  L.col0 = P.tile * TNC;
+  wave_blocks(J, P, &L.k0, &L.nblk);
+  return L;
+}
+
 // Issues the loads of block b of the wave's range into ring slot `slot`.  Blocks past
 // the range load the range's last block again (or block 0 of the matrix when the wave
 // has none): every register of the slot is written.
 template <bool W4>
-__device__ __forceinline__ void load_block(const EJob& J, const EPos& P, int k0, int nblk, int b, ERing<W4>& R,
-                                           int slot) {
+__device__ __forceinline__ void load_block(const ELoad& L, int b, ERing<W4>& R, int slot) {
   constexpr int NR = ERing<W4>::NR;
   const int lane = etid() & 63, j = lane & 15, g = lane >> 4;
-  const int N = J.N;
-  const int col = P.tile * TNC + j * 8;
+  const int N = L.N;
+  const int col = L.col0 + j * 8;
   const int ccl = col < N ? col : 0;
-  const int kb = nblk > 0 ? k0 + 64 * min(b, nblk - 1) : 0;
-  const uint8_t* w = P.set ? J.w[1] : J.w[0];
+  const int kb = L.nblk > 0 ? L.k0 + 64 * min(b, L.nblk - 1) : 0;
   const long long r0 = W4 ? (long long)(kb / 2 + 8 * g) : (long long)(kb + 16 * g);
-  const uint8_t* base = w + r0 * N + ccl;
+  const uint8_t* base = L.w + r0 * N + ccl;
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const u32x2 v = ld_global_nt<u32x2>(base + (long long)r * N);
@@ -195,13 +216,12 @@ __device__ __forceinline__ void load_block(const EJob& J, const EPos& P, int k0,
     R.w[slot][r][1] = v.y;
   }
   if constexpr (W4) {
-    const long long idx = (long long)(kb / J.group) * N + ccl;
-    const bool f32 = J.sdt == DT_F32;
-    const uint8_t* sb = (const uint8_t*)(P.set ? J.s[1] : J.s[0]) + idx * (f32 ? 4 : 2);
+    const long long idx = (long long)(kb / L.group) * N + ccl;
+    const bool f32 = L.sdt == DT_F32;
+    const uint8_t* sb = (const uint8_t*)L.s + idx * (f32 ? 4 : 2);
     R.sraw[slot][0] = ld_global<u32x4>(sb);
     R.sraw[slot][1] = ld_global<u32x4>(sb + (f32 ? 16 : 0));
-    const uint8_t* zp = P.set ? J.z[1] : J.z[0];
-    const u32x2 zv = ld_global<u32x2>(zp ? zp + idx : sb);
+    const u32x2 zv = ld_global<u32x2>(L.z ? L.z + idx : sb);
     R.zr[slot][0] = zv.x;
     R.zr[slot][1] = zv.y;
   }
@@ -350,11 +370,61 @@ __device__ __forceinline__ unsigned* level_flag(uint8_t* plan, const EHdr& H, in
   return (unsigned*)(plan + H.flag_off) + 32 * l;
 }
 
+// What the epilogue reads from memory, loaded ahead so that it is not on the critical
+// path after the split-K exchange: the W8 column scales of the thread's 4 columns (both
+// weight sets; constant, loaded at the unit's start) and its residual (written by an
+// earlier level, so loaded after the dependency wait).  Thread c's chunk is row c / 32,
+// columns 4 (c % 32) of the tile.
+struct EEpiPre {
+  uint32_t csr;  // raw bits of thread t's column scale: set t / 128, column t % 128
+  u32x2 rv;
+};
+
+__device__ __forceinline__ void epi_chunk(const EJob& J, const EPos& P, int M, int* row, int* gc, bool* valid) {
+  const int nch = M * (TNC / 4);
+  const int c = etid();
+  const int cc = c < nch ? c : nch - 1;
+  *row = cc >> 5;
+  *gc = P.tile * TNC + (cc & 31) * 4;
+  *valid = c < nch && *gc < J.N;
+}
+
+template <bool W4>
+__device__ __forceinline__ void epi_prefetch_scales(const EJob& J, const EPos& P, EEpiPre& e) {
+  e.csr = 0u;
+  if constexpr (!W4) {
+    const int t = etid();
+    const int set = (t >> 7) < J.nsets ? (t >> 7) : 0;
+    const int col = min(P.tile * TNC + (t & (TNC - 1)), J.N - 1);
+    e.csr = ld_scale1_raw(set ? J.s[1] : J.s[0], J.sdt, col);
+  }
+}
+
+// The column scales into LDS (before a barrier that precedes the epilogue).
+template <bool W4>
+__device__ __forceinline__ void epi_scales_to_lds(const EJob& J, const EPos& P, const EEpiPre& e, ESh& sh) {
+  if constexpr (!W4) {
+    const int t = etid();
+    const int col = min(P.tile * TNC + (t & (TNC - 1)), J.N - 1);
+    sh.cs[t] = cvt_scale1(e.csr, J.sdt, col);
+  }
+}
+
+__device__ __forceinline__ void epi_prefetch_res(const EJob& J, const EPos& P, int M, EEpiPre& e) {
+  int row, gc;
+  bool valid;
+  epi_chunk(J, P, M, &row, &gc, &valid);
+  const __amdgpu_buffer_rsrc_t rr =
+      part_rsrc(J.res ? J.res : J.out, (unsigned)(((long long)(M - 1) * (J.res ? J.ldr : J.ldo) + J.N) * 2));
+  e.rv = bitcast<u32x2>(__builtin_amdgcn_raw_buffer_load_b64(
+      rr, (valid && J.res) ? (unsigned)(((long long)row * J.ldr + gc) * 2) : 0xFFFFFFF0u, 0, kCpolSc1));
+}
+
 // The part of a unit after its K loop: wave sums, K-split / weight-set exchange,
 // epilogue.  Returns whether this unit finished its tile (it ran the epilogue).
 template <bool W4>
 __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M, f32x4 (&acc)[8], ESh& sh,
-                                            float* part_base, unsigned* cnt_base) {
+                                            float* part_base, unsigned* cnt_base, const EEpiPre& pre) {
   const int tid = etid(), wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
   const int nch = M * (TNC / 4);
   const long long MT = (long long)M * TNC;
@@ -431,17 +501,19 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
 #pragma unroll
     for (int e = 0; e < 4; ++e) cs[s][e] = 1.0f;
   if constexpr (!W4) {
-    cvt_scale4_nb(ld_scale4_raw(J.s[0], J.sdt, gcl), J.sdt, cs[0]);
-    cvt_scale4_nb(ld_scale4_raw(J.nsets == 2 ? J.s[1] : J.s[0], J.sdt, gcl), J.sdt, cs[1]);
+    const int lc = (cc & 31) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      cs[0][e] = sh.cs[lc + e];
+      cs[1][e] = sh.cs[TNC + lc + e];
+    }
   }
+  (void)gcl;
   if (J.epi == EE_STORE) {
     float y[4];
     const __amdgpu_buffer_rsrc_t orr = part_rsrc(J.out, (unsigned)(((long long)(M - 1) * J.ldo + N) * 2));
     if (J.res) {
-      const __amdgpu_buffer_rsrc_t rr = part_rsrc(J.res, (unsigned)(((long long)(M - 1) * J.ldr + N) * 2));
-      const u32x2 rv = bitcast<u32x2>(__builtin_amdgcn_raw_buffer_load_b64(
-          rr, valid ? (unsigned)(((long long)row * J.ldr + gc) * 2) : 0xFFFFFFF0u, 0, kCpolSc1));
-      const uint32_t rw[2] = {rv.x, rv.y};
+      const uint32_t rw[2] = {pre.rv.x, pre.rv.y};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint16_t h = (uint16_t)(rw[e >> 1] >> (16 * (e & 1)));
@@ -530,8 +602,8 @@ template <bool W4, typename Before, typename Next>
 __device__ __forceinline__ void unit_loop(const EJob& J, const EPos& P, int M, ERing<W4>& R, const ESh& sh,
                                           f32x4 (&acc)[8], Before&& before_last, Next&& refill_next) {
   const int wave = etid() >> 6;
-  int k0, nblk;
-  wave_blocks(J, P, &k0, &nblk);
+  const ELoad Ld = make_load(J, P);
+  const int nblk = Ld.nblk;
   const int ncyc = J.wblk / RB;
   const bool hz = J.hz != 0;
 #pragma unroll
@@ -547,7 +619,7 @@ __device__ __forceinline__ void unit_loop(const EJob& J, const EPos& P, int M, E
     for (int s = 0; s < RB; ++s) {
       block(RB * cyc + s, s);
       __builtin_amdgcn_sched_barrier(0);
-      load_block<W4>(J, P, k0, nblk, RB * (cyc + 1) + s, R, s);
+      load_block<W4>(Ld, RB * (cyc + 1) + s, R, s);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -578,26 +650,31 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
   const int kbase = P.split * ku;
   const int kuu = min(ku, J.K - kbase);
   ERing<W4> R;
-  int k0, nblk;
-  wave_blocks(J, P, &k0, &nblk);
+  const ELoad Ld = make_load(J, P);
+  EEpiPre pre;
   if (J.pro.kind != PRO_NONE) {
 #pragma unroll
-    for (int s = 0; s < RB; ++s) load_block<W4>(J, P, k0, nblk, s, R, s);
+    for (int s = 0; s < RB; ++s) load_block<W4>(Ld, s, R, s);
+    epi_prefetch_scales<W4>(J, P, pre);
+    epi_prefetch_res(J, P, M, pre);
     stage_producer(J, P, M, kbase, kuu, sh);
   } else {
     EStage st;
     stage_issue(J, M, kbase, kuu, st);
 #pragma unroll
-    for (int s = 0; s < RB; ++s) load_block<W4>(J, P, k0, nblk, s, R, s);
+    for (int s = 0; s < RB; ++s) load_block<W4>(Ld, s, R, s);
+    epi_prefetch_scales<W4>(J, P, pre);
+    epi_prefetch_res(J, P, M, pre);
     stage_store(M, kuu, st, sh);
     __syncthreads();
   }
+  epi_scales_to_lds<W4>(J, P, pre, sh);  // read after the wave-sum barrier
   f32x4 acc[8];
   unit_loop<W4>(J, P, M, R, sh, acc, []() {}, [](int) {});
-  unit_finish<W4>(J, P, M, acc, sh, a.part, a.cnt);
+  unit_finish<W4>(J, P, M, acc, sh, a.part, a.cnt, pre);
 }
 
-// Persistent chain: workgroup b takes units from queue b % 8 until the plan runs out.
+// Persistent chain: workgroup b takes units from queue b % 64 until the plan runs out.
 template <bool W4>
 __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void echain_kernel(
     uint8_t* plan, const EJob* __restrict__ jobs, const int* __restrict__ unit_job, const unsigned* __restrict__ need) {
@@ -609,27 +686,47 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
   const int M = H.M;
   const int q = (int)(blockIdx.x % kQueues);
   unsigned* const queue = cnt + 32 * q;
-  if (tid == 0) sh.unit = (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kQueues + q;
+  auto take = [&]() {
+    return (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kQueues + q;
+  };
+  // A workgroup holds two units from its queue: the one it runs and the next, whose
+  // descriptor is then read before the current unit's dependency wait.  Queues hand
+  // their units out in increasing order, so the smallest unfinished unit is always
+  // some workgroup's current unit and never waits.
+  if (tid == 0) {
+    sh.unit = take();
+    sh.unit2 = take();
+  }
   __syncthreads();
   int u = sh.unit;
+  int un = sh.unit2;
   ERing<W4> R;
   int jn = 0;
   EPos P;
   if (u < H.nunits) {
     jn = __builtin_amdgcn_readfirstlane(unit_job[u]);
     P = unit_pos(jobs[jn], jn, u);
-    int k0, nblk;
-    wave_blocks(jobs[jn], P, &k0, &nblk);
+    const ELoad L0 = make_load(jobs[jn], P);
 #pragma unroll
-    for (int s = 0; s < RB; ++s) load_block<W4>(jobs[jn], P, k0, nblk, s, R, s);
+    for (int s = 0; s < RB; ++s) load_block<W4>(L0, s, R, s);
   }
   while (u < H.nunits) {
-    int nxt = 0;
-    if (tid == 0) nxt = (int)__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * kQueues + q;
+    // the unit after the next one: taken now, read at the next unit's start
+    int nn = 0;
+    if (tid == 0) nn = take();
     const EJob& J = jobs[jn];
     const int ku = EW * J.wblk * 64;
     const int kbase = P.split * ku;
     const int kuu = min(ku, J.K - kbase);
+
+    // ---- the next unit's descriptor (past the last unit: this job's first unit, whose
+    // first rows the last ring cycle then reads again from L2, with no branch) ----
+    const bool more = un < H.nunits;
+    const int jnn = more ? __builtin_amdgcn_readfirstlane(unit_job[un]) : jn;
+    const EPos Pn = unit_pos(jobs[jnn], jnn, more ? un : jobs[jnn].unit0);
+    const ELoad Ln = make_load(jobs[jnn], Pn);
+    EEpiPre pre;
+    epi_prefetch_scales<W4>(J, P, pre);
 
     // ---- dependency: level L waits for every tile of level L - 1 ----
     if (J.level > 0) {
@@ -649,6 +746,7 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
       }
       __syncthreads();
     }
+    epi_prefetch_res(J, P, M, pre);
 
     // ---- activations into LDS ----
     if (J.pro.kind != PRO_NONE) {
@@ -660,24 +758,14 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
       stage_store(M, kuu, st, sh);
       __syncthreads();
     }
+    // (written after the staging's loads, so that their wait does not precede them; read
+    // after the wave-sum barrier)
+    epi_scales_to_lds<W4>(J, P, pre, sh);
 
-    // ---- K loop; its last cycle loads the next unit's first blocks ----
-    int un = 0, jnn = jn;
-    EPos Pn = P;
-    int k0n = 0, nblkn = 0;
-    auto publish = [&]() {
-      if (tid == 0) sh.unit = nxt;
-      __syncthreads();
-      un = (int)__builtin_amdgcn_readfirstlane((uint32_t)sh.unit);
-      const bool more = un < H.nunits;
-      jnn = more ? __builtin_amdgcn_readfirstlane(unit_job[un]) : jn;
-      Pn = unit_pos(jobs[jnn], jnn, more ? un : jobs[jnn].unit0);
-      wave_blocks(jobs[jnn], Pn, &k0n, &nblkn);
-    };
-    auto refill_next = [&](int s) { load_block<W4>(jobs[jnn], Pn, k0n, nblkn, s, R, s); };
+    // ---- K loop ----
     f32x4 acc[8];
-    unit_loop<W4>(J, P, M, R, sh, acc, publish, refill_next);
-    const bool fin = unit_finish<W4>(J, P, M, acc, sh, part, cnt + kLevel0 + 32 * H.nlevels);
+    unit_loop<W4>(J, P, M, R, sh, acc, []() {}, [](int) {});
+    const bool fin = unit_finish<W4>(J, P, M, acc, sh, part, cnt + kLevel0 + 32 * H.nlevels, pre);
 
     // ---- the tile counts for its level; the level's last tile sets the flag ----
     if (fin && J.level + 1 < H.nlevels) {
@@ -692,10 +780,18 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
           __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    // ---- the next unit's first blocks.  Issued only now: gfx950 counts loads and
+    // stores on one in-order counter, so weight loads issued before this unit's
+    // partial and output stores would make every wait for those stores (on the path
+    // to the next level) wait for the weights as well. ----
+#pragma unroll
+    for (int s = 0; s < RB; ++s) load_block<W4>(Ln, s, R, s);
+    if (tid == 0) sh.unit2 = nn;
     __syncthreads();
     jn = jnn;
     P = Pn;
     u = un;
+    un = (int)__builtin_amdgcn_readfirstlane((uint32_t)sh.unit2);
   }
   // the last workgroup to leave resets the queues, level counters and flags, and
   // publishes this launch's error word
