@@ -80,7 +80,9 @@ int qlin_gemm_i8(const int8_t* a_q, const float* a_s, int M, int K,
  * and a prefill call whose partials exceed it runs in blocks of rows (rows are
  * independent).  A call that cannot fit even one block of rows fails with
  * QLIN_ERR_WORKSPACE before launching anything.  Calls that overlap in time on one
- * GPU share the array and race: serialize them (one stream, or the engine's lock). */
+ * GPU share the array and race: serialize them (one stream, or the engine's lock).
+ * The replay of a HIP graph that holds a call is a call: it must not overlap another
+ * call or replay on the same GPU either (streams do not separate them). */
 int qlin_gemm_i8_noalloc(const int8_t* a_q, const float* a_s, int M, int K,
                          const int8_t* b, const void* b_s, int bs_dtype, int N,
                          void* out, int64_t ldo, const void* residual, int64_t ldr,
@@ -318,8 +320,9 @@ int qlin_chain_init(const qlin_chain_job* jobs, int njobs, int M, void* plan, si
 
 /* Runs every job of the plan in one launch on `stream`, asynchronously; capturable
  * in a HIP graph.  The plan's counters return to zero when the launch ends.  Launches
- * of one plan must not overlap in time.  The int at byte offset 20 of the plan
- * becomes nonzero if a dependency wait gave up (it polls about 4 M times). */
+ * of one plan must not overlap in time.  The int at byte offset 20 of the plan is 1
+ * after a launch in which a dependency wait gave up (it polls about 4 M times), 0
+ * otherwise; it describes the last finished launch. */
 int qlin_chain_run(void* plan, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -16,11 +16,12 @@
 //     q, q + 8, ... in order; the next index is fetched while the current unit runs),
 //     so a unit only ever waits for units of lower levels, all taken before it: every
 //     wait ends whether or not all workgroups are resident.
-//   * A unit issues all of its weight (and scale, zero) loads first, then, above level
-//     0, waits for the level below (one thread polls the level's done flag with a
-//     bounded spin), then reads its activations with device-coherent loads (level 0:
-//     issued with the weights).  The next unit's loads go out as soon as this unit's
-//     partial stores have completed.
+//   * A unit's weight (and scale, zero) loads are in flight before it waits: above
+//     level 0 it waits for the level below (one thread polls the level's done flag with
+//     a bounded spin), then reads its activations with device-coherent loads (level 0:
+//     issued with the weights).  The last ring cycle of a unit refills each slot with
+//     the next unit's first step as soon as the slot's MFMAs are issued, so a wave's
+//     loads stay in flight across the unit boundary.
 //   * Each wave computes its 128-row K range for the tile's 128 columns on
 //     v_mfma_f32_16x16x32_f16 with exactly converted weights (the skinny decode
 //     kernel's operand construction: qlin_dev.h w8_pair_f16 / w4_pair_offset with the
@@ -31,11 +32,14 @@
 //     residual (one fmaf), and stores the 16-bit output with device-coherent stores.
 //     After those stores complete it counts the tile for its level, and the level's
 //     last tile sets the level's flag.
-//   * The K order of an output depends on (K, N) only, so rows of an M = 4 step equal
-//     an M = 1 step bit for bit.
+//   * The K order of an output depends on (K, N) and on the size of the job's level
+//     (levels with many units take longer units), never on M: rows of an M = 4 chain
+//     equal an M = 1 chain of the same jobs bit for bit, but the same linear in a chain
+//     of other levels (or another layer count) may differ in the last bits.
 //   * The last workgroup to leave resets the queues, the exit and level counters and
 //     the flags, so a plan can be launched again (and replayed in a HIP graph) without
-//     clearing.
+//     clearing, and publishes the launch's error word (a dependency wait that gave up):
+//     the header's `err` always describes the last finished launch.
 #include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -90,6 +94,8 @@ struct alignas(16) ChainHdr {
   int magic, nunits, njobs, nlevels;
   int M, err, ncnt, w4;
   long long jobs_off, unit_off, need_off, cnt_off, flag_off, part_off, bytes;
+  int err_run;  // set by a wait that gives up during a launch; moved to `err` at its end
+  int pad_[3];
 };
 constexpr int kMagic = 0x71636831;  // "qch1"
 
@@ -359,7 +365,8 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
         int spins = 0, nap = 1;
         while (ld_agent(f) == 0u) {
           if (++spins > kSpinLimit) {
-            __hip_atomic_store((int*)(plan + offsetof(ChainHdr, err)), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store((int*)(plan + offsetof(ChainHdr, err_run)), 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
           if (nap == 1) __builtin_amdgcn_s_sleep(1);
@@ -688,6 +695,10 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
       }
       for (int qq = 0; qq < kQueues; ++qq) __hip_atomic_store(cnt + 32 * qq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(cnt + 32 * kQueues, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int* const er = (int*)(plan + offsetof(ChainHdr, err_run));
+      const int e = __hip_atomic_load(er, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store((int*)(plan + offsetof(ChainHdr, err)), e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(er, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

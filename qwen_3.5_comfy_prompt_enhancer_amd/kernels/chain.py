@@ -1,23 +1,26 @@
-"""Decode chains: the A16 linears of a whole decode step in one persistent launch.
+"""Decode chains: many A16 linears in one persistent launch.
 
 The reference launches one kernel per linear and names whole-step decode capture as
 its next step, since decode is dispatch-bound (ENGINEERING.md:383-399).  A
 `DecodeChain` holds a list of linears -- each one what `linear_w8` / `linear_w4`
-computes -- with dependency levels, and `run()` computes all of them in one launch of
-libqlin.so's chain kernel:
+computes, with fp16 activations -- with dependency levels, and `run()` computes all of
+them in one launch of libqlin.so's chain kernel.  Every input of a job must be written
+before `run()` or be the output of a job of a lower level; anything that is not a
+linear (attention, a norm, an activation function) ends a chain.  For example, the
+independent GEMVs of a decode sweep, then a projection of one of their outputs:
 
     chain = DecodeChain(M=1)
-    chain.add(x, wq, sq, q_out)                        # level 0
-    chain.add(x, wk, sk, k_out)                        # level 0
-    chain.add(attn_out, wo, so, h, residual=h, level=1) # waits for level 0
+    chain.add(x, wq, sq, q_out)                         # level 0: x written before run()
+    chain.add(x, wk, sk, k_out)                         # level 0
+    chain.add(q_out, wp, sp, p_out, level=1)            # reads q_out, written by level 0
     chain.build()
-    chain.run()                                        # every job, one launch
+    chain.run()                                         # every job, one launch
 
-Jobs of level L > 0 read their activations only after every job of level L - 1 has
-written its output, so a job may consume another job's output.  Levels start at 0
-and rise by at most 1 along the list.  The tensors are bound when `build()` runs:
-write new inputs into the same tensors and call `run()` again (a HIP graph may
-capture `run()`).  W4 jobs take group-128 scales.
+The engine's own decode step holds int8 activations and producers between its linears:
+it runs on `kernels/echain.py` `EngineChain` instead.  Levels start at 0 and rise by at
+most 1 along the list.  The tensors are bound when `build()` runs: write new inputs
+into the same tensors and call `run()` again (a HIP graph may capture `run()`).  W4
+jobs take group-128 scales.
 """
 from __future__ import annotations
 
@@ -141,8 +144,16 @@ class DecodeChain:
                 "qlin_chain_run")
 
     def wait_error(self) -> int:
-        """Nonzero if a dependency wait of a finished launch gave up (reads device memory)."""
+        """1 if a dependency wait of the last finished launch gave up, else 0 (reads device
+        memory; synchronizes with the current stream)."""
         return int(self.plan[20:24].view(torch.int32).item())
+
+    def run_checked(self):
+        """run(), then wait for it and raise if a dependency wait gave up."""
+        self.run()
+        if self.wait_error():
+            raise RuntimeError("decode chain: a dependency wait gave up (a job read inputs that no lower level "
+                               "wrote in time)")
 
     @property
     def nbytes(self) -> int:
