@@ -29,20 +29,22 @@
 //     in fp32 (kernels/gemm.py:43-45); W4 nibbles enter as int8 16 * (n - 8) and fold
 //     against a_s * b_s[group] / 16, explicit zeros add (8 - z) * sum(a)
 //     (kernels/w4.py:64-104).  Waves are summed in LDS in wave order, K splits in
-//     split order (device-coherent partials, arrival counter), then the W8 column scale
-//     and the residual in one fmaf, or the gate/up epilogue silu(g) * u -> bf16 ->
-//     per-64 max(amax / 127, 1e-8) -> round half away from zero (gemm.py:195-211).
-//     gate and up are separate units of one tile; the tile's last arrival runs the
-//     epilogue.
+//     split order (device-coherent partials), then the W8 column scale and the
+//     residual in one fmaf, or the gate/up epilogue silu(g) * u -> bf16 -> per-64
+//     max(amax / 127, 1e-8) -> round half away from zero (gemm.py:195-211).  gate and
+//     up are separate units of one tile.  In a single call the tile's last arrival at
+//     a counter runs the epilogue; in the chain the tile's last unit does, polling its
+//     partners' slots (unit_finish).
 //   * Activations: each unit stages its rows' codes and scales of its K range in LDS
 //     (device-coherent loads, or the producer, producers.h pro_block<true>), after its
 //     dependency wait; its weights come through a register ring of 2 blocks per wave
-//     issued before the wait, and the last ring cycle of a unit already loads the next
-//     unit's first blocks, so weights stream across unit boundaries.
+//     issued before the wait (in the chain: right after the previous unit's exchange
+//     and epilogue, so that they stream while the workgroup waits).
 //   * Scheduling (persistent form): 64 queues hand out units in increasing order, and a
-//     unit waits only for units of lower levels (bounded polls; a wait that gives up
-//     sets an error word), so every wait ends whether or not all workgroups are
-//     resident.  The last workgroup to leave resets the queues, counters and flags.
+//     unit waits only for units of lower levels, through a flag per level that the
+//     level's last tile sets (bounded polls; a wait that gives up sets an error word),
+//     so every wait ends whether or not all workgroups are resident.  The last
+//     workgroup to leave resets the queues, counts and flags.
 #include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -124,6 +126,7 @@ struct ESh {
   float s[(KU_MAX / 64) * 16];         // the unit's activation scales [block][row (16)]
   float lr[EMAXM];                     // producer: per-row inverse RMS
   float cs[2 * TNC];                   // the tile's W8 column scales [set][column]
+  u32x2 rv[ET];                        // thread t's residual chunk
   int unit, unit2, flag;
 };
 
@@ -366,15 +369,18 @@ __device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Level l's flag, set by its last tile.  (Waiting units poll this word, not the level's
+// count: polls of the word that the tiles' atomics update slow those atomics down.)
 __device__ __forceinline__ unsigned* level_flag(uint8_t* plan, const EHdr& H, int l) {
   return (unsigned*)(plan + H.flag_off) + 32 * l;
 }
 
-// What the epilogue reads from memory, loaded ahead so that it is not on the critical
-// path after the split-K exchange: the W8 column scales of the thread's 4 columns (both
-// weight sets; constant, loaded at the unit's start) and its residual (written by an
-// earlier level, so loaded after the dependency wait).  Thread c's chunk is row c / 32,
-// columns 4 (c % 32) of the tile.
+
+// What the epilogue of a single call reads from memory, loaded ahead so that it is not
+// on the critical path after the split-K exchange: the W8 column scale of thread t
+// (set t / 128, column t % 128) and the residual of thread c's chunk (row c / 32,
+// columns 4 (c % 32) of the tile).  (The chain's finisher loads them with its partial
+// reads instead.)
 struct EEpiPre {
   uint32_t csr;  // raw bits of thread t's column scale: set t / 128, column t % 128
   u32x2 rv;
@@ -400,14 +406,16 @@ __device__ __forceinline__ void epi_prefetch_scales(const EJob& J, const EPos& P
   }
 }
 
-// The column scales into LDS (before a barrier that precedes the epilogue).
+// The column scales and the residual into LDS (before a barrier that precedes the
+// epilogue): held in registers through the K loop, they would be spilled.
 template <bool W4>
-__device__ __forceinline__ void epi_scales_to_lds(const EJob& J, const EPos& P, const EEpiPre& e, ESh& sh) {
+__device__ __forceinline__ void epi_pre_to_lds(const EJob& J, const EPos& P, const EEpiPre& e, ESh& sh) {
+  const int t = etid();
   if constexpr (!W4) {
-    const int t = etid();
     const int col = min(P.tile * TNC + (t & (TNC - 1)), J.N - 1);
     sh.cs[t] = cvt_scale1(e.csr, J.sdt, col);
   }
+  sh.rv[t] = e.rv;
 }
 
 __device__ __forceinline__ void epi_prefetch_res(const EJob& J, const EPos& P, int M, EEpiPre& e) {
@@ -420,11 +428,57 @@ __device__ __forceinline__ void epi_prefetch_res(const EJob& J, const EPos& P, i
       rr, (valid && J.res) ? (unsigned)(((long long)row * J.ldr + gc) * 2) : 0xFFFFFFF0u, 0, kCpolSc1));
 }
 
+// A partial-sum slot of the persistent chain holds -0.0 in every word until its unit
+// stores its part.  A part is never -0.0: every sum starts from +0.0, and a rounded
+// sum or fused multiply-add is -0.0 only when its addend is.
+constexpr uint32_t kEmptyPart = 0x80000000u;
+
+__device__ __forceinline__ bool part_empty(f32x4 v) {
+  const u32x4 b = bitcast<u32x4>(v);
+  return b.x == kEmptyPart || b.y == kEmptyPart || b.z == kEmptyPart || b.w == kEmptyPart;
+}
+
+// The unit of a tile that runs its epilogue in the persistent chain: the tile's last
+// (set, split), whose unit number is the tile's largest.
+__device__ __forceinline__ bool unit_is_finisher(const EJob& J, const EPos& P) {
+  return P.set == J.nsets - 1 && P.split == J.splits - 1;
+}
+
+// The chain's finisher empties its partners' slots for the next launch (after its level
+// count, off the tile's path).
+__device__ __forceinline__ void empty_parts(const EJob& J, const EPos& P, int M, float* part_base) {
+  const int c = etid();
+  const long long MT = (long long)M * TNC;
+  if (!J.xch || c >= M * (TNC / 4)) return;
+  const int S = J.splits, NSx = J.nsets;
+  const __amdgpu_buffer_rsrc_t pr =
+      part_rsrc(part_base + J.part, (unsigned)((long long)J.ntiles * NSx * S * MT * 4));
+  // (made here: hoisted out of the persistent loop, the constant would be spilled)
+  uint32_t em;
+  asm volatile("v_bfrev_b32 %0, 1" : "=v"(em));  // kEmptyPart
+  const f32x4 empty = bitcast<f32x4>(u32x4{em, em, em, em});
+  for (int s = 0; s < NSx; ++s)
+    for (int p = 0; p < S; ++p)
+      if (!(s == NSx - 1 && p == S - 1))
+        st_coherent(empty, pr, (unsigned)(((((long long)P.tile * NSx + s) * S + p) * MT + c * 4) * 4));
+}
+
 // The part of a unit after its K loop: wave sums, K-split / weight-set exchange,
 // epilogue.  Returns whether this unit finished its tile (it ran the epilogue).
-template <bool W4>
+//
+// Two exchanges give the same sums in the same order (per set, split 0 + split 1 + ...):
+//  * single calls (POLL false): every part is stored, the stores are waited for, an
+//    arrival counter per tile picks the last arrival, which reads and sums the parts;
+//  * the persistent chain (POLL true): the tile's finisher unit (unit_is_finisher)
+//    polls its partners' slots in the plan until none is empty and sums them with its
+//    own part (kept in registers); empty_parts() empties them for the next launch.  The others
+//    store their part and go on without waiting.  One memory round trip on the
+//    tile's path instead of three (store completion, counter, reads).  The finisher's
+//    partners have smaller unit numbers, so the smallest unfinished unit of the chain
+//    never polls for a part that no workgroup holds.
+template <bool W4, bool POLL = false>
 __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M, f32x4 (&acc)[8], ESh& sh,
-                                            float* part_base, unsigned* cnt_base, const EEpiPre& pre) {
+                                            float* part_base, unsigned* cnt_base, int* err_run = nullptr) {
   const int tid = etid(), wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
   const int nch = M * (TNC / 4);
   const long long MT = (long long)M * TNC;
@@ -439,6 +493,27 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
   f32x4 v[2];  // the tile's sums: [set 0, set 1] of chunk tid (row tid / 32, columns 4 (tid % 32))
   v[0] = v[1] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int c = tid;  // nch <= 256
+  // the thread's epilogue chunk (row, 4 columns)
+  const int N = J.N;
+  const int cc = c < nch ? c : nch - 1;  // every thread takes part in the amax shuffles
+  const int row = cc >> 5, gc = P.tile * TNC + (cc & 31) * 4;
+  const bool valid = c < nch && gc < N;
+  const int gcl = gc < N ? gc : N - 4;
+  // The chain's finisher loads its epilogue inputs (residual, W8 column scales) with
+  // its first reads of the partners' parts, in the same round trip; single calls load
+  // them ahead, into LDS.
+  u32x2 rvv = u32x2{0u, 0u};
+  u32x4 csr[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  const auto load_epi_in = [&]() {
+    const __amdgpu_buffer_rsrc_t rr =
+        part_rsrc(J.res ? J.res : J.out, (unsigned)(((long long)(M - 1) * (J.res ? J.ldr : J.ldo) + N) * 2));
+    rvv = bitcast<u32x2>(__builtin_amdgcn_raw_buffer_load_b64(
+        rr, (valid && J.res) ? (unsigned)(((long long)row * J.ldr + gc) * 2) : 0xFFFFFFF0u, 0, kCpolSc1));
+    if constexpr (!W4) {
+      csr[0] = ld_scale4_raw(J.s[0], J.sdt, gcl);
+      csr[1] = ld_scale4_raw(J.nsets > 1 ? J.s[1] : J.s[0], J.sdt, gcl);
+    }
+  };
   if (c < nch) {
     const int row = c >> 5, cc = (c & 31) * 4;
     f32x4 sum = *(const f32x4*)&sh.red[row * TNP + cc];
@@ -447,7 +522,55 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
     v[0] = sum;
   }
   bool finish = true;
-  if (J.xch) {
+  if (POLL && J.xch) {
+    const int S = J.splits, NSx = J.nsets;
+    float* const part = part_base + J.part;
+    const __amdgpu_buffer_rsrc_t pr = part_rsrc(part, (unsigned)((long long)J.ntiles * NSx * S * MT * 4));
+    const auto slot = [&](int s, int p) {
+      return (unsigned)(((((long long)P.tile * NSx + s) * S + p) * MT + c * 4) * 4);
+    };
+    if (!unit_is_finisher(J, P)) {
+      if (c < nch) st_coherent(v[0], pr, slot(P.set, P.split));
+      return false;
+    }
+    load_epi_in();
+    if (c < nch) {
+      const f32x4 mine = v[0];
+      bool late = false;
+      for (int s = 0; s < NSx; ++s) {
+        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int p0 = 0; p0 < S; p0 += 8) {
+          f32x4 pp[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) pp[q] = ld_coherent(pr, slot(s, min(p0 + q, S - 1)));
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int p = p0 + q;
+            if (p < S) {
+              if (s == NSx - 1 && p == S - 1) {
+                pp[q] = mine;
+              } else {
+                int spins = 0;
+                while (part_empty(pp[q])) {
+                  if (++spins > kSpinLimit) {
+                    late = true;
+                    break;
+                  }
+                  __builtin_amdgcn_s_sleep(1);
+                  pp[q] = ld_coherent(pr, slot(s, p));
+                }
+              }
+              sum = (p == 0) ? pp[q] : sum + pp[q];
+            }
+          }
+        }
+        v[s] = sum;
+      }
+      if (late && err_run) __hip_atomic_store(err_run, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else if (POLL) {
+    load_epi_in();
+  } else if (J.xch) {
     // every (set, split) of the tile stores its sums; the last to arrive sums them in
     // split order per set
     const int S = J.splits, NSx = J.nsets;
@@ -490,30 +613,30 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
   if (!finish) return false;
 
   // ---------------- epilogue ----------------
-  const int N = J.N;
-  const int cc = c < nch ? c : nch - 1;  // every thread takes part in the amax shuffles
-  const int row = cc >> 5, gc = P.tile * TNC + (cc & 31) * 4;
-  const bool valid = c < nch && gc < N;
-  const int gcl = gc < N ? gc : N - 4;
   float cs[2][4];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int e = 0; e < 4; ++e) cs[s][e] = 1.0f;
   if constexpr (!W4) {
-    const int lc = (cc & 31) * 4;
+    if constexpr (POLL) {
+      cvt_scale4_nb(csr[0], J.sdt, cs[0]);
+      cvt_scale4_nb(csr[1], J.sdt, cs[1]);
+    } else {
+      const int lc = (cc & 31) * 4;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      cs[0][e] = sh.cs[lc + e];
-      cs[1][e] = sh.cs[TNC + lc + e];
+      for (int e = 0; e < 4; ++e) {
+        cs[0][e] = sh.cs[lc + e];
+        cs[1][e] = sh.cs[TNC + lc + e];
+      }
     }
   }
-  (void)gcl;
   if (J.epi == EE_STORE) {
     float y[4];
     const __amdgpu_buffer_rsrc_t orr = part_rsrc(J.out, (unsigned)(((long long)(M - 1) * J.ldo + N) * 2));
     if (J.res) {
-      const uint32_t rw[2] = {pre.rv.x, pre.rv.y};
+      const u32x2 rv = POLL ? rvv : sh.rv[c];
+      const uint32_t rw[2] = {rv.x, rv.y};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint16_t h = (uint16_t)(rw[e >> 1] >> (16 * (e & 1)));
@@ -668,10 +791,10 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
     stage_store(M, kuu, st, sh);
     __syncthreads();
   }
-  epi_scales_to_lds<W4>(J, P, pre, sh);  // read after the wave-sum barrier
+  epi_pre_to_lds<W4>(J, P, pre, sh);  // read after the wave-sum barrier
   f32x4 acc[8];
   unit_loop<W4>(J, P, M, R, sh, acc, []() {}, [](int) {});
-  unit_finish<W4>(J, P, M, acc, sh, a.part, a.cnt, pre);
+  unit_finish<W4>(J, P, M, acc, sh, a.part, a.cnt);
 }
 
 // Persistent chain: workgroup b takes units from queue b % 64 until the plan runs out.
@@ -719,14 +842,12 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
     const int kbase = P.split * ku;
     const int kuu = min(ku, J.K - kbase);
 
-    // ---- the next unit's descriptor (past the last unit: this job's first unit, whose
-    // first rows the last ring cycle then reads again from L2, with no branch) ----
+    // ---- the next unit's descriptor (past the last unit: any valid descriptor; the
+    // workgroup leaves before loading anything for it) ----
     const bool more = un < H.nunits;
     const int jnn = more ? __builtin_amdgcn_readfirstlane(unit_job[un]) : jn;
     const EPos Pn = unit_pos(jobs[jnn], jnn, more ? un : jobs[jnn].unit0);
     const ELoad Ln = make_load(jobs[jnn], Pn);
-    EEpiPre pre;
-    epi_prefetch_scales<W4>(J, P, pre);
 
     // ---- dependency: level L waits for every tile of level L - 1 ----
     if (J.level > 0) {
@@ -746,8 +867,6 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
       }
       __syncthreads();
     }
-    epi_prefetch_res(J, P, M, pre);
-
     // ---- activations into LDS ----
     if (J.pro.kind != PRO_NONE) {
       stage_producer(J, P, M, kbase, kuu, sh);
@@ -758,16 +877,14 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
       stage_store(M, kuu, st, sh);
       __syncthreads();
     }
-    // (written after the staging's loads, so that their wait does not precede them; read
-    // after the wave-sum barrier)
-    epi_scales_to_lds<W4>(J, P, pre, sh);
-
     // ---- K loop ----
     f32x4 acc[8];
     unit_loop<W4>(J, P, M, R, sh, acc, []() {}, [](int) {});
-    const bool fin = unit_finish<W4>(J, P, M, acc, sh, part, cnt + kLevel0 + 32 * H.nlevels, pre);
+    const bool fin = unit_finish<W4, true>(J, P, M, acc, sh, part, cnt + kLevel0 + 32 * H.nlevels,
+                                           (int*)(plan + offsetof(EHdr, err_run)));
 
-    // ---- the tile counts for its level; the level's last tile sets the flag ----
+    // ---- the tile counts for its level (its outputs written first); the level's last
+    // tile sets the flag ----
     if (fin && J.level + 1 < H.nlevels) {
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       __builtin_amdgcn_s_waitcnt(0);
@@ -780,10 +897,14 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
           __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    if (fin) empty_parts(J, P, M, part);
     // ---- the next unit's first blocks.  Issued only now: gfx950 counts loads and
     // stores on one in-order counter, so weight loads issued before this unit's
     // partial and output stores would make every wait for those stores (on the path
-    // to the next level) wait for the weights as well. ----
+    // to the next level) wait for the weights as well.  A workgroup with no next unit
+    // leaves here: loads for nothing would queue in front of the memory operations on
+    // other units' dependency paths. ----
+    if (!more) break;
 #pragma unroll
     for (int s = 0; s < RB; ++s) load_block<W4>(Ln, s, R, s);
     if (tid == 0) sh.unit2 = nn;
@@ -1171,7 +1292,9 @@ extern "C" int qlin_echain_init(const qlin_echain_job* jobs, int njobs, int M, v
   if (!plan || plan_bytes < (size_t)L.bytes) return set_error(QLIN_ERR_WORKSPACE, "qlin_echain_init: plan buffer too small");
   if (!ealigned(plan, 16)) return set_error(QLIN_ERR_UNSUPPORTED, "qlin_echain_init: plan must be 16-byte aligned");
   need.resize(L.nlevels, 0u);
-  std::vector<uint8_t> img((size_t)L.part_off, 0);
+  // the image runs to the end of the plan: the partial-sum slots start empty
+  std::vector<uint8_t> img((size_t)L.bytes, 0);
+  for (size_t o = (size_t)L.part_off; o + 4 <= img.size(); o += 4) memcpy(img.data() + o, &kEmptyPart, 4);
   EHdr h;
   memset(&h, 0, sizeof(h));
   h.magic = kMagic;
