@@ -310,7 +310,10 @@ __device__ __forceinline__ i32x4 mfma64(u32x4 a, u32x4 b) {
 }
 
 // One 64-wide W8 block of the lane's 8 columns, folded into acc.
-__device__ __forceinline__ void w8_block(const uint32_t (&w)[16][2], u32x4 a, f32x4 as, f32x4 (&acc)[8]) {
+// multi: the unit has more than one activation row.  With one, rows 1-3 of a lane's
+// accumulators are never read and their fold (three quarters of it) is skipped.
+__device__ __forceinline__ void w8_block(const uint32_t (&w)[16][2], u32x4 a, f32x4 as, f32x4 (&acc)[8],
+                                         bool multi) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     uint32_t x0[4], x1[4], x2[4], x3[4];
@@ -322,9 +325,13 @@ __device__ __forceinline__ void w8_block(const uint32_t (&w)[16][2], u32x4 a, f3
 #pragma unroll
     for (int u = 0; u < 4; ++u) p[u] = mfma64(a, u32x4{x0[u], x1[u], x2[u], x3[u]});
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < 4; ++u) acc[4 * q + u][0] = fmaf((float)p[u][0], as[0], acc[4 * q + u][0]);
+    if (multi) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[4 * q + u][r] = fmaf((float)p[u][r], as[r], acc[4 * q + u][r]);
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int r = 1; r < 4; ++r) acc[4 * q + u][r] = fmaf((float)p[u][r], as[r], acc[4 * q + u][r]);
+    }
   }
 }
 
@@ -332,7 +339,7 @@ __device__ __forceinline__ void w8_block(const uint32_t (&w)[16][2], u32x4 a, f3
 // operand permuted to match), folded against a_s * b_s / 16; explicit zeros add
 // 16 (8 - z) sum(a) (z = 8 when the job has none: no correction).
 __device__ __forceinline__ void w4_block(const uint32_t (&w)[8][2], const u32x4 (&sraw)[2], const uint32_t (&zr)[2],
-                                         int sdt, bool hz, u32x4 a, f32x4 as, f32x4 (&acc)[8]) {
+                                         int sdt, bool hz, u32x4 a, f32x4 as, f32x4 (&acc)[8], bool multi) {
   const u32x4 ap = u32x4{perm(a.y, a.x, 0x06040200u), perm(a.w, a.z, 0x06040200u), perm(a.y, a.x, 0x07050301u),
                          perm(a.w, a.z, 0x07050301u)};
   const i32x4 sx = mfma64(ap, u32x4{0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u});
@@ -355,12 +362,18 @@ __device__ __forceinline__ void w4_block(const uint32_t (&w)[8][2], const u32x4 
     i32x4 p[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) p[u] = mfma64(ap, u32x4{e0[u], e1[u], o0[u], o1[u]});
+    int zc[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = 4 * q + u;
-      const int zc = hz ? (8 - (int)((zr[q] >> (8 * u)) & 0xFFu)) * 16 : 0;
+    for (int u = 0; u < 4; ++u) zc[u] = hz ? (8 - (int)((zr[q] >> (8 * u)) & 0xFFu)) * 16 : 0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf((float)(p[u][r] + zc * sx[r]), as[r] * ws[t], acc[t][r]);
+    for (int u = 0; u < 4; ++u)
+      acc[4 * q + u][0] = fmaf((float)(p[u][0] + zc[u] * sx[0]), as[0] * ws[4 * q + u], acc[4 * q + u][0]);
+    if (multi) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int r = 1; r < 4; ++r)
+          acc[4 * q + u][r] = fmaf((float)(p[u][r] + zc[u] * sx[r]), as[r] * ws[4 * q + u], acc[4 * q + u][r]);
     }
   }
 }
@@ -729,13 +742,14 @@ __device__ __forceinline__ void unit_loop(const EJob& J, const EPos& P, int M, E
   const int nblk = Ld.nblk;
   const int ncyc = J.wblk / RB;
   const bool hz = J.hz != 0;
+  const bool multi = M > 1;
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto block = [&](int b, int s) {
     const u32x4 a = a_operand(sh, M, wave, J.wblk, nblk, b);
     const f32x4 as = a_scales(sh, wave, J.wblk, nblk, b);
-    if constexpr (W4) w4_block(R.w[s], R.sraw[s], R.zr[s], J.sdt, hz, a, as, acc);
-    else w8_block(R.w[s], a, as, acc);
+    if constexpr (W4) w4_block(R.w[s], R.sraw[s], R.zr[s], J.sdt, hz, a, as, acc, multi);
+    else w8_block(R.w[s], a, as, acc, multi);
   };
   for (int cyc = 0; cyc + 1 < ncyc; ++cyc) {
 #pragma unroll
