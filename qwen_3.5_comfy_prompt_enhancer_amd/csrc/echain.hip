@@ -441,16 +441,6 @@ __device__ __forceinline__ void epi_prefetch_res(const EJob& J, const EPos& P, i
       rr, (valid && J.res) ? (unsigned)(((long long)row * J.ldr + gc) * 2) : 0xFFFFFFF0u, 0, kCpolSc1));
 }
 
-// A partial-sum slot of the persistent chain holds -0.0 in every word until its unit
-// stores its part.  A part is never -0.0: every sum starts from +0.0, and a rounded
-// sum or fused multiply-add is -0.0 only when its addend is.
-constexpr uint32_t kEmptyPart = 0x80000000u;
-
-__device__ __forceinline__ bool part_empty(f32x4 v) {
-  const u32x4 b = bitcast<u32x4>(v);
-  return b.x == kEmptyPart || b.y == kEmptyPart || b.z == kEmptyPart || b.w == kEmptyPart;
-}
-
 // The unit of a tile that runs its epilogue in the persistent chain: the tile's last
 // (set, split), whose unit number is the tile's largest.
 __device__ __forceinline__ bool unit_is_finisher(const EJob& J, const EPos& P) {

@@ -162,6 +162,17 @@ __device__ __forceinline__ f32x4 ld_coherent(__amdgpu_buffer_rsrc_t r, unsigned 
   return bitcast<f32x4>(__builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
 }
 
+// The engine chain's partial-sum slots hold -0.0 in every word until a unit stores its
+// part there, and the tile's finisher polls for data.  A part is never -0.0: every
+// sum starts from +0.0, and a rounded sum or fused multiply-add is -0.0 only when its
+// addend is.
+constexpr uint32_t kEmptyPart = 0x80000000u;
+
+__device__ __forceinline__ bool part_empty(f32x4 v) {
+  const u32x4 b = bitcast<u32x4>(v);
+  return b.x == kEmptyPart || b.y == kEmptyPart || b.z == kEmptyPart || b.w == kEmptyPart;
+}
+
 // ---------------------------------------------------------------------------
 // MFMA wrappers (16x16 output; lane l holds D[4*(l/16)+r][l%16], r = 0..3)
 // ---------------------------------------------------------------------------
