@@ -386,8 +386,11 @@ int qlin_echain_init(const qlin_echain_job* jobs, int njobs, int M, void* plan, 
 
 /* Runs every job of the plan in one launch on `stream`, asynchronously; capturable in
  * a HIP graph.  Launches of one plan must not overlap in time.  The int at byte offset
- * 20 of the plan is 1 after a launch in which a dependency wait gave up (it polls about
- * 4 M times), 0 otherwise; it describes the last finished launch. */
+ * 20 of the plan is 1 after a launch in which a wait gave up (a dependency or a split
+ * tile's partial sums; each polls about 4 M times), 0 otherwise; it describes the last
+ * finished launch.  The plan holds the split-K partial sums between the units of a
+ * launch (its slots are left empty at the launch's end); after a launch that reported
+ * 1, initialize the plan again (qlin_echain_init) before the next launch. */
 int qlin_echain_run(void* plan, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -242,7 +242,7 @@ class EngineChain:
         n = L.qlin_echain_bytes(arr, len(self._jobs), self.M)
         if n == 0:
             C.check(C.QLIN_ERR_INVALID, "qlin_echain_bytes")
-        plan = torch.empty(n, dtype=torch.uint8, device=self.device)
+        plan = torch.empty(n, dtype=torch.uint8, device=self.device) if self.plan is None else self.plan
         C.check(L.qlin_echain_init(arr, len(self._jobs), self.M, C.ptr(plan), n,
                                    torch.cuda.current_stream(self.device).cuda_stream), "qlin_echain_init")
         self.plan = plan
@@ -257,16 +257,20 @@ class EngineChain:
                 "qlin_echain_run")
 
     def wait_error(self) -> int:
-        """1 if a dependency wait of the last finished launch gave up, else 0 (reads device
-        memory; synchronizes with the current stream)."""
+        """1 if a wait of the last finished launch gave up (a dependency, or a split tile's
+        partial sums), else 0 (reads device memory; synchronizes with the current stream).
+        After a 1 the plan must be written again (build()) before the next launch: its
+        partial-sum slots may not be empty."""
         return int(self.plan[20:24].view(torch.int32).item())
 
     def run_checked(self):
-        """run(), then wait for it and raise if a dependency wait gave up."""
+        """run(), then wait for it and raise if a wait gave up (the plan is written again
+        first, so the chain can be launched once more)."""
         self.run()
         if self.wait_error():
-            raise RuntimeError("engine chain: a dependency wait gave up (a job read inputs that no lower level "
-                               "wrote in time)")
+            self.build()
+            raise RuntimeError("engine chain: a wait gave up (a job read inputs that no lower level wrote in time, "
+                               "or a split tile's partial sums did not arrive)")
 
     @property
     def nbytes(self) -> int:
