@@ -12,8 +12,8 @@
  *     never synchronizes and never allocates memory;
  *   - writes only into caller-allocated outputs.  Split-K partial sums go through the
  *     caller-supplied `workspace` (at least qlin_workspace_bytes() bytes, zero-filled
- *     once before first use; the library leaves its counters at zero after every
- *     call).  Calls that share a workspace must not overlap in time.
+ *     once before first use; the library leaves its counters and exchange slots at
+ *     zero after every call).  Calls that share a workspace must not overlap in time.
  *
  * Layouts are the engine's (weights.py:297-309, quant_formats.py:6-9):
  *   W8  : int8  b[K][N] (N contiguous), scale[N]
@@ -73,7 +73,8 @@ int qlin_gemm_i8(const int8_t* a_q, const float* a_s, int M, int K,
 /* qlin_gemm_i8 without a workspace argument: no counterpart in the reference.  For
  * callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  Split-K partials and arrival
- * counters go to a static device array of 9 MiB per GPU (1 MiB of counters, 8 MiB of
+ * counters go to a static device array of 13 MiB per GPU (1 MiB of counters, 4 MiB of
+ * slots that decode calls' split tiles exchange through and leave zero, 8 MiB of
  * partials), held until the process ends; nothing is allocated or freed per call.
  * Each call first zeroes the arrival counters it can use with a fill kernel on
  * `stream`.  Results equal qlin_gemm_i8's bit for bit: decode plans fit the scratch,

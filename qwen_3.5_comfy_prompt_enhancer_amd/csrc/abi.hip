@@ -46,9 +46,13 @@ __global__ void zero_u32(unsigned* p, int n) {
   } while (0)
 
 
-// Workspace: [counters | partial sums].  Counters must be zero between calls.
+// Workspace: [counters | polling-exchange slots | partial sums].  Counters and slots
+// must be zero between calls (every kernel leaves them so; the slots are used only by
+// the engine decode units' polling exchange).
 constexpr size_t kWorkspaceBytes = size_t(256) << 20;
 constexpr size_t kCounterBytes = size_t(1) << 20;
+constexpr size_t kPollBytes = size_t(4) << 20;
+constexpr size_t kPartBase = kCounterBytes + kPollBytes;
 constexpr int kWideTiles = 512;          // 256-column tiles at which no K split is needed
 // narrow launches: most waves to spread K over, and least K per wave (measured with
 // 8-wave workgroups: many short waves keep the most weight bytes in flight)
@@ -262,7 +266,7 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
   for (int s = 0; s < (P.epi == EPI_STORE ? a.nseg : 1); ++s) ntiles += (a.seg[s].n + TN - 1) / TN;
   // rows per launch: the split-K partials and arrival counters of a launch must fit
   // the workspace (rows are independent, so blocks of rows give the same bits)
-  const size_t part_cap = (workspace && ws_bytes > kCounterBytes) ? ws_bytes - kCounterBytes : 0;
+  const size_t part_cap = (workspace && ws_bytes > kPartBase) ? ws_bytes - kPartBase : 0;
   const int rstep = tiled ? 128 : 16;
   long long mb_rows = P.M;
   if (S > 1) {
@@ -284,7 +288,7 @@ int engine_rows(const char* fn, const Problem& P, SkArgs& a, void* workspace, si
     SkArgs b = row_block(a, (int)m0, rows);
     b.splits = S;
     b.cnt = S > 1 ? (unsigned*)workspace : nullptr;
-    b.part = S > 1 ? (float*)((char*)workspace + kCounterBytes) : nullptr;
+    b.part = S > 1 ? (float*)((char*)workspace + kPartBase) : nullptr;
     hipError_t err;
     if (tiled) {
       if (!b.x || !b.xs) return fail(QLIN_ERR_INVALID, "%s: internal error: no activations for the tiled kernel", fn);
@@ -336,7 +340,8 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   if (P.act == ACT_I8 && P.M <= kDecodeRowsMax && echain_covers(a, P.wk, P.M)) {
     const char* ed = getenv("QLIN_ENGINE_DECODE");
     if (!(ed && strcmp(ed, "skinny") == 0))
-      return echain_engine_call(fn, a, P.wk, P.epi, P.M, workspace, ws_bytes, kCounterBytes, stream, clear);
+      return echain_engine_call(fn, a, P.wk, P.epi, P.M, workspace, ws_bytes, kCounterBytes, kPollBytes, stream,
+                                clear);
   }
   if (P.act == ACT_I8 && P.M >= kRowsM) return engine_rows(fn, P, a, workspace, ws_bytes, stream, clear);
   SkLaunch L;
@@ -414,7 +419,7 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
     splits = (chunks + waves - 1) / waves;
   }
   // partial sums must fit the workspace; without a workspace there is no cross-workgroup split
-  const size_t part_cap = (workspace && ws_bytes > kCounterBytes) ? ws_bytes - kCounterBytes : 0;
+  const size_t part_cap = (workspace && ws_bytes > kPartBase) ? ws_bytes - kPartBase : 0;
   auto fits = [&](int s) {
     const size_t need = (size_t)s * P.nsets * (size_t)P.M * (size_t)P.ncols * sizeof(float);
     const size_t cnt_need = (size_t)rtiles * ntiles * sizeof(unsigned);
@@ -432,7 +437,7 @@ int plan_and_launch(const char* fn, const Problem& P, SkArgs& a, void* workspace
   a.splits = splits;
   if (splits > 1) {
     a.cnt = (unsigned*)workspace;
-    a.part = (float*)((char*)workspace + kCounterBytes);
+    a.part = (float*)((char*)workspace + kPartBase);
   } else {
     a.cnt = nullptr;
     a.part = nullptr;
@@ -491,7 +496,7 @@ int setup_pro(const char* fn, ProArgs& p, int M, int K, void* ws, size_t* wsb) {
   } else {
     const size_t qb = ((size_t)M * K + 255) & ~(size_t)255;
     const size_t sb = ((size_t)M * (K / 64) * sizeof(float) + 255) & ~(size_t)255;
-    if (!ws || *wsb < kCounterBytes + qb + sb)
+    if (!ws || *wsb < kPartBase + qb + sb)
       return fail(QLIN_ERR_WORKSPACE, "%s: no room in the workspace for the activation codes", fn);
     *wsb -= qb + sb;
     p.tq = (int8_t*)ws + *wsb;
@@ -620,7 +625,7 @@ int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int
   a.ldr = ldr;
   a.pro = pa;
   Problem P{ACT_I8, wk, EPI_STORE, b_z != nullptr, M, K, a.group, 1, N};
-  if (clear && (!ws || wsb <= kCounterBytes)) return fail(QLIN_ERR_WORKSPACE, "%s: no scratch", fn);
+  if (clear && (!ws || wsb <= kPartBase)) return fail(QLIN_ERR_WORKSPACE, "%s: no scratch", fn);
   return plan_and_launch(fn, P, a, ws, wsb, (hipStream_t)stream, clear);
 }
 
@@ -861,7 +866,7 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
   const bool force_tiled = pimpl && strcmp(pimpl, "tiled") == 0;
   // the DMA kernel addresses activations with 32-bit byte offsets
   const bool fits32 = ((long long)(M - 1) * ldx + K) * 2 < (1LL << 31);
-  const size_t part_cap = (ws && wsb > kCounterBytes) ? wsb - kCounterBytes : 0;
+  const size_t part_cap = (ws && wsb > kPartBase) ? wsb - kPartBase : 0;
   if (M > 16 && K % 64 == 0 && !force_skinny) {
     TlArgs t;
     t.x = (const _Float16*)x;
@@ -917,7 +922,7 @@ int a16_linear(const char* fn, int wk, const void* x, int x_dtype, int M, int K,
         if (p.sk == 0) t.gm = prefill_tile_group(wk, M, K, N, p.shape);
         if (p.splits > 1 || p.sk > 0) {
           t.cnt = (unsigned*)ws;
-          t.part = (float*)((char*)ws + kCounterBytes);
+          t.part = (float*)((char*)ws + kPartBase);
         }
         return hip_status(fn, launch_prefill(t, wk, zero != nullptr, p.shape, (hipStream_t)stream));
       }
@@ -957,6 +962,7 @@ int gemm_i8_scratch(const char* fn, const int8_t* a_q, const float* a_s, int M, 
 }
 
 size_t counter_bytes() { return kCounterBytes; }
+size_t poll_bytes() { return kPollBytes; }
 
 }  // namespace qlin
 

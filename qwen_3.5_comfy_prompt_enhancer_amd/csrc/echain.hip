@@ -447,8 +447,9 @@ __device__ __forceinline__ bool unit_is_finisher(const EJob& J, const EPos& P) {
   return P.set == J.nsets - 1 && P.split == J.splits - 1;
 }
 
-// The chain's finisher empties its partners' slots for the next launch (after its level
-// count, off the tile's path).
+// A polling finisher empties its partners' slots for the next use (in the chain after
+// its level count, off the tile's path).
+template <bool FLIP>
 __device__ __forceinline__ void empty_parts(const EJob& J, const EPos& P, int M, float* part_base) {
   const int c = etid();
   const long long MT = (long long)M * TNC;
@@ -456,10 +457,7 @@ __device__ __forceinline__ void empty_parts(const EJob& J, const EPos& P, int M,
   const int S = J.splits, NSx = J.nsets;
   const __amdgpu_buffer_rsrc_t pr =
       part_rsrc(part_base + J.part, (unsigned)((long long)J.ntiles * NSx * S * MT * 4));
-  // (made here: hoisted out of the persistent loop, the constant would be spilled)
-  uint32_t em;
-  asm volatile("v_bfrev_b32 %0, 1" : "=v"(em));  // kEmptyPart
-  const f32x4 empty = bitcast<f32x4>(u32x4{em, em, em, em});
+  const f32x4 empty = part_mark<FLIP>();
   for (int s = 0; s < NSx; ++s)
     for (int p = 0; p < S; ++p)
       if (!(s == NSx - 1 && p == S - 1))
@@ -470,16 +468,21 @@ __device__ __forceinline__ void empty_parts(const EJob& J, const EPos& P, int M,
 // epilogue.  Returns whether this unit finished its tile (it ran the epilogue).
 //
 // Two exchanges give the same sums in the same order (per set, split 0 + split 1 + ...):
-//  * single calls (POLL false): every part is stored, the stores are waited for, an
-//    arrival counter per tile picks the last arrival, which reads and sums the parts;
-//  * the persistent chain (POLL true): the tile's finisher unit (unit_is_finisher)
-//    polls its partners' slots in the plan until none is empty and sums them with its
-//    own part (kept in registers); empty_parts() empties them for the next launch.  The others
-//    store their part and go on without waiting.  One memory round trip on the
-//    tile's path instead of three (store completion, counter, reads).  The finisher's
-//    partners have smaller unit numbers, so the smallest unfinished unit of the chain
-//    never polls for a part that no workgroup holds.
-template <bool W4, bool POLL = false>
+//  * counter (POLL false; a single call with more units than the chip holds at once):
+//    every part is stored, the stores are waited for, an arrival counter per tile picks
+//    the last arrival, which reads and sums the parts;
+//  * polling (POLL true; the persistent chain, and single calls whose units are all
+//    resident at once): the tile's finisher unit (unit_is_finisher) polls its partners'
+//    slots until none is empty (part_flip encoding, qlin_dev.h) and sums them with its
+//    own part (kept in registers); empty_parts() zeroes them again.  The others store
+//    their part and go on without waiting.  One memory round trip on the tile's path
+//    instead of three (store completion, counter, reads).  In the chain the finisher's
+//    partners have smaller unit numbers, so the smallest unfinished unit never polls
+//    for a part that no workgroup holds; in a single call every unit is resident.
+// PRE_LDS: the unit's residual and column scales were loaded ahead into LDS
+// (epi_pre_to_lds); the polling finisher of a split tile loads its own with its polls.
+// FLIP: the slots' encoding (part_code, qlin_dev.h).
+template <bool W4, bool POLL = false, bool PRE_LDS = !POLL, bool FLIP = false>
 __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M, f32x4 (&acc)[8], ESh& sh,
                                             float* part_base, unsigned* cnt_base, int* err_run = nullptr) {
   const int tid = etid(), wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
@@ -533,7 +536,7 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
       return (unsigned)(((((long long)P.tile * NSx + s) * S + p) * MT + c * 4) * 4);
     };
     if (!unit_is_finisher(J, P)) {
-      if (c < nch) st_coherent(v[0], pr, slot(P.set, P.split));
+      if (c < nch) st_coherent(part_code<FLIP>(v[0]), pr, slot(P.set, P.split));
       return false;
     }
     load_epi_in();
@@ -554,7 +557,7 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
                 pp[q] = mine;
               } else {
                 int spins = 0;
-                while (part_empty(pp[q])) {
+                while (part_empty<FLIP>(pp[q])) {
                   if (++spins > kSpinLimit) {
                     late = true;
                     break;
@@ -563,7 +566,8 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
                   pp[q] = ld_coherent(pr, slot(s, p));
                 }
               }
-              sum = (p == 0) ? pp[q] : sum + pp[q];
+              const f32x4 x = (s == NSx - 1 && p == S - 1) ? pp[q] : part_code<FLIP>(pp[q]);
+              sum = (p == 0) ? x : sum + x;
             }
           }
         }
@@ -571,7 +575,7 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
       }
       if (late && err_run) __hip_atomic_store(err_run, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-  } else if (POLL) {
+  } else if (POLL && !PRE_LDS) {
     load_epi_in();
   } else if (J.xch) {
     // every (set, split) of the tile stores its sums; the last to arrive sums them in
@@ -622,7 +626,7 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
 #pragma unroll
     for (int e = 0; e < 4; ++e) cs[s][e] = 1.0f;
   if constexpr (!W4) {
-    if constexpr (POLL) {
+    if (POLL && (J.xch || !PRE_LDS)) {
       cvt_scale4_nb(csr[0], J.sdt, cs[0]);
       cvt_scale4_nb(csr[1], J.sdt, cs[1]);
     } else {
@@ -638,7 +642,7 @@ __device__ __forceinline__ bool unit_finish(const EJob& J, const EPos& P, int M,
     float y[4];
     const __amdgpu_buffer_rsrc_t orr = part_rsrc(J.out, (unsigned)(((long long)(M - 1) * J.ldo + N) * 2));
     if (J.res) {
-      const u32x2 rv = POLL ? rvv : sh.rv[c];
+      const u32x2 rv = (POLL && (J.xch || !PRE_LDS)) ? rvv : sh.rv[c];
       const uint32_t rw[2] = {rv.x, rv.y};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -765,7 +769,9 @@ __device__ __forceinline__ void unit_loop(const EJob& J, const EPos& P, int M, E
 // ------------------------------------------------------------------ kernels
 
 // Single call: unit u = blockIdx.x of up to 3 jobs (proj3 segments; one job otherwise).
-template <bool W4>
+// POLL: every unit of the grid is resident at once, and split tiles use the polling
+// exchange on slots that start zero and are left zero.
+template <bool W4, bool POLL>
 __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ecall_kernel(const ECallArgs a) {
   __shared__ ESh sh;
   const int u = blockIdx.x;
@@ -798,7 +804,7 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
   epi_pre_to_lds<W4>(J, P, pre, sh);  // read after the wave-sum barrier
   f32x4 acc[8];
   unit_loop<W4>(J, P, M, R, sh, acc, []() {}, [](int) {});
-  unit_finish<W4>(J, P, M, acc, sh, a.part, a.cnt);
+  if (unit_finish<W4, POLL, true, true>(J, P, M, acc, sh, a.part, a.cnt) && POLL) empty_parts<true>(J, P, M, a.part);
 }
 
 // Persistent chain: workgroup b takes units from queue b % 64 until the plan runs out.
@@ -901,7 +907,7 @@ __global__ __launch_bounds__(ET) __attribute__((amdgpu_waves_per_eu(3))) void ec
           __hip_atomic_store(level_flag(plan, H, J.level), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    if (fin) empty_parts(J, P, M, part);
+    if (fin) empty_parts<false>(J, P, M, part);
     // ---- the next unit's first blocks.  Issued only now: gfx950 counts loads and
     // stores on one in-order counter, so weight loads issued before this unit's
     // partial and output stores would make every wait for those stores (on the path
@@ -1054,8 +1060,32 @@ std::vector<EPlanInfo> g_eplans;
 // The single-call form: up to 3 jobs (same K, activations, weight format) at level 0,
 // split-K scratch from the caller's workspace ([counters | partials]).  `clear` zeroes
 // the counters first (a scratch not known to be zero).
+// Workgroups of a single call's grid that are resident on the device at once.
+int g_cres[64][2];
+int ecall_resident(bool w4, int* n) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) return set_error(QLIN_ERR_HIP, "echain_call: hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_emu);
+  if (g_cres[dev][w4] == 0) {
+    int cus = 0, per = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = w4 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, ecall_kernel<true, true>, ET, 0)
+             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, ecall_kernel<false, true>, ET, 0);
+    if (e != hipSuccess || cus <= 0 || per <= 0) return set_error(QLIN_ERR_HIP, "echain_call: occupancy query failed");
+    g_cres[dev][w4] = cus * per;
+  }
+  *n = g_cres[dev][w4];
+  return QLIN_OK;
+}
+
+// The workspace (or a scratch laid out like it): `counter_bytes` of arrival counters,
+// `poll_bytes` of polling-exchange slots (zero between calls), then split-K partials.
+// A call whose units are all resident at once takes the polling exchange
+// (QLIN_ECALL_POLL=0 turns it off); a larger one the arrival counters.
 int echain_call(const char* fn, EJob* jobs, int njobs, int M, void* ws, size_t wsb, size_t counter_bytes,
-                hipStream_t stream, bool clear) {
+                size_t poll_bytes, hipStream_t stream, bool clear) {
   if (njobs < 1 || njobs > 3) return set_error(QLIN_ERR_INVALID, "echain_call: 1-3 jobs");
   ECallArgs a;
   memset(&a, 0, sizeof(a));
@@ -1079,24 +1109,42 @@ int echain_call(const char* fn, EJob* jobs, int njobs, int M, void* ws, size_t w
     a.jobs[i] = d;
   }
   if (units > 0x7FFFFFFFLL) return set_error(QLIN_ERR_UNSUPPORTED, "echain_call: grid too large");
+  bool poll = false;
+  if (parts > 0) {
+    int resident = 0;
+    QL_TRY_E(ecall_resident(w4, &resident));
+    const char* ep = getenv("QLIN_ECALL_POLL");
+    poll = !(ep && strcmp(ep, "0") == 0) && ws && units <= resident && (size_t)parts * 4 <= poll_bytes &&
+           wsb >= counter_bytes + poll_bytes;
+  }
   if (cnts > 0 || parts > 0) {
-    if (!ws || (size_t)cnts * 4 > counter_bytes || wsb < counter_bytes + (size_t)parts * 4) {
-      char msg[200];
-      snprintf(msg, sizeof(msg), "%s: the workspace cannot hold %lld split-K partial floats", fn, parts);
-      return set_error(QLIN_ERR_WORKSPACE, msg);
-    }
-    a.cnt = (unsigned*)ws;
-    a.part = (float*)((char*)ws + counter_bytes);
-    if (clear) {
-      const hipError_t e = clear_counters(ws, cnts, stream);
-      if (e != hipSuccess) return set_error(QLIN_ERR_HIP, "echain_call: counter clear failed");
+    if (poll) {
+      a.cnt = (unsigned*)ws;
+      a.part = (float*)((char*)ws + counter_bytes);
+    } else {
+      if (!ws || (size_t)cnts * 4 > counter_bytes || wsb < counter_bytes + poll_bytes + (size_t)parts * 4) {
+        char msg[200];
+        snprintf(msg, sizeof(msg), "%s: the workspace cannot hold %lld split-K partial floats", fn, parts);
+        return set_error(QLIN_ERR_WORKSPACE, msg);
+      }
+      a.cnt = (unsigned*)ws;
+      a.part = (float*)((char*)ws + counter_bytes + poll_bytes);
+      if (clear) {
+        const hipError_t e = clear_counters(ws, cnts, stream);
+        if (e != hipSuccess) return set_error(QLIN_ERR_HIP, "echain_call: counter clear failed");
+      }
     }
   }
   a.njobs = njobs;
   a.M = M;
   a.nunits = (int)units;
-  if (w4) hipLaunchKernelGGL(ecall_kernel<true>, dim3((unsigned)units), dim3(ET), 0, stream, a);
-  else hipLaunchKernelGGL(ecall_kernel<false>, dim3((unsigned)units), dim3(ET), 0, stream, a);
+  if (w4) {
+    if (poll) hipLaunchKernelGGL((ecall_kernel<true, true>), dim3((unsigned)units), dim3(ET), 0, stream, a);
+    else hipLaunchKernelGGL((ecall_kernel<true, false>), dim3((unsigned)units), dim3(ET), 0, stream, a);
+  } else {
+    if (poll) hipLaunchKernelGGL((ecall_kernel<false, true>), dim3((unsigned)units), dim3(ET), 0, stream, a);
+    else hipLaunchKernelGGL((ecall_kernel<false, false>), dim3((unsigned)units), dim3(ET), 0, stream, a);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     char msg[200];
@@ -1118,7 +1166,7 @@ bool echain_covers(const SkArgs& a, int wk, int M) {
 // An engine-signature call (SkArgs as abi.hip builds it) as echain jobs: one per
 // proj3 column segment, one for gemm or gate/up.
 int echain_engine_call(const char* fn, const SkArgs& a, int wk, int epi, int M, void* ws, size_t ws_bytes,
-                       size_t counter_bytes, hipStream_t stream, bool clear) {
+                       size_t counter_bytes, size_t poll_bytes, hipStream_t stream, bool clear) {
   EJob base;
   memset(&base, 0, sizeof(base));
   base.aq = (const int8_t*)a.x;
@@ -1161,7 +1209,7 @@ int echain_engine_call(const char* fn, const SkArgs& a, int wk, int epi, int M, 
     d.os = a.os;
     jobs[nj++] = d;
   }
-  return echain_call(fn, jobs, nj, M, ws, ws_bytes, counter_bytes, stream, clear);
+  return echain_call(fn, jobs, nj, M, ws, ws_bytes, counter_bytes, poll_bytes, stream, clear);
 }
 
 // ------------------------------------------------------------------ chain plans
@@ -1296,9 +1344,10 @@ extern "C" int qlin_echain_init(const qlin_echain_job* jobs, int njobs, int M, v
   if (!plan || plan_bytes < (size_t)L.bytes) return set_error(QLIN_ERR_WORKSPACE, "qlin_echain_init: plan buffer too small");
   if (!ealigned(plan, 16)) return set_error(QLIN_ERR_UNSUPPORTED, "qlin_echain_init: plan must be 16-byte aligned");
   need.resize(L.nlevels, 0u);
-  // the image runs to the end of the plan: the partial-sum slots start empty
+  // the image runs to the end of the plan: the partial-sum slots start empty (-0.0)
   std::vector<uint8_t> img((size_t)L.bytes, 0);
-  for (size_t o = (size_t)L.part_off; o + 4 <= img.size(); o += 4) memcpy(img.data() + o, &kEmptyPart, 4);
+  const uint32_t mark = 0x80000000u;
+  for (size_t o = (size_t)L.part_off; o + 4 <= img.size(); o += 4) memcpy(img.data() + o, &mark, 4);
   EHdr h;
   memset(&h, 0, sizeof(h));
   h.magic = kMagic;

@@ -2,8 +2,10 @@
 // instead of a caller-supplied workspace, for callers that cannot allocate device memory
 // (code under HIP graph capture, serving loops, harnesses that forbid allocation).
 //
-// The array `scratch` (kScratchBytes: 1 MiB of arrival counters, then 8 MiB of fp32
-// partial sums, the workspace's layout) exists once per GPU for the life of the process.
+// The array `scratch` (kScratchBytes: 1 MiB of arrival counters, 4 MiB of polling-exchange
+// slots, then 8 MiB of fp32 partial sums, the workspace's layout; zero at load, and the
+// counters and slots are left zero by every call) exists once per GPU for the life of
+// the process.
 // Its device address is taken once per device with hipGetSymbolAddress, with that device
 // current, and kept per device; host code uses only that address, never the array's
 // name (in host code the name is a host-side stand-in, not a device address).  Every
@@ -20,7 +22,7 @@
 namespace {
 
 constexpr size_t kScratchPartialBytes = size_t(8) << 20;
-constexpr size_t kScratchBytes = (size_t(1) << 20) + kScratchPartialBytes;
+constexpr size_t kScratchBytes = (size_t(1) << 20) + (size_t(4) << 20) + kScratchPartialBytes;
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
@@ -54,7 +56,7 @@ int scratch_ptr(void** out) {
 extern "C" int qlin_gemm_i8_noalloc(const int8_t* a_q, const float* a_s, int M, int K, const int8_t* b,
                                     const void* b_s, int bs_dtype, int N, void* out, int64_t ldo,
                                     const void* residual, int64_t ldr, void* stream) {
-  if (qlin::counter_bytes() + kScratchPartialBytes != kScratchBytes)
+  if (qlin::counter_bytes() + qlin::poll_bytes() + kScratchPartialBytes != kScratchBytes)
     return qlin::set_error(QLIN_ERR_WORKSPACE, "qlin_gemm_i8_noalloc: scratch layout mismatch");
   void* ptr = nullptr;
   const int rc = scratch_ptr(&ptr);

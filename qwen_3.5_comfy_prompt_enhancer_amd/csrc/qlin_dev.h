@@ -162,15 +162,39 @@ __device__ __forceinline__ f32x4 ld_coherent(__amdgpu_buffer_rsrc_t r, unsigned 
   return bitcast<f32x4>(__builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
 }
 
-// The engine chain's partial-sum slots hold -0.0 in every word until a unit stores its
-// part there, and the tile's finisher polls for data.  A part is never -0.0: every
-// sum starts from +0.0, and a rounded sum or fused multiply-add is -0.0 only when its
-// addend is.
-constexpr uint32_t kEmptyPart = 0x80000000u;
+// Partial-sum slots of the decode units' polling exchange hold an empty mark in every
+// word until a unit stores its part: -0.0, which a part never is (every sum starts from
+// +0.0, and a rounded sum or fused multiply-add is -0.0 only when its addend is).  With
+// FLIP a part is stored with its sign bits flipped, so the mark is a zero word: a slot
+// the caller zeroed, or one zeroed again after its tile finished.  A reader polls until
+// no word of the slot holds the mark.
+__device__ __forceinline__ uint32_t sign_mask() {
+  // (made where it is used: a persistent kernel would hoist the constant out of its loop
+  // and spill it)
+  uint32_t m;
+  asm volatile("v_bfrev_b32 %0, 1" : "=v"(m));
+  return m;
+}
 
-__device__ __forceinline__ bool part_empty(f32x4 v) {
-  const u32x4 b = bitcast<u32x4>(v);
-  return b.x == kEmptyPart || b.y == kEmptyPart || b.z == kEmptyPart || b.w == kEmptyPart;
+template <bool FLIP>
+__device__ __forceinline__ f32x4 part_code(f32x4 v) {
+  if constexpr (!FLIP) return v;
+  const uint32_t m = sign_mask();
+  return bitcast<f32x4>(bitcast<u32x4>(v) ^ u32x4{m, m, m, m});
+}
+
+template <bool FLIP>
+__device__ __forceinline__ bool part_empty(f32x4 stored) {
+  const u32x4 b = bitcast<u32x4>(stored);
+  const uint32_t e = FLIP ? 0u : 0x80000000u;
+  return b.x == e || b.y == e || b.z == e || b.w == e;
+}
+
+template <bool FLIP>
+__device__ __forceinline__ f32x4 part_mark() {
+  if constexpr (FLIP) return f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t m = sign_mask();
+  return bitcast<f32x4>(u32x4{m, m, m, m});
 }
 
 // ---------------------------------------------------------------------------

@@ -142,12 +142,14 @@ bool prefill_shape_ok(int shape);
 // Sets the message qlin_last_error() returns on this thread; returns `code`.
 int set_error(int code, const char* msg);
 // qlin_gemm_i8 on a caller-owned scratch laid out like the workspace (counter_bytes()
-// of arrival counters, then partial sums): validates, clears the arrival counters the
-// call can use with a fill kernel on `stream`, then plans and launches.
+// of arrival counters, poll_bytes() of polling-exchange slots that start zero, then
+// partial sums): validates, clears the arrival counters the call can use with a fill
+// kernel on `stream`, then plans and launches.
 int gemm_i8_scratch(const char* fn, const int8_t* a_q, const float* a_s, int M, int K, const int8_t* b,
                     const void* b_s, int bs_dtype, int N, void* out, int64_t ldo, const void* residual,
                     int64_t ldr, void* scratch, size_t scratch_bytes, void* stream);
 size_t counter_bytes();
+size_t poll_bytes();
 
 // Validates an activation producer for M rows of K columns (norm_gated's input row
 // stride becomes K); returns a status with the message set.
@@ -157,11 +159,12 @@ hipError_t clear_counters(void* ws, long long n, hipStream_t stream);
 // Engine decode work units (echain.hip): whether an engine-signature call of M rows
 // runs on them (M <= 8, W8 or W4 groups that are multiples of 64, 16-byte aligned
 // activations), and the call as a one-level launch of them.  The workspace holds
-// `counter_bytes` of arrival counters, then split-K partials.
+// `counter_bytes` of arrival counters, `poll_bytes` of polling-exchange slots (zero
+// between calls), then split-K partials.
 constexpr int kDecodeRowsMax = 8;
 bool echain_covers(const SkArgs& a, int wk, int M);
 int echain_engine_call(const char* fn, const SkArgs& a, int wk, int epi, int M, void* ws, size_t ws_bytes,
-                       size_t counter_bytes, hipStream_t stream, bool clear);
+                       size_t counter_bytes, size_t poll_bytes, hipStream_t stream, bool clear);
 
 // Standalone producer launch: codes and scales of all M rows into p.q / p.s.
 hipError_t launch_producer(const ProArgs& p, int M, int K, hipStream_t st);
