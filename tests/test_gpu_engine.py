@@ -611,3 +611,62 @@ def test_two_streams_use_separate_workspaces():
     for o1, o2 in zip(outs1, outs2):
         assert torch.equal(o1, ref1)
         assert torch.equal(o2, ref2)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+def test_decode_polling_exchange_same_bits_and_slots_left_zero(kind, M, monkeypatch):
+    """Decode-sized engine calls whose units are all resident finish their split tiles
+    by polling the partners' slots in the workspace's slot region (parts stored with
+    flipped sign bits, zero = empty); QLIN_ECALL_POLL=0 takes the arrival counters.
+    Both give the same bits for gemm + residual, proj3 and gate/up + requant (K = 2048
+    and 6144: 4 and 12 splits), call after call, and the slot region is zero after
+    every call (the next call's finisher would read a leftover part as data)."""
+    from qwen35_amd.kernels import qlin
+    gemm, w4 = _g()
+    K1, N1, K2, N2 = 2048, 6144, 6144, 2048
+    a1, s1 = H.engine_act(M, K1, seed=71)
+    a2, s2 = H.engine_act(M, K2, seed=72)
+    if kind == "w8":
+        wg, sg = H.engine_w8(K1, N1, seed=73)
+        wu, su = H.engine_w8(K1, N1, seed=74)
+        wd, sd = H.engine_w8(K2, N2, seed=75)
+        zg = zu = zd = None
+    else:
+        wg, sg, zg = _w4_engine(K1, N1, seed=73, zeros="random")
+        wu, su, zu = _w4_engine(K1, N1, seed=74, zeros="random")
+        wd, sd, zd = _w4_engine(K2, N2, seed=75)
+    cu = lambda t: None if t is None else t.cuda()
+    res = torch.randn((M, N2), dtype=torch.float32).to(torch.bfloat16).cuda()
+
+    def calls():
+        outs = {}
+        q = torch.empty((M, N1), dtype=torch.int8, device="cuda")
+        qs = torch.empty((M, N1 // 64), dtype=torch.float32, device="cuda")
+        gemm.mlp_gate_up_quant(cu(a1), cu(s1), cu(wg), cu(sg), cu(wu), cu(su), q, qs, zg=cu(zg), zu=cu(zu))
+        outs["q"], outs["qs"] = q.cpu(), qs.cpu()
+        d = res.clone()
+        if kind == "w8":
+            gemm.gemm_i8(cu(a2), cu(s2), cu(wd), cu(sd), d, residual=d)
+        else:
+            w4.gemm_w4(cu(a2), cu(s2), cu(wd), cu(sd), d, residual=d, b_z=cu(zd))
+        outs["d"] = d.cpu()
+        p = torch.empty((M, 512 + 1024 + 1536), dtype=torch.bfloat16, device="cuda")
+        if kind == "w8":
+            gemm.proj3(cu(a1), cu(s1), cu(wg[:, :512].contiguous()), cu(sg[:512].contiguous()),
+                       cu(wu[:, :1024].contiguous()), cu(su[:1024].contiguous()),
+                       cu(wg[:, 512:2048].contiguous()), cu(sg[512:2048].contiguous()), p)
+            outs["p"] = p.cpu()
+        torch.cuda.synchronize()
+        return outs
+
+    slots = lambda: qlin.workspace(torch.device("cuda", torch.cuda.current_device()))[1 << 20:5 << 20]
+    monkeypatch.setenv("QLIN_ECALL_POLL", "0")
+    ref = calls()
+    assert int(slots().count_nonzero()) == 0
+    monkeypatch.setenv("QLIN_ECALL_POLL", "1")
+    for _ in range(3):
+        got = calls()
+        assert int(slots().count_nonzero()) == 0
+        for k in ref:
+            assert torch.equal(ref[k], got[k]), k
