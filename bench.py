@@ -427,10 +427,11 @@ ENGINE_LAYER = [  # the engine's four quantized calls of one 2B-class layer (eng
 ]
 
 
-def engine_bench(args, kind):
+def engine_bench(args, kind, ms=(1, 4, 512)):
     """The engine-signature calls of one layer (int8 activations with per-64 scales,
     bf16 outputs, in-place residuals, the fused gate/up + requantization) over
-    `layers` weight copies, at decode rows M = 1, 4 and a prefill chunk M = 512.
+    `layers` weight copies, at decode rows M = 1, 4 and a prefill chunk M = 512
+    (`ms` drops the chunk when only the decode rows are wanted).
     Returns (bytes per step at M = 1, 4; flops per step at M = 512; per-M times)."""
     import torch
     dev = torch.device("cuda", 0)
@@ -475,7 +476,7 @@ def engine_bench(args, kind):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e-3 / args.steps / layers
 
-    for M in (1, 4, 512):
+    for M in ms:
         a = torch.randint(-127, 128, (M, 2048), generator=gen, dtype=torch.int8).to(dev)
         s = (torch.rand(M, 32, generator=gen) * 1e-2).to(dev)
         a6 = torch.randint(-127, 128, (M, 6144), generator=gen, dtype=torch.int8).to(dev)
@@ -561,7 +562,7 @@ def engine_bench(args, kind):
     out_bytes = lambda M: M * 2 * (8192 + 2048 * 2 * 2) + M * (6144 + 96 * 4)
     dec_bytes = {M: layer_wbytes + act_bytes(M) + out_bytes(M) for M in (1, 4)}
     flops = 2 * 512 * (2048 * 8192 + 2048 * 2048 + 2048 * 12288 + 6144 * 2048)
-    for M in (1, 4, 512):
+    for M in ms:
         extra = (f"{dec_bytes[M] / res[M] / 1e9:7.0f} GB/s" if M in dec_bytes
                  else f"{flops / res[M] / 1e12:7.1f} TOPS")
         log(f"engine {kind} layer M={M:4d}: {res[M] * 1e6:8.1f} us per layer  {extra}")
@@ -1001,6 +1002,22 @@ def main() -> int:
             if not config["output_check"]["ok"]:
                 print(json.dumps({"error": "decode sweep outputs out of tolerance", **config["output_check"]}))
                 return 1
+        if wl in ("decode-w8", "decode-w4"):
+            # beside the sweep: the call sequence the engine's decode step makes, the
+            # four engine-signature linears of one layer (int8 codes + per-64 scales),
+            # as four launches per layer and as one engine-chain launch per layer
+            # that also makes the activations (its producers)
+            dec_bytes, _, res, pro_res, chain_res = engine_bench(args, kind, ms=(1, 4))
+            config["engine_signature"] = {
+                "layer_calls": "proj3, gemm_i8 + residual, mlp_gate_up_quant, gemm_i8 + residual "
+                               "(one 2B-class layer, hipgraph of all layer copies per M)",
+                "bytes_per_layer": {str(M): dec_bytes[M] for M in (1, 4)},
+                "calls_us_per_layer": {str(M): round(res[M] * 1e6, 1) for M in (1, 4)},
+                "calls_frac": {str(M): round(dec_bytes[M] / res[M] / 1e9 / HBM_PEAK_GBS, 4) for M in (1, 4)},
+                "chain_with_producers_us_per_layer": {str(M): round(chain_res[M] * 1e6, 1) for M in (1, 4)},
+                "chain_frac": {str(M): round(dec_bytes[M] / chain_res[M] / 1e9 / HBM_PEAK_GBS, 4)
+                               for M in (1, 4)},
+                "calls_with_producers_us_per_layer": {str(M): round(pro_res[M][1] * 1e6, 1) for M in (1, 4)}}
         dtype = "f16 x int8" if kind == "w8" else "f16 x int4"
     elif wl in ("engine-w8", "engine-w4"):
         kind = wl.split("-")[1]
