@@ -571,34 +571,49 @@ def engine_bench(args, kind, ms=(1, 4, 512)):
     return dec_bytes, flops, res, pro_res, chain_res
 
 
-def check_sweep(ctx, kind, shapes, head, ms, layers, max_cols=4096):
+def check_sweep(ctx, kind, shapes, head, ms, layers, max_cols=4096, every_layer_cols=None):
     """Checks the outputs the timed decode steps left: every shape of the last layer
     copy and sampled columns of the vocabulary head, at every M, against the fp32 CPU
-    path (torch_dequant + fp32 matmul of the same fp16 activations).  Returns the
-    worst normalized error max|y - ref| / max|ref| and whether it is within the 2e-3
-    tolerance plus the fp16 output rounding (2**-11 relative)."""
+    path (torch_dequant + fp32 matmul of the same fp16 activations).  With
+    `every_layer_cols` set, the other layer copies are checked too, each job on that
+    many sampled columns (the columns are picked on the device, so only they are
+    copied and dequantized).  Returns the worst normalized error max|y - ref| /
+    max|ref| and whether it is within the 2e-3 tolerance plus the fp16 output
+    rounding (2**-11 relative)."""
     import torch
     lw, hw, xs, outs, hout = ctx[:5]
     worst = 0.0
     gen = torch.Generator().manual_seed(17)
-    jobs = [(lw[layers - 1][i], (lambda M, i=i: outs[M][layers - 1][i]), None) for i in range(len(shapes))]
-    cols = torch.randperm(head[2], generator=gen)[:max_cols].sort().values
-    jobs.append((hw, (lambda M: hout[M]), cols))
-    for w, out_of, cols_ in jobs:
-        wd = torch_dequant(kind, w.w.cpu(), w.s.cpu())
-        if cols_ is not None:
-            wd = wd[:, cols_]
+
+    def pick(n, k):
+        return torch.randperm(n, generator=gen)[:k].sort().values
+
+    jobs = [(lw[layers - 1][i], layers - 1, i, None) for i in range(len(shapes))]
+    if every_layer_cols:
+        jobs += [(lw[l][i], l, i, pick(shapes[i][2], every_layer_cols))
+                 for l in range(layers - 1) for i in range(len(shapes))]
+    jobs.append((hw, None, None, pick(head[2], max_cols)))
+    njobs = 0
+    for w, l, i, cols in jobs:
+        if cols is None:
+            wd = torch_dequant(kind, w.w.cpu(), w.s.cpu())
+        else:
+            cd = cols.to(w.w.device)
+            wd = torch_dequant(kind, w.w[:, cd].cpu(), (w.s[cd] if kind == "w8" else w.s[:, cd]).cpu())
         for M in ms:
             x = xs[M][:, :w.K].float().cpu()
             ref = x @ wd
-            y = out_of(M).float().cpu()
-            if cols_ is not None:
-                y = y[:, cols_]
+            y = (outs[M][l][i] if l is not None else hout[M])
+            y = (y if cols is None else y[:, cols.to(y.device)]).float().cpu()
             err = float((y - ref).abs().max() / ref.abs().max())
             worst = max(worst, err)
-    return {"max_rel_err": round(worst, 6), "ok": worst <= 2e-3 + 2.0 ** -11,
-            "checked": (f"every shape of layer copy {layers - 1} and {max_cols} sampled vocab-head columns, "
-                        f"M={'/'.join(map(str, ms))}, against dequantize + fp32 matmul on the CPU")}
+        njobs += 1
+    what = f"every shape of layer copy {layers - 1}"
+    if every_layer_cols:
+        what += f", {every_layer_cols} sampled columns of every shape of layer copies 0-{layers - 2}"
+    return {"max_rel_err": round(worst, 6), "ok": worst <= 2e-3 + 2.0 ** -11, "jobs": njobs,
+            "checked": (f"{what} and {max_cols} sampled vocab-head columns, M={'/'.join(map(str, ms))}, "
+                        "against dequantize + fp32 matmul on the CPU")}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -967,6 +982,16 @@ def main() -> int:
         log(("chain" if args.launch == "chain" else "vocab head") + " per-launch us by M: " +
             ", ".join(f"M={M}: {v * 1e3:.1f} ({head_bytes[M] / v / 1e6:.0f} GB/s)" for M, v in per_m.items()))
         other = None
+        check = None
+        if layers > 0:
+            # the outputs the timed steps left, before any other run rewrites them; the
+            # 9B-class chain is checked on every layer copy (sampled columns)
+            check = check_sweep(ctx, kind, shapes, head, ms, layers,
+                                every_layer_cols=256 if wl == "chain-w4" else None)
+            log(f"output check: {check}")
+            if not check["ok"]:
+                print(json.dumps({"error": "decode sweep outputs out of tolerance", **check}))
+                return 1
         if args.launch == "chain":
             for M, ch in ctx[6].items():
                 if ch.wait_error():
@@ -996,12 +1021,8 @@ def main() -> int:
                              if not args.no_graph else "eager")}
         if other is not None:
             config["other_levels"] = other
-        if layers > 0 and wl != "chain-w4":
-            config["output_check"] = check_sweep(ctx, kind, shapes, head, ms, layers)
-            log(f"output check: {config['output_check']}")
-            if not config["output_check"]["ok"]:
-                print(json.dumps({"error": "decode sweep outputs out of tolerance", **config["output_check"]}))
-                return 1
+        if check is not None:
+            config["output_check"] = check
         if wl in ("decode-w8", "decode-w4"):
             # beside the sweep: the call sequence the engine's decode step makes, the
             # four engine-signature linears of one layer (int8 codes + per-64 scales),
