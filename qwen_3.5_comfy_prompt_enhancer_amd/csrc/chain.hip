@@ -245,7 +245,7 @@ __device__ __forceinline__ void load_x(const UnitPos& P, int M, bool now, u32x4 
   for (int s = 0; s < STEPS; ++s) xv[s] = load_x_step(P, xr, M, now, k0, nsteps, s);
 }
 
-// W8 with M <= 4: the activations of one ring cycle (RING steps, 128 K rows of rows 0-3)
+// M <= 4: the activations of one ring cycle (RING steps, 128 K rows of rows 0-3)
 // in one 64-lane load, lane 16 r + c holding row r, K rows k0 + 128 cyc + 8 c .. + 7 (two
 // whole 128-byte lines per row), instead of RING loads with 4 M of 64 lanes active and
 // half a line per row each.  Rows past M, steps past the wave's range and any step when
@@ -340,7 +340,6 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
   UnitPos P;
   u32x4 xv[STEPS];
   u32x4 xc = u32x4{0u, 0u, 0u, 0u};  // XC: the current ring cycle's activations
-  static_assert(!(W4 && XC), "one-load activation cycles are built for W8");
   // a level-0 unit's activations go out with its weights; a later level's after its wait
   if (u < H.nunits) {
     P = decode_unit(jobs, unit_job, u);
@@ -416,7 +415,7 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
     f32x4 acc[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (XC) {
+    if constexpr (XC && !W4) {
       // as below, with each cycle's activations in one register per lane: the cycle's
       // step operands are permuted out of it at the cycle's start, and the next cycle's
       // load goes out with the refill of the first slot
@@ -491,6 +490,10 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
       auto cycle = [&](int cyc, auto wl) {
         constexpr int LOADS = decltype(wl)::value;
         f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f}, c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (XC) {
+#pragma unroll
+          for (int s = 0; s < STEPS; ++s) xv[s] = x_of_step(xc, s);
+        }
         static_for<0, RING>([&](auto scc) {
           constexpr int st = decltype(scc)::value;
           const f16x8 av = bitcast<f16x8>(xv[st]);
@@ -509,10 +512,12 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           refill_fence();
           if constexpr (LOADS == 1) {
             const int nx = RING * (cyc + 1) + st;
-            xv[st] = load_x_step(P, xr, M, true, k0, nsteps, nx);
+            if constexpr (!XC) xv[st] = load_x_step(P, xr, M, true, k0, nsteps, nx);
+            else if constexpr (st == 0) xc = load_x_cycle(P, xr, M, true, k0, nsteps, cyc + 1);
             load_w_step<true>(P, k0, nsteps, nx, R.w[st]);
           } else {
-            xv[st] = load_x_step(Pn, xrn, M, xn_now, k0n, nstepsn, st);
+            if constexpr (!XC) xv[st] = load_x_step(Pn, xrn, M, xn_now, k0n, nstepsn, st);
+            else if constexpr (st == 0) xc = load_x_cycle(Pn, xrn, M, xn_now, k0n, nstepsn, 0);
             load_w_step<true>(Pn, k0n, nstepsn, st, R.w[st]);
           }
           refill_fence();
@@ -847,21 +852,22 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
 }
 
 std::mutex g_mu;
-int g_grid[64][3];                       // resident workgroups per device and kernel variant
+int g_grid[64][4];                       // resident workgroups per device and kernel variant
 struct PlanInfo {
   const void* plan;
   int w4, M;
   long long jobs_off, unit_off, need_off;
 };
 
-// Kernel variant of a plan: 0 W8, 1 W4, 2 W8 with one activation load per ring cycle
-// (M = 2-4; QLIN_CHAIN_XC=0 turns it off).  Every variant gives the same bits.  At
+// Kernel variant of a plan: 0 W8, 1 W4, 2 W8 and 3 W4 with one activation load per ring
+// cycle (M = 2-4; QLIN_CHAIN_XC=0 turns it off).  Every variant gives the same bits.  At
 // M = 1 the per-step loads have only 4 lanes active anyway, and the permutes' latency
 // at each cycle's start made the one-load form 1 % slower there (measured).
 int chain_variant(const PlanInfo& pi) {
-  if (pi.w4) return 1;
   const char* e = getenv("QLIN_CHAIN_XC");
-  return (pi.M >= 2 && pi.M <= 4 && !(e && strcmp(e, "0") == 0)) ? 2 : 0;
+  const bool xc = pi.M >= 2 && pi.M <= 4 && !(e && strcmp(e, "0") == 0);
+  if (pi.w4) return xc ? 3 : 1;
+  return xc ? 2 : 0;
 }
 std::vector<PlanInfo> g_plans;  // plans initialized in this process
 
@@ -876,6 +882,7 @@ int chain_grid(int variant, int* grid) {
     if (e == hipSuccess) {
       if (variant == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<true, false>, CT, 0);
       else if (variant == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<false, true>, CT, 0);
+      else if (variant == 3) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<true, true>, CT, 0);
       else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<false, false>, CT, 0);
     }
     if (e != hipSuccess || cus <= 0 || per <= 0) return set_error(QLIN_ERR_HIP, "qlin_chain_run: occupancy query failed");
@@ -978,6 +985,7 @@ extern "C" int qlin_chain_run(void* plan, void* stream) {
   const hipStream_t st = (hipStream_t)stream;
   if (variant == 1) hipLaunchKernelGGL((chain_kernel<true, false>), dim3(grid), dim3(CT), 0, st, p, jobs, units, need);
   else if (variant == 2) hipLaunchKernelGGL((chain_kernel<false, true>), dim3(grid), dim3(CT), 0, st, p, jobs, units, need);
+  else if (variant == 3) hipLaunchKernelGGL((chain_kernel<true, true>), dim3(grid), dim3(CT), 0, st, p, jobs, units, need);
   else hipLaunchKernelGGL((chain_kernel<false, false>), dim3(grid), dim3(CT), 0, st, p, jobs, units, need);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -193,24 +193,25 @@ def test_bad_levels_rejected():
         ch.build()
 
 
+@pytest.mark.parametrize("kind", ["w8", "w4"])
 @pytest.mark.parametrize("M", [2, 3, 4])
-def test_w8_one_load_activation_cycles_same_bits(M, monkeypatch):
-    """W8 chains at M = 2-4 load a ring cycle's activations with one load and permute
-    them to the MFMA lanes; QLIN_CHAIN_XC=0 takes one load per step instead.  The same
-    plan gives the same bits both ways: whole-K units (2048 deep), K-split units (6144
-    deep) and a dependent level that reads a level-0 output.  The first output is also
-    checked against the oracle."""
+def test_one_load_activation_cycles_same_bits(kind, M, monkeypatch):
+    """Chains at M = 2-4 load a ring cycle's activations with one load and permute them
+    to the MFMA lanes; QLIN_CHAIN_XC=0 takes one load per step instead.  The same plan
+    gives the same bits both ways, W8 and W4 (the K-split job with explicit zeros):
+    whole-K units (2048 deep), K-split units (6144 deep) and a dependent level that
+    reads a level-0 output.  The first output is also checked against the oracle."""
     shapes = [(2048, 2048), (6144, 2048), (2048, 6144)]
-    ws = [_weights("w8", K, N, 870 + i) for i, (K, N) in enumerate(shapes)]
+    ws = [_weights(kind, K, N, 870 + i, zeros="random" if i == 1 else "none") for i, (K, N) in enumerate(shapes)]
     X = {K: H.act_f16(M, K, seed=875 + K).cuda() for K, _ in shapes}
     outs = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _, N in shapes]
-    w4k, s4k, _ = _weights("w8", 6144, 2048, 879)
+    w4k, s4k, z4k = _weights(kind, 6144, 2048, 879)
     s4k = (s4k.float() / 64).to(torch.float16)
     dep = torch.empty((M, 2048), dtype=torch.float16, device="cuda")
     ch = _chain(M)
-    for (K, N), (w, s, _), o in zip(shapes, ws, outs):
-        ch.add(X[K], _cu(w), _cu(s), o, level=0)
-    ch.add(outs[2], _cu(w4k), _cu(s4k), dep, level=1)
+    for (K, N), (w, s, z), o in zip(shapes, ws, outs):
+        ch.add(X[K], _cu(w), _cu(s), o, zero=_cu(z), level=0)
+    ch.add(outs[2], _cu(w4k), _cu(s4k), dep, zero=_cu(z4k), level=1)
     ch.build()
     res = {}
     for xc in ("1", "0"):
@@ -223,5 +224,7 @@ def test_w8_one_load_activation_cycles_same_bits(M, monkeypatch):
         res[xc] = [o.cpu() for o in outs + [dep]]
     for a, b in zip(res["1"], res["0"]):
         assert torch.equal(a, b)
-    w0, s0, _ = ws[0]
-    H.assert_out_close(res["1"][0], _ref("w8", X[2048].cpu(), w0, s0, None, np.arange(2048)))
+    w0, s0, z0 = ws[0]
+    H.assert_out_close(res["1"][0], _ref(kind, X[2048].cpu(), w0, s0, z0, np.arange(2048)))
+    w1, s1, z1 = ws[1]
+    H.assert_out_close(res["1"][1], _ref(kind, X[6144].cpu(), w1, s1, z1, np.arange(2048)))
