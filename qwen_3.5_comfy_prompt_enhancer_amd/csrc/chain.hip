@@ -530,7 +530,26 @@ __global__ __launch_bounds__(CT) __attribute__((amdgpu_waves_per_eu(3))) void ch
           const u32x4 hi = u32x4{R.sraw[0].z, R.sraw[0].w, 0u, 0u};
           cvt_scale4(hi, J.sdt, sc + 4);
         }
-        if (4 * g < R4) {
+        if constexpr (XC) {
+          // One-load cycles put activation row j & 3 in MFMA row j, so every lane group
+          // holds rows 0-3 (copies, bit for bit): lane group g folds row g, all rows in
+          // one pass, with the same operations as the per-row fold below.
+          if (g < M) {
+            auto pick = [&](const f32x4& v) { return g == 0 ? v[0] : g == 1 ? v[1] : g == 2 ? v[2] : v[3]; };
+            const float c1g = pick(c1), c2g = pick(c2);
+            f32x4* const row = (f32x4*)(slot + g * TNP + j * 8);
+            f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            if (cyc > 0) o[0] = row[0], o[1] = row[1];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const float zt = hz ? (float)((R.zr[t >> 2] >> (8 * (t & 3))) & 0xFFu) : 8.0f;
+              const float d = pick(acc[t]) - fmaf(zt, c2g, c1g);
+              o[t >> 2][t & 3] = fmaf(sc[t], d, o[t >> 2][t & 3]);
+            }
+            row[0] = o[0];
+            row[1] = o[1];
+          }
+        } else if (4 * g < R4) {
           float zf[8];
 #pragma unroll
           for (int t = 0; t < 8; ++t) zf[t] = hz ? (float)((R.zr[t >> 2] >> (8 * (t & 3))) & 0xFFu) : 8.0f;
