@@ -125,16 +125,17 @@ def test_rows_equal_across_M(kind):
         assert torch.equal(res[16][i][:4], res[4][i])
 
 
-def test_graph_replay_matches_eager():
+@pytest.mark.parametrize("kind", ["w8", "w4"])
+def test_graph_replay_matches_eager(kind):
     """run() captured in a HIP graph, replayed three times with eager work in between;
-    every replay equals the eager launch."""
+    every replay equals the eager launch (M = 2: the one-load activation cycles)."""
     M = 2
     ch = _chain(M)
     outs = []
     for i, (K, N) in enumerate([(2048, 2048), (6144, 2048), (2048, 512)]):
-        w, s, _ = _weights("w8", K, N, 850 + i)
+        w, s, z = _weights(kind, K, N, 850 + i, zeros="random" if i == 1 else "none")
         o = torch.empty((M, N), dtype=torch.float16, device="cuda")
-        ch.add(H.act_f16(M, K, seed=855 + i).cuda(), w.cuda(), s.cuda(), o, level=0)
+        ch.add(H.act_f16(M, K, seed=855 + i).cuda(), w.cuda(), s.cuda(), o, zero=_cu(z), level=0)
         outs.append(o)
     ch.build()
     ch.run()
