@@ -131,7 +131,7 @@ class DecodeChain:
             C.check(C.QLIN_ERR_INVALID, "qlin_chain_bytes")
         plan = torch.empty(n, dtype=torch.uint8, device=self.device)
         C.check(L.qlin_chain_init(arr, len(self._jobs), self.M, C.ptr(plan), n,
-                                  torch.cuda.current_stream(self.device).cuda_stream), "qlin_chain_init")
+                                  C.current_stream(self.device)), "qlin_chain_init")
         self.plan = plan
         return self
 
@@ -140,7 +140,7 @@ class DecodeChain:
         if self.plan is None:
             self.build()
         L = C.lib()
-        C.check(L.qlin_chain_run(C.ptr(self.plan), torch.cuda.current_stream(self.device).cuda_stream),
+        C.check(L.qlin_chain_run(C.ptr(self.plan), C.current_stream(self.device)),
                 "qlin_chain_run")
 
     def wait_error(self) -> int:

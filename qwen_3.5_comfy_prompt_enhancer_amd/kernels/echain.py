@@ -244,7 +244,7 @@ class EngineChain:
             C.check(C.QLIN_ERR_INVALID, "qlin_echain_bytes")
         plan = torch.empty(n, dtype=torch.uint8, device=self.device) if self.plan is None else self.plan
         C.check(L.qlin_echain_init(arr, len(self._jobs), self.M, C.ptr(plan), n,
-                                   torch.cuda.current_stream(self.device).cuda_stream), "qlin_echain_init")
+                                   C.current_stream(self.device)), "qlin_echain_init")
         self.plan = plan
         return self
 
@@ -253,7 +253,7 @@ class EngineChain:
         if self.plan is None:
             self.build()
         L = C.lib()
-        C.check(L.qlin_echain_run(C.ptr(self.plan), torch.cuda.current_stream(self.device).cuda_stream),
+        C.check(L.qlin_echain_run(C.ptr(self.plan), C.current_stream(self.device)),
                 "qlin_echain_run")
 
     def wait_error(self) -> int:

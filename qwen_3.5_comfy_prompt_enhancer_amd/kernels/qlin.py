@@ -124,9 +124,26 @@ def dtype_code(t: torch.Tensor) -> int:
         raise ValueError(f"unsupported dtype {t.dtype}") from None
 
 
+# The current stream's raw handle without building a torch Stream object (0.1 us
+# against 2-3 us for torch.cuda.current_stream(), which is most of a call's host time
+# otherwise); the public API where this build of torch lacks the binding.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream(device: torch.device | int) -> int:
+    """The current HIP stream of a device (torch.device or index), as the hipStream_t
+    the C ABI takes."""
+    idx = device if isinstance(device, int) else device.index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    if _raw_stream is not None:
+        return int(_raw_stream(idx))
+    return torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream
+
+
 def stream_of(t: torch.Tensor) -> int:
     """The current HIP stream of `t`'s device, as the hipStream_t the C ABI takes."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return current_stream(t.get_device())
 
 
 def check(status: int, name: str) -> None:
@@ -156,7 +173,7 @@ def workspace(device: torch.device, stream: int | None = None) -> torch.Tensor:
     other or as calls on that stream."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     if stream is None:
-        stream = torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream
+        stream = current_stream(idx)
     key = (idx, int(stream))
     w = _ws.get(key)
     if w is not None:
