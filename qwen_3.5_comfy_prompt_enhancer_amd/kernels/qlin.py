@@ -136,6 +136,8 @@ def current_stream(device: torch.device | int) -> int:
     idx = device if isinstance(device, int) else device.index
     if idx is None:
         idx = torch.cuda.current_device()
+    if idx < 0:
+        raise ValueError("tensors must be on the GPU")
     if _raw_stream is not None:
         return int(_raw_stream(idx))
     return torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream

@@ -145,6 +145,16 @@ def test_shims_validate_before_launch():
         linear.linear_w8(x, b, bs.half(), out.half())
 
 
+def test_stream_of_rejects_host_tensors():
+    """The current-stream lookup (torch's raw-stream binding) refuses a tensor that is
+    not on a GPU instead of handing a host pointer's call a stream."""
+    from qwen35_amd.kernels import qlin
+    with pytest.raises(ValueError, match="GPU"):
+        qlin.stream_of(torch.zeros(4))
+    with pytest.raises(ValueError, match="GPU"):
+        qlin.current_stream(-1)
+
+
 def test_w4_dispatch_follows_weight_dtype():
     """uint8 weights route gemm_i8 / proj3 / mlp_gate_up_quant to the W4 path
     (kernels/gemm.py:15-17): the W4 validator's message proves the route."""
