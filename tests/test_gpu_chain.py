@@ -201,8 +201,9 @@ def test_one_load_activation_cycles_same_bits(kind, M, monkeypatch):
     to the MFMA lanes; QLIN_CHAIN_XC=0 takes one load per step instead.  The same plan
     gives the same bits both ways, W8 and W4 (the K-split job with explicit zeros):
     whole-K units (2048 deep), K-split units (6144 deep) and a dependent level that
-    reads a level-0 output.  The first output is also checked against the oracle."""
-    shapes = [(2048, 2048), (6144, 2048), (2048, 6144)]
+    reads a level-0 output, and a K of 2176 whose last split holds waves with no steps.
+    Three outputs are also checked against the oracle."""
+    shapes = [(2048, 2048), (6144, 2048), (2048, 6144), (2176, 1024)]
     ws = [_weights(kind, K, N, 870 + i, zeros="random" if i == 1 else "none") for i, (K, N) in enumerate(shapes)]
     X = {K: H.act_f16(M, K, seed=875 + K).cuda() for K, _ in shapes}
     outs = [torch.empty((M, N), dtype=torch.float16, device="cuda") for _, N in shapes]
@@ -229,3 +230,5 @@ def test_one_load_activation_cycles_same_bits(kind, M, monkeypatch):
     H.assert_out_close(res["1"][0], _ref(kind, X[2048].cpu(), w0, s0, z0, np.arange(2048)))
     w1, s1, z1 = ws[1]
     H.assert_out_close(res["1"][1], _ref(kind, X[6144].cpu(), w1, s1, z1, np.arange(2048)))
+    w3, s3, z3 = ws[3]
+    H.assert_out_close(res["1"][3], _ref(kind, X[2176].cpu(), w3, s3, z3, np.arange(1024)))
