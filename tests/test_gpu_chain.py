@@ -125,6 +125,29 @@ def test_rows_equal_across_M(kind):
         assert torch.equal(res[16][i][:4], res[4][i])
 
 
+@pytest.mark.parametrize("M", [1, 4])
+def test_w4_explicit_zero_eight_is_identical(M):
+    """A W4 job with an explicit zero tensor of all 8s gives the bits of the same job with
+    none (z = 8 implied), at M = 1 (per-row group fold) and M = 4 (one-load cycles, one
+    row per lane group), whole-K and K-split units."""
+    outs = {}
+    for zeros in ("none", "eight"):
+        ch = _chain(M)
+        res = []
+        for i, (K, N) in enumerate([(2048, 2048), (6144, 1024)]):
+            w, s, z = _weights("w4", K, N, 890 + i, zeros=zeros)
+            o = torch.empty((M, N), dtype=torch.float16, device="cuda")
+            ch.add(H.act_f16(M, K, seed=895 + i).cuda(), w.cuda(), s.cuda(), o, zero=_cu(z), level=0)
+            res.append(o)
+        ch.build()
+        ch.run()
+        torch.cuda.synchronize()
+        assert ch.wait_error() == 0
+        outs[zeros] = [o.cpu() for o in res]
+    for a, b in zip(outs["none"], outs["eight"]):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("kind", ["w8", "w4"])
 def test_graph_replay_matches_eager(kind):
     """run() captured in a HIP graph, replayed three times with eager work in between;

@@ -288,6 +288,31 @@ def test_gemm_w4_prefill_tiled(group, zeros, M, tiled):
     H.assert_out_close(out, ref)
 
 
+@pytest.mark.parametrize("M", [1, 4])
+def test_decode_w4_explicit_zero_eight_is_identical(M):
+    """Engine decode units (1-8 rows): a W4 call with an explicit zero tensor of all 8s
+    gives the bits of the same call with none, for gemm_w4 with a residual (K split over
+    units) and the fused gate/up + quant."""
+    _, w4 = _g()
+    K, N = 2048, 1024
+    a, as_ = H.engine_act(M, K, seed=430 + M)
+    b, bs, _ = _w4_engine(K, N, seed=431)
+    z8 = torch.full((K // 128, N), 8, dtype=torch.uint8, device="cuda")
+    res = torch.randn((M, N), generator=H.gen(432)).to(torch.bfloat16).cuda()
+    o0 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    o1 = torch.empty_like(o0)
+    w4.gemm_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), o0, residual=res)
+    w4.gemm_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), o1, residual=res, b_z=z8)
+    assert torch.equal(o0, o1)
+    bu, bsu, _ = _w4_engine(K, N, seed=433)
+    q0 = torch.empty((M, N), dtype=torch.int8, device="cuda")
+    s0 = torch.empty((M, N // 64), dtype=torch.float32, device="cuda")
+    q1, s1 = torch.empty_like(q0), torch.empty_like(s0)
+    w4.mlp_gate_up_quant_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), bu.cuda(), bsu.cuda(), q0, s0)
+    w4.mlp_gate_up_quant_w4(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), bu.cuda(), bsu.cuda(), q1, s1, zg=z8, zu=z8)
+    assert torch.equal(q0, q1) and torch.equal(s0, s1)
+
+
 def test_prefill_tiled_w4_explicit_zero_eight_is_identical(tiled):
     _, w4 = _g()
     M, K, N = 64, 1024, 1024
