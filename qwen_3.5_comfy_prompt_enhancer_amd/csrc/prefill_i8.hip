@@ -162,35 +162,48 @@ void prefill_i8_kernel(const SkArgs a) {
     uint32_t bs;  // W4: raw dword of one group scale of set tid / 256
     uint32_t bz;  // W4 with zeros: the matching zero
   };
+  // The block of every load below is uniform over a wave (its K group k2 is a function of
+  // the wave), so each address is a per-thread offset fixed for the whole loop plus the
+  // block's offset in a scalar register: buffer loads over the activations, weights and
+  // activation scales (the host keeps each under 2^31 bytes), no per-stage address
+  // arithmetic on the vector ALU.
+  const __amdgpu_buffer_rsrc_t xr = part_rsrc(xq, (unsigned)((long long)M * K));
+  const __amdgpu_buffer_rsrc_t sr = part_rsrc(a.xs, (unsigned)((long long)M * NG * 4));
+  __amdgpu_buffer_rsrc_t wr[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) wr[s] = part_rsrc(wset[s], (unsigned)((long long)(W4 ? K / 2 : K) * n));
+  unsigned xoff[2], woff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = tid + THREADS * i;
+    const int r = (q & 511) >> 2, c = q & 3;
+    xoff[i] = (unsigned)(min(m0 + r, M - 1) * K + 16 * c);
+    const int rw = W4 ? (tid & 255) >> 3 : (q & 511) >> 3, cw = W4 ? tid & 7 : q & 7;
+    woff[i] = (unsigned)(rw * n + ncol0 + 16 * cw);
+  }
+  const unsigned soff = (unsigned)(min(m0 + (tid & 127), M - 1) * NG * 4);
   auto fetch = [&](Regs& rg, int st) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int q = tid + THREADS * i;
-      const int k2 = q >> 9, r = (q & 511) >> 2, c = q & 3;
-      const int blk = kb0 + min(2 * st + k2, nk - 1);
-      const int row = min(m0 + r, M - 1);
-      rg.av[i] = *(const u32x4*)(xq + (long long)row * K + blk * 64 + 16 * c);
+      const int blk = kb0 + min(2 * st + i, nk - 1);  // K group i (q >> 9 = i)
+      rg.av[i] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i], blk * 64, 0));
     }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       if constexpr (W4) {
-        const int k2 = tid >> 8, r = (tid & 255) >> 3, c = tid & 7;
-        const int blk = kb0 + min(2 * st + k2, nk - 1);
-        rg.bv[s][0] = *(const u32x4*)(wset[s] + (long long)(blk * 32 + r) * n + ncol0 + 16 * c);
+        const int blk = kb0 + min(2 * st + (tid >> 8), nk - 1);
+        rg.bv[s][0] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(wr[s], woff[0], blk * 32 * n, 0));
       } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          const int q = tid + THREADS * i;
-          const int k2 = q >> 9, r = (q & 511) >> 3, c = q & 7;
-          const int blk = kb0 + min(2 * st + k2, nk - 1);
-          rg.bv[s][i] = *(const u32x4*)(wset[s] + (long long)(blk * 64 + r) * n + ncol0 + 16 * c);
+          const int blk = kb0 + min(2 * st + i, nk - 1);
+          rg.bv[s][i] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(wr[s], woff[i], blk * 64 * n, 0));
         }
       }
     }
     if (tid < 256) {
-      const int k2 = tid >> 7, r = tid & 127;
-      const int blk = kb0 + min(2 * st + k2, nk - 1);
-      rg.as_ = a.xs[(long long)min(m0 + r, M - 1) * NG + blk];
+      const int blk = kb0 + min(2 * st + (tid >> 7), nk - 1);
+      rg.as_ = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, soff, blk * 4, 0));
     }
     if constexpr (W4) {
       // group scales (and zeros) of both blocks: 256 per set, thread tid takes one of
@@ -683,6 +696,11 @@ static int i8_bn(int wk, int epi, int splits) {
 // (the DMA tile is only forced where it covers the call).
 bool prefill_i8_ok(const SkArgs& a, int wk, int epi) {
   if (a.M <= 16 || a.K % 64 != 0 || ((uintptr_t)a.x & 15) != 0) return false;
+  // the copies address activations, their scales and each weight matrix with buffer
+  // offsets computed in 31 bits
+  if ((long long)a.M * a.K >= (1LL << 31) || (long long)a.M * (a.K / 64) * 4 >= (1LL << 31)) return false;
+  for (int s = 0; s < a.nseg; ++s)
+    if ((long long)a.K * a.seg[s].n >= (1LL << 31)) return false;
   if (wk == WK_W4 && a.group < 64) return false;
   const char* e = getenv("QLIN_I8_DMA");
   const int bn = (e && atoi(e) == 1 && wk == WK_W8 && epi == EPI_STORE) ? 64 : 128;
