@@ -43,7 +43,7 @@ import torch
 from . import qlin as C
 from .fused import Producer, _CProducer
 from .gemm import _check_act, _check_out, _check_quant_out, _check_w8
-from .w4 import _check_w4
+from .w4 import _check_w4, fill_zeros
 
 __all__ = ["EngineChain"]
 
@@ -172,8 +172,11 @@ class EngineChain:
         """proj3 (kernels/gemm.py:290-312, kernels/w4.py:220-251): up to three linears of the
         same activations into column ranges [0, N1), [N1, N1 + N2), [N1 + N2, NT) of `out`.
         One job per projection, all at one level; a producer's codes are kept (q / s)
-        by the first."""
+        by the first.  Zeros given for only some projections follow the reference's
+        fill rule (kernels/w4.py fill_zeros)."""
         K, pro = self._acts(a_q, a_s, pro)
+        z1, z2, z3 = fill_zeros((z1, z2, z3), (s1, s2 if w2 is not None else None, s3 if w3 is not None else None),
+                                next((z for z in (z1, z2, z3) if z is not None), None))
         lvl = self.level if level is None else int(level)
         segs, col, g0 = [], 0, None
         for name, w, s, z in (("w1", w1, s1, z1), ("w2", w2, s2, z2), ("w3", w3, s3, z3)):
@@ -198,14 +201,13 @@ class EngineChain:
                           level=None):
         """h = silu(a @ Wg) * (a @ Wu), rounded through bf16 and requantized per 64 columns
         into out_q int8 [M, N] / out_s fp32 [M, N/64] (kernels/gemm.py:214-231,
-        kernels/w4.py:300-323)."""
+        kernels/w4.py:300-323); one of zg / zu alone stands in for the other (fill_zeros)."""
         K, pro = self._acts(a_q, a_s, pro)
+        zg, zu = fill_zeros((zg, zu), (wsg, wsu), zg if zg is not None else zu)
         N, g = self._weights("wg", wg, wsg, zg, K)
         Nu, gu = self._weights("wu", wu, wsu, zu, K, g if g else None)
         if Nu != N or gu != g or wsg.dtype != wsu.dtype:
             raise ValueError("gate and up must have the same shape, group and scale dtype")
-        if (zg is None) != (zu is None):
-            raise ValueError("zeros for gate and up, or for neither")
         if out_q.shape[0] < self.M or out_s.shape[0] < self.M:
             raise ValueError(f"out_q / out_s need {self.M} rows")
         _check_quant_out(out_q, out_s, out_q.shape[0], N)
@@ -216,14 +218,14 @@ class EngineChain:
         return self
 
     def mlp_gate_up(self, a_q, a_s, wg, wsg, wu, wsu, out, zg=None, zu=None, *, pro=None, level=None):
-        """out[M, N] (bf16) = silu(a @ Wg) * (a @ Wu) (kernels/gemm.py:140-151)."""
+        """out[M, N] (bf16) = silu(a @ Wg) * (a @ Wu) (kernels/gemm.py:140-151); zeros as
+        mlp_gate_up_quant."""
         K, pro = self._acts(a_q, a_s, pro)
+        zg, zu = fill_zeros((zg, zu), (wsg, wsu), zg if zg is not None else zu)
         N, g = self._weights("wg", wg, wsg, zg, K)
         Nu, gu = self._weights("wu", wu, wsu, zu, K, g if g else None)
         if Nu != N or gu != g or wsg.dtype != wsu.dtype:
             raise ValueError("gate and up must have the same shape, group and scale dtype")
-        if (zg is None) != (zu is None):
-            raise ValueError("zeros for gate and up, or for neither")
         _check_out("out", out, self.M, N)
         j = _EJob(kind=QLIN_EJ_GATE_UP, a_q=C.ptr(a_q), a_s=C.ptr(a_s), K=K, N=N, group=g, w=C.ptr(wg),
                   scale=C.ptr(wsg), zero=C.ptr(zg), w2=C.ptr(wu), scale2=C.ptr(wsu), zero2=C.ptr(zu),

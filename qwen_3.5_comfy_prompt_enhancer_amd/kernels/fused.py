@@ -25,7 +25,7 @@ from . import qlin as C
 from .gemm import _check_out, _check_quant_out, _check_w8
 from .norm import (QLIN_PRO_GATE_MUL, QLIN_PRO_NORM_GATED, QLIN_PRO_RMSNORM, check_act16,
                    check_codes)
-from .w4 import _check_w4
+from .w4 import _check_w4, fill_zeros
 
 __all__ = ["Producer", "pro_gemm_i8", "pro_proj3", "pro_mlp_gate_up_quant"]
 
@@ -181,6 +181,8 @@ def pro_proj3(pro: Producer, w1, s1, w2, s2, w3, s3, out, z1=None, z2=None, z3=N
     M, K = pro.rows, pro.cols
     p = pro.c_struct()
     if _is_w4(w1):
+        z1, z2, z3 = fill_zeros((z1, z2, z3), (s1, s2 if w2 is not None else None, s3 if w3 is not None else None),
+                                next((z for z in (z1, z2, z3) if z is not None), None))
         ns, grp = [], None
         for name, w, s, z in (("w1", w1, s1, z1), ("w2", w2, s2, z2), ("w3", w3, s3, z3)):
             if w is None:
@@ -225,6 +227,7 @@ def pro_mlp_gate_up_quant(pro: Producer, wg, wsg, wu, wsu, out_q, out_s, zg=None
     if wsg.dtype != wsu.dtype:
         raise ValueError("gate and up scales must share a dtype")
     if _is_w4(wg):
+        zg, zu = fill_zeros((zg, zu), (wsg, wsu), zg if zg is not None else zu)
         N, grp = _check_w4("wg", wg, wsg, zg, K)
         if _check_w4("wu", wu, wsu, zu, K, grp)[0] != N:
             raise ValueError("gate and up must have the same N")

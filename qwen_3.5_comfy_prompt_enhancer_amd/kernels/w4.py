@@ -59,6 +59,34 @@ def _check_w4(name, w, s, z, K, group=None):
     return N, g
 
 
+def fill_zeros(zs, scales, fill):
+    """The zero tensors a multi-weight call passes on when its weights give zeros only
+    in part: the reference then runs its kernel with zeros for every weight, and a
+    weight without its own reads the memory of `fill` (the first given zero tensor)
+    with its own [K/group, N] strides (kernels/w4.py:235-241 and 309-314 pass `fill`
+    in place of each missing one; _w4_acc indexes it by the weight's row stride,
+    kernels/w4.py:82-83).  `scales[i]` is weight i's scale tensor (its shape is the
+    zero shape), None for an absent weight.  All given or all None: returned as is.
+    A weight whose zero grid needs more elements than `fill` holds is refused (the
+    reference would read past the end of `fill`)."""
+    if fill is None or all(z is not None for z, s in zip(zs, scales) if s is not None):
+        return list(zs)
+    if fill.dtype != torch.uint8:
+        raise ValueError("zeros must be uint8")
+    C.require_contig("zeros", fill)
+    flat = fill.reshape(-1)
+    out = []
+    for z, s in zip(zs, scales):
+        if z is None and s is not None:
+            rows, n = s.shape
+            if flat.numel() < rows * n:
+                raise ValueError(f"the given zeros ({flat.numel()} elements) cannot stand in for a "
+                                 f"missing [{rows}, {n}] zero grid")
+            z = flat[: rows * n].view(rows, n)
+        out.append(z)
+    return out
+
+
 def _check_out(name, t, M, N, dtype=torch.bfloat16):
     if t.dtype != dtype:
         raise ValueError(f"{name} must be {dtype}")
@@ -87,8 +115,11 @@ def gemm_w4(a_q, a_s, b, b_s, out, residual=None, b_z=None, block_m=None, block_
 
 def proj3_w4(a_q, a_s, w1, s1, w2, s2, w3, s3, out, z1=None, z2=None, z3=None, block_k=64):
     """Three W4 projections sharing one activation tile; per-projection group zeros
-    (kernels/w4.py:220-251)."""
+    (kernels/w4.py:220-251).  Zeros given for only some projections follow the
+    reference's fill rule (fill_zeros)."""
     M, K = _check_act(a_q, a_s)
+    z1, z2, z3 = fill_zeros((z1, z2, z3), (s1, s2 if w2 is not None else None, s3 if w3 is not None else None),
+                            next((z for z in (z1, z2, z3) if z is not None), None))
     ns = []
     group = None
     for name, w, s, z in (("w1", w1, s1, z1), ("w2", w2, s2, z2), ("w3", w3, s3, z3)):
@@ -125,7 +156,9 @@ def _gate_up_common(a_q, a_s, wg, sg, wu, su, zg, zu):
 
 def mlp_gate_up_quant_w4(a_q, a_s, wg, sg, wu, su, out_q, out_s, zg=None, zu=None, block_k=64):
     """W4 gate/up fusion + per-64 int8 quantization; `zg`/`zu` optional per-group
-    zeros ([K//WGRP, N]) (kernels/w4.py:300-323).  Returns (out_q, out_s)."""
+    zeros ([K//WGRP, N]) (kernels/w4.py:300-323); one of them alone stands in for
+    the other (fill_zeros).  Returns (out_q, out_s)."""
+    zg, zu = fill_zeros((zg, zu), (sg, su), zg if zg is not None else zu)
     M, K, N, group = _gate_up_common(a_q, a_s, wg, sg, wu, su, zg, zu)
     if N % GROUP != 0:
         raise ValueError(f"N={N} must be a multiple of {GROUP}")
@@ -146,7 +179,9 @@ def mlp_gate_up_quant_w4(a_q, a_s, wg, sg, wu, su, out_q, out_s, zg=None, zu=Non
 def mlp_gate_up_w4(a_q, a_s, wg, sg, wu, su, out, zg=None, zu=None):
     """bf16 silu(gate) * up with W4 weights.  The reference's `mlp_gate_up`
     (kernels/gemm.py:140-151) is W8 only; this W4 form lets the fused quant epilogue
-    be checked against the unfused composition (.dev/test_fused.py:22-46)."""
+    be checked against the unfused composition (.dev/test_fused.py:22-46).  Zeros
+    as mlp_gate_up_quant_w4."""
+    zg, zu = fill_zeros((zg, zu), (sg, su), zg if zg is not None else zu)
     M, K, N, group = _gate_up_common(a_q, a_s, wg, sg, wu, su, zg, zu)
     if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N):
         raise ValueError(f"out must be bf16 [{M}, {N}]")
