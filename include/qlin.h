@@ -22,6 +22,14 @@
  *         group, not packed); the weight value is (nibble - z), z = 8 when absent.
  *   engine activations: int8 a_q[M][K] (row stride K) with fp32 a_s[M][K/64].
  * All matrices are row-major; `ld*` arguments are row strides in elements.
+ *
+ * Engine-signature entry points take any N and pointers aligned to their element
+ * size only, as the reference's masked kernels do (kernels/gemm.py:50-57).  Their fast
+ * kernels need N % 16 == 0 (per projection), 16-byte aligned weights, scales, zeros,
+ * outputs and residuals, 16-bit row strides that are multiples of 8, and 8-byte
+ * aligned a_q; a call outside those rules runs on a generic kernel (same arithmetic
+ * per block, one K split; correct, not fast).  The A16 entry points (qlin_linear_*)
+ * and the chains keep the fast rules and refuse other layouts.
  */
 #ifndef QLIN_H
 #define QLIN_H

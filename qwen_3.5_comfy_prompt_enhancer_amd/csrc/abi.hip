@@ -479,9 +479,69 @@ int check_weight(const char* fn, const void* w, const void* s, const uint8_t* z,
 int check_engine_act(const char* fn, const int8_t* a_q, const float* a_s, int M, int K) {
   if (M > 0 && (!a_q || !a_s)) return fail(QLIN_ERR_INVALID, "%s: null activations", fn);
   if (K % 64 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 64", fn, K);
-  if (!aligned(a_q, 8) || !aligned(a_s, 4))
-    return fail(QLIN_ERR_UNSUPPORTED, "%s: activations must be 8-byte aligned", fn);
+  if (!aligned(a_s, 4)) return fail(QLIN_ERR_UNSUPPORTED, "%s: a_s must be 4-byte aligned", fn);
   return QLIN_OK;
+}
+
+// Engine-signature calls take any N and pointers aligned to their element size only
+// (the reference's kernels mask every edge, kernels/gemm.py:50-57).  The fast kernels
+// need N % 16 == 0, 16-byte aligned weights, scales, zeros and 16-bit rows (row
+// strides multiples of 8) and 8-byte aligned codes; a valid call outside those rules
+// runs on the edge kernel (edge.hip).
+int check_engine_weight(const char* fn, const void* w, const void* s, int n, int sdt) {
+  if (n == 0) return QLIN_OK;
+  if (!w || !s) return fail(QLIN_ERR_INVALID, "%s: null weight or scale", fn);
+  if (!aligned(s, sdt == QLIN_F32 ? 4 : 2))
+    return fail(QLIN_ERR_UNSUPPORTED, "%s: scales must be aligned to their element size", fn);
+  return QLIN_OK;
+}
+
+bool engine_weight_fast(const void* w, const void* s, const uint8_t* z, int n) {
+  return n == 0 || (n % 16 == 0 && aligned(w, 16) && aligned(s, 16) && (!z || aligned(z, 16)));
+}
+
+int check_engine_out(const char* fn, const void* p, int64_t ld, int N, const char* what) {
+  if (!p) return fail(QLIN_ERR_INVALID, "%s: null %s", fn, what);
+  if (ld < N) return fail(QLIN_ERR_INVALID, "%s: %s row stride %lld < N=%d", fn, what, (long long)ld, N);
+  if (!aligned(p, 2)) return fail(QLIN_ERR_UNSUPPORTED, "%s: %s must be 2-byte aligned", fn, what);
+  return QLIN_OK;
+}
+
+bool engine_out_fast(const void* p, int64_t ld) { return aligned(p, 16) && ld % 8 == 0; }
+
+// A call on the edge kernel; a producer first runs as a launch of its own into the
+// codes setup_pro chose.
+int engine_edge(const char* fn, int wk, int epi, const int8_t* a_q, const float* a_s, int M, int K, const Seg* segs,
+                int nseg, int ncols, int group, int sdt, void* out, int64_t ldo, const void* res, int64_t ldr,
+                int8_t* oq, float* os, const ProArgs* pa, hipStream_t st) {
+  if (pa && pa->kind != PRO_NONE) {
+    ProArgs p = *pa;
+    p.q = p.tq;
+    p.s = p.ts;
+    QL_TRY(hip_status(fn, launch_producer(p, M, K, st)));
+    a_q = p.tq;
+    a_s = p.ts;
+  }
+  EdgeArgs e;
+  memset(&e, 0, sizeof(e));
+  e.x = a_q;
+  e.xs = a_s;
+  e.M = M;
+  e.K = K;
+  for (int i = 0; i < nseg; ++i) e.seg[i] = segs[i];
+  e.nseg = nseg;
+  e.ncols = ncols;
+  e.group = (wk == WK_W4) ? group : 64;
+  e.sdt = sdt;
+  e.epi = epi;
+  e.odt = QLIN_BF16;
+  e.out = out;
+  e.ldo = ldo;
+  e.res = res;
+  e.ldr = ldr;
+  e.oq = oq;
+  e.os = os;
+  return hip_status(fn, launch_edge(e, wk, st));
 }
 
 // Validates an activation producer (kernels/norm.py:28-57, 95-137, 168-188) for M rows
@@ -605,9 +665,15 @@ int engine_gemm(const char* fn, int wk, const int8_t* a_q, const float* a_s, int
   }
   if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
   if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
-  QL_TRY(check_weight(fn, b, b_s, b_z, N, wk));
-  QL_TRY(check_out16(fn, out, ldo, N, "out"));
-  if (residual) QL_TRY(check_out16(fn, residual, ldr, N, "residual"));
+  QL_TRY(check_engine_weight(fn, b, b_s, N, bs_dtype));
+  QL_TRY(check_engine_out(fn, out, ldo, N, "out"));
+  if (residual) QL_TRY(check_engine_out(fn, residual, ldr, N, "residual"));
+  if (!engine_weight_fast(b, b_s, b_z, N) || !engine_out_fast(out, ldo) ||
+      (residual && !engine_out_fast(residual, ldr)) || (!pro && !aligned(a_q, 8))) {
+    const Seg s0 = make_seg(b, b_s, b_z, N, 0);
+    return engine_edge(fn, wk, EPI_STORE, a_q, a_s, M, K, &s0, 1, N, group, bs_dtype, out, ldo, residual, ldr,
+                       nullptr, nullptr, pro ? &pa : nullptr, (hipStream_t)stream);
+  }
   SkArgs a = base_args();
   a.x = a_q;
   a.xs = a_s;
@@ -646,13 +712,29 @@ int engine_proj3(const char* fn, int wk, const int8_t* a_q, const float* a_s, in
   }
   if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
   if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
-  QL_TRY(check_weight(fn, w1, s1, z1, n1, wk));
-  QL_TRY(check_weight(fn, w2, s2, z2, n2, wk));
-  QL_TRY(check_weight(fn, w3, s3, z3, n3, wk));
-  QL_TRY(check_out16(fn, out, ldo, NT, "out"));
+  QL_TRY(check_engine_weight(fn, w1, s1, n1, bs_dtype));
+  QL_TRY(check_engine_weight(fn, w2, s2, n2, bs_dtype));
+  QL_TRY(check_engine_weight(fn, w3, s3, n3, bs_dtype));
+  QL_TRY(check_engine_out(fn, out, ldo, NT, "out"));
   const bool hz = (z1 || z2 || z3);
   if (hz && ((n1 && !z1) || (n2 && !z2) || (n3 && !z3)))
     return fail(QLIN_ERR_INVALID, "%s: zeros must be given for every projection or for none", fn);
+  if (!engine_weight_fast(w1, s1, z1, n1) || !engine_weight_fast(w2, s2, z2, n2) ||
+      !engine_weight_fast(w3, s3, z3, n3) || !engine_out_fast(out, ldo) || (!pro && !aligned(a_q, 8))) {
+    Seg sg[3];
+    int ns = 0, col = 0;
+    const void* wv[3] = {w1, w2, w3};
+    const void* sv[3] = {s1, s2, s3};
+    const uint8_t* zv[3] = {z1, z2, z3};
+    const int nv[3] = {n1, n2, n3};
+    for (int i = 0; i < 3; ++i) {
+      if (nv[i] == 0) continue;
+      sg[ns++] = make_seg(wv[i], sv[i], zv[i], nv[i], col);
+      col += nv[i];
+    }
+    return engine_edge(fn, wk, EPI_STORE, a_q, a_s, M, K, sg, ns, NT, group, bs_dtype, out, ldo, nullptr, 0,
+                       nullptr, nullptr, pro ? &pa : nullptr, (hipStream_t)stream);
+  }
   SkArgs a = base_args();
   a.x = a_q;
   a.xs = a_s;
@@ -695,17 +777,24 @@ int engine_gate_up(const char* fn, int wk, int epi, const int8_t* a_q, const flo
   }
   if (!dtype_scale_ok(bs_dtype)) return fail(QLIN_ERR_UNSUPPORTED, "%s: scale dtype %d", fn, bs_dtype);
   if (wk == WK_W4) QL_TRY(check_group(fn, group, K));
-  QL_TRY(check_weight(fn, wg, sg, zg, N, wk));
-  QL_TRY(check_weight(fn, wu, su, zu, N, wk));
+  QL_TRY(check_engine_weight(fn, wg, sg, N, bs_dtype));
+  QL_TRY(check_engine_weight(fn, wu, su, N, bs_dtype));
   if ((zg == nullptr) != (zu == nullptr))
     return fail(QLIN_ERR_INVALID, "%s: zeros must be given for both gate and up or for neither", fn);
+  bool fast = engine_weight_fast(wg, sg, zg, N) && engine_weight_fast(wu, su, zu, N) && (pro || aligned(a_q, 8));
   if (epi == EPI_GATEUP) {
-    QL_TRY(check_out16(fn, out, N, N, "out"));
+    QL_TRY(check_engine_out(fn, out, N, N, "out"));
+    fast = fast && engine_out_fast(out, N);
   } else {
     if (N % 64 != 0) return fail(QLIN_ERR_UNSUPPORTED, "%s: N=%d is not a multiple of 64", fn, N);
     if (!out_q || !out_s) return fail(QLIN_ERR_INVALID, "%s: null out_q/out_s", fn);
-    if (!aligned(out_q, 16) || !aligned(out_s, 4))
-      return fail(QLIN_ERR_UNSUPPORTED, "%s: out_q must be 16-byte aligned", fn);
+    if (!aligned(out_s, 4)) return fail(QLIN_ERR_UNSUPPORTED, "%s: out_s must be 4-byte aligned", fn);
+    fast = fast && aligned(out_q, 16);
+  }
+  if (!fast) {
+    const Seg sgs[2] = {make_seg(wg, sg, zg, N, 0), make_seg(wu, su, zu, N, 0)};
+    return engine_edge(fn, wk, epi, a_q, a_s, M, K, sgs, 2, N, group, bs_dtype, out, N, nullptr, 0, out_q, out_s,
+                       pro ? &pa : nullptr, (hipStream_t)stream);
   }
   SkArgs a = base_args();
   a.x = a_q;

@@ -99,6 +99,29 @@ hipError_t launch_skinny_i8w4(const SkLaunch& L, const SkArgs& a, hipStream_t st
 // == 0, W4 groups of at least 64, every column range a multiple of 128), and its launch.
 bool prefill_i8_ok(const SkArgs& a, int wk, int epi);
 hipError_t launch_prefill_i8(SkArgs a, int wk, bool hz, int epi, hipStream_t stream);
+
+// Engine-signature call outside the fast kernels' layout rules (edge.hip): any N,
+// pointers aligned to their element size only.  Segments, epilogue and element types
+// as SkArgs.
+struct EdgeArgs {
+  const int8_t* x;     // int8 codes [M][K]
+  const float* xs;     // fp32 scales [M][K/64]
+  int M, K;
+  Seg seg[3];          // EPI_STORE: column segments; gate/up: seg[0] = gate, seg[1] = up
+  int nseg;
+  int ncols;
+  int group;           // W4 weight group
+  int sdt;             // weight-scale element type (DT_*)
+  int epi;             // EpiKind
+  int odt;             // 16-bit output (and residual) element type
+  void* out;
+  long long ldo;
+  const void* res;
+  long long ldr;
+  int8_t* oq;          // EPI_GATEUP_Q codes [M][ncols]
+  float* os;           // EPI_GATEUP_Q scales [M][ncols/64]
+};
+hipError_t launch_edge(const EdgeArgs& a, int wk, hipStream_t st);
 // whether a skinny variant runs with up to 8 waves per workgroup (else 4)
 bool skinny_big(int act, int wk, int epi, int cols);
 

@@ -77,14 +77,24 @@ def test_bad_k_rejected():
     assert b"K=96" in L.qlin_last_error()
 
 
-def test_bad_n_and_alignment_rejected():
+def test_element_misalignment_rejected():
+    """Any N and any 16-byte misalignment are valid engine calls (they run on the edge
+    kernel); a pointer off its own element size, or a row stride below N, is refused
+    before any launch."""
     qlin, L = _lib()
-    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 128, FAKE, FAKE, qlin.QLIN_F32, 40, FAKE, I64(40), None, I64(0),
+    odd = ctypes.c_void_p(0x10001)
+    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 128, FAKE, odd, qlin.QLIN_F32, 40, FAKE, I64(40), None, I64(0),
                         None, SZ(0), None)
-    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"N=40" in L.qlin_last_error()
-    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 128, ctypes.c_void_p(0x10001), FAKE, qlin.QLIN_F32, 64, FAKE,
-                        I64(64), None, I64(0), None, SZ(0), None)
-    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"aligned" in L.qlin_last_error()
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"scales must be aligned" in L.qlin_last_error()
+    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 128, FAKE, FAKE, qlin.QLIN_F32, 40, odd, I64(40), None, I64(0),
+                        None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"out must be 2-byte aligned" in L.qlin_last_error()
+    rc = L.qlin_gemm_i8(FAKE, odd, 1, 128, FAKE, FAKE, qlin.QLIN_F32, 40, FAKE, I64(40), None, I64(0),
+                        None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_UNSUPPORTED and b"a_s must be 4-byte aligned" in L.qlin_last_error()
+    rc = L.qlin_gemm_i8(FAKE, FAKE, 1, 128, FAKE, FAKE, qlin.QLIN_F32, 40, FAKE, I64(39), None, I64(0),
+                        None, SZ(0), None)
+    assert rc == qlin.QLIN_ERR_INVALID and b"row stride" in L.qlin_last_error()
 
 
 def test_bad_group_rejected():

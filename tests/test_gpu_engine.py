@@ -237,11 +237,6 @@ def test_bad_arguments_raise_before_launch():
     out = torch.empty((2, 64), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError):
         gemm.gemm_i8(a.cuda(), as_[:, :1].contiguous().cuda(), b.cuda(), bs.cuda(), out)
-    a, as_ = H.engine_act(2, 128, seed=1)
-    b, bs = H.engine_w8(128, 40, seed=2)          # N not a multiple of 16
-    out = torch.empty((2, 40), dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(ValueError):
-        gemm.gemm_i8(a.cuda(), as_.cuda(), b.cuda(), bs.cuda(), out)
 
 
 # ---------------------------------------------------------------- prefill-sized M (tiled int8 kernel)
