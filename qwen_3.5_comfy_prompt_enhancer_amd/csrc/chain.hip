@@ -66,10 +66,16 @@ constexpr int kSpinLimit = 1 << 22;        // polls of a dependency before givin
 constexpr int kWaitVm0 = 0x0F70;           // s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima)
 // Levels whose units at the shortest length outnumber the workgroups that fit the chip
 // this many times over (kPlanSlots: 3 workgroups on each of 256 CUs) take longer units
-// -- up to a tile's whole K -- streamed through the same register ring: fewer split-K
-// exchanges, the same parallelism.
+// -- up to kMaxR shortest units or a tile's whole K -- streamed through the same
+// register ring: fewer split-K exchanges, the same parallelism.
 constexpr int kPlanSlots = 768;
 constexpr int kLongFactor = 2;
+// Longest unit: 4 x KU = 2048 K rows.  With a tile's whole K allowed (down's 6144 in
+// units of 5120 and 1024, lin_out's 4096 in one) the flat decode sweep's units differ
+// in length and the last round of workgroups ends unevenly; uniform 2048-row units
+// are faster (W8 180-181 vs 182.3-182.6 us per launch, W4 107-112 vs 111-113 us,
+// alternated three times).
+constexpr int kMaxR = 4;
 
 // Device descriptor of one job.
 struct alignas(16) ChainJob {
@@ -750,7 +756,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Unit length: each wave of a unit folds RING steps of 32 K rows (the shortest unit, KU
 // = 512 rows per unit) or, for levels with many units, a multiple of that streamed
 // through the ring: r = (the level's shortest units) / (kLongFactor * kPlanSlots), at
-// most a tile's whole K.  Within a level, jobs are laid out longest unit first, so the
+// most kMaxR (2048 rows) and a tile's whole K.  Within a level, jobs are laid out longest unit first, so the
 // queues hand out the long units early and the short ones fill the end.
 int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::vector<ChainJob>* jobs_out,
                  std::vector<int>* unit_job, std::vector<unsigned>* need) {
@@ -801,7 +807,7 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
   for (int i = 0; i < njobs; ++i) {
     const qlin_chain_job& q = jobs[i];
     const long long lr = level_units[q.level] / ((long long)kLongFactor * kPlanSlots);
-    const int r = (int)std::max<long long>(1, std::min<long long>(lr, (q.K + KU - 1) / KU));
+    const int r = (int)std::max<long long>(1, std::min<long long>(std::min<long long>(lr, kMaxR), (q.K + KU - 1) / KU));
     wsteps[i] = RING * r;
     order[i] = i;
   }
