@@ -15,7 +15,8 @@
 //     take units from 8 queues (workgroup b from queue b % 8; queue q hands out units
 //     q, q + 8, ... in order; the next index is fetched while the current unit runs),
 //     so a unit only ever waits for units of lower levels, all taken before it: every
-//     wait ends whether or not all workgroups are resident.
+//     wait ends whether or not all workgroups are resident.  Within a level the units
+//     go round robin over its jobs (every job's first unit, then every job's second).
 //   * A unit's weight (and scale, zero) loads are in flight before it waits: above
 //     level 0 it waits for the level below (one thread polls the level's done flag with
 //     a bounded spin), then reads its activations with device-coherent loads (level 0:
@@ -76,6 +77,9 @@ constexpr int kLongFactor = 2;
 // are faster (W8 180-181 vs 182.3-182.6 us per launch, W4 107-112 vs 111-113 us,
 // alternated three times).
 constexpr int kMaxR = 4;
+// A unit-table entry holds its job (low kJobBits bits) and its index within the job.
+constexpr int kJobBits = 12;
+constexpr int kMaxJobs = 1 << kJobBits;
 
 // Device descriptor of one job.
 struct alignas(16) ChainJob {
@@ -152,9 +156,9 @@ struct UnitPos {
 __device__ __forceinline__ UnitPos decode_unit(const ChainJob* __restrict__ jobs, const int* __restrict__ unit_job,
                                                int u) {
   UnitPos p;
-  const int jn = __builtin_amdgcn_readfirstlane(unit_job[u]);
-  p.J = jobs[jn];
-  const int local = u - p.J.unit0;
+  const int e = (int)__builtin_amdgcn_readfirstlane((uint32_t)unit_job[u]);
+  p.J = jobs[e & (kMaxJobs - 1)];
+  const int local = e >> kJobBits;
   p.tile = local / p.J.splits;
   p.split = local - p.tile * p.J.splits;
   return p;
@@ -761,6 +765,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::vector<ChainJob>* jobs_out,
                  std::vector<int>* unit_job, std::vector<unsigned>* need) {
   if (!jobs || njobs <= 0) return set_error(QLIN_ERR_INVALID, "qlin_chain: no jobs");
+  if (njobs > kMaxJobs) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: %d jobs (at most %d)", njobs, kMaxJobs);
   if (M < 1 || M > 16) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: M=%d (1-16 rows)", M);
   int prev_level = 0;
   const bool w4_chain = jobs[0].group != 0;
@@ -817,6 +822,7 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
     return unit_rows(a) > unit_rows(b);
   });
   long long units = 0, ncnt = 0, parts = 0;
+  std::vector<int> job_units;
   for (int oi = 0; oi < njobs; ++oi) {
     const int i = order[oi];
     const qlin_chain_job& q = jobs[i];
@@ -850,7 +856,9 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
       d.index = i;
       d.wsteps = wsteps[i];
       jobs_out->push_back(d);
-      for (long long t = 0; t < (long long)ntiles * splits; ++t) unit_job->push_back(oi);
+      job_units.push_back((int)((long long)ntiles * splits));
+      if ((long long)ntiles * splits >= (1LL << (31 - kJobBits)))
+        return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: job %d has too many work units", i);
       if ((int)need->size() <= q.level) need->resize(q.level + 1, 0u);
       (*need)[q.level] += (unsigned)ntiles;  // tiles of the level
     }
@@ -860,6 +868,30 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
       parts += (long long)ntiles * splits * M * TNC;
     }
     if (units > (1LL << 30)) return fail_chain(QLIN_ERR_UNSUPPORTED, "qlin_chain: too many work units (job %d)", i);
+  }
+  if (jobs_out) {
+    // The unit order within a level: round robin over its jobs by unit index (the
+    // first unit of every job, then the second, ...), so the units in flight at any
+    // time read the same tiles of many matrices rather than neighbouring tiles of one
+    // (QLIN_CHAIN_ORDER=0: each job's units together).
+    const char* eo = getenv("QLIN_CHAIN_ORDER");
+    const bool rr = !(eo && strcmp(eo, "0") == 0);
+    int first = 0;
+    while (first < njobs) {
+      int last = first;
+      while (last < njobs && jobs[order[last]].level == jobs[order[first]].level) ++last;
+      if (rr) {
+        int most = 0;
+        for (int oi = first; oi < last; ++oi) most = std::max(most, job_units[oi]);
+        for (int r = 0; r < most; ++r)
+          for (int oi = first; oi < last; ++oi)
+            if (r < job_units[oi]) unit_job->push_back(oi | (r << kJobBits));
+      } else {
+        for (int oi = first; oi < last; ++oi)
+          for (int r = 0; r < job_units[oi]; ++r) unit_job->push_back(oi | (r << kJobBits));
+      }
+      first = last;
+    }
   }
   L->nunits = (int)units;
   L->nlevels = nlevels;
