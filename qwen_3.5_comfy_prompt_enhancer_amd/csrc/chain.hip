@@ -909,10 +909,10 @@ int layout_chain(const qlin_chain_job* jobs, int njobs, int M, Layout* L, std::v
 }
 
 std::mutex g_mu;
-int g_grid[64][4];                       // resident workgroups per device and kernel variant
+int g_grid[64][4][2];                    // per device, kernel variant and grid form (below): workgroups
 struct PlanInfo {
   const void* plan;
-  int w4, M;
+  int w4, M, nlevels;
   long long jobs_off, unit_off, need_off;
 };
 
@@ -928,12 +928,20 @@ int chain_variant(const PlanInfo& pi) {
 }
 std::vector<PlanInfo> g_plans;  // plans initialized in this process
 
-int chain_grid(int variant, int* grid) {
+// Workgroups of a launch: every workgroup that fits (3 per CU), except for W8 chains of
+// one level (the decode sweep), which take 2 per CU.  A launch's third workgroup per
+// CU starts its first unit 15-40 us late (the CU issues the older waves' loads first),
+// and a launch of one level ends when its slowest workgroup finishes its last unit:
+// with 2 per CU each workgroup streams faster and the last units end sooner (W8 sweep
+// 178.1-178.2 vs 180.4-182.0 us per launch).  W4 units carry half the bytes and run
+// best with 3 per CU (106-108 vs 113-115 us), as do W8 chains with dependency levels
+// (2168 vs 2088 GB/s).
+int chain_grid(int variant, bool two_per_cu, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= 64) return set_error(QLIN_ERR_HIP, "qlin_chain_run: hipGetDevice failed");
   std::lock_guard<std::mutex> lk(g_mu);
-  if (g_grid[dev][variant] == 0) {
+  if (g_grid[dev][variant][two_per_cu] == 0) {
     int cus = 0, per = 0;
     e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e == hipSuccess) {
@@ -943,9 +951,9 @@ int chain_grid(int variant, int* grid) {
       else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, chain_kernel<false, false>, CT, 0);
     }
     if (e != hipSuccess || cus <= 0 || per <= 0) return set_error(QLIN_ERR_HIP, "qlin_chain_run: occupancy query failed");
-    g_grid[dev][variant] = cus * per;
+    g_grid[dev][variant][two_per_cu] = cus * (two_per_cu ? std::min(per, 2) : per);
   }
-  *grid = g_grid[dev][variant];
+  *grid = g_grid[dev][variant][two_per_cu];
   return QLIN_OK;
 }
 
@@ -1020,7 +1028,7 @@ extern "C" int qlin_chain_init(const qlin_chain_job* jobs, int njobs, int M, voi
     snprintf(msg, sizeof(msg), "qlin_chain_init: copy: HIP error %d (%s)", (int)e, hipGetErrorString(e));
     return set_error(QLIN_ERR_HIP, msg);
   }
-  remember_plan(PlanInfo{plan, L.w4, M, L.jobs_off, L.unit_off, L.need_off});
+  remember_plan(PlanInfo{plan, L.w4, M, L.nlevels, L.jobs_off, L.unit_off, L.need_off});
   return QLIN_OK;
 }
 
@@ -1033,7 +1041,7 @@ extern "C" int qlin_chain_run(void* plan, void* stream) {
     return set_error(QLIN_ERR_INVALID, "qlin_chain_run: plan not initialized by qlin_chain_init in this process");
   int grid = 0;
   const int variant = chain_variant(pi);
-  const int rc = chain_grid(variant, &grid);
+  const int rc = chain_grid(variant, !pi.w4 && pi.nlevels == 1, &grid);
   if (rc != QLIN_OK) return rc;
   uint8_t* const p = (uint8_t*)plan;
   const ChainJob* jobs = (const ChainJob*)(p + pi.jobs_off);
