@@ -265,20 +265,32 @@ def decode_sweep(args, kind, shapes, head, ms, layers, reuse=None):
     return total, step, head_ev, head_bytes, record, (lw, hw, xs, outs, hout, lin, None)
 
 
-def time_steps(step, steps, warmup, record=None):
+def time_steps(step, steps, warmup, record=None, span=None):
+    """Seconds per step over `steps` timed steps after `warmup` untimed ones.  With
+    `record`, the step records its per-launch events while timed; with `span` (a dict),
+    one HIP event pair on the current stream brackets the timed steps and span["ms"]
+    receives its elapsed time (no event inside the region)."""
     import torch
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     if record is not None:
         record["on"] = True
+    if span is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    if span is not None:
+        e0.record()
     for _ in range(steps):
         step()
+    if span is not None:
+        e1.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     if record is not None:
         record["on"] = False
+    if span is not None:
+        span["ms"] = e0.elapsed_time(e1)
     return (t1 - t0) / steps
 
 
@@ -954,12 +966,24 @@ def main() -> int:
         if wl == "single":
             args.launch = "graph"
         total, step, head_ev, head_bytes, record, ctx = decode_sweep(args, kind, shapes, head, ms, layers)
-        t = time_steps(step, args.steps, args.warmup, record)
+        if args.launch == "chain":
+            # the step is nothing but the chain launches (one per M): the timed steps hold
+            # no event but one pair bracketing them (an event recorded between launches
+            # costs the step 8-11 us per launch, measured), and the chain's average launch
+            # period -- the bracket over the launches, gaps between launches included, so
+            # at least the kernel's duration -- prices the roofline
+            span = {}
+            t = time_steps(step, args.steps, args.warmup, None, span)
+            period = span["ms"] * 1e-3 / (args.steps * len(ms))
+            durs = [(M, period) for M in ms]
+            # per-M launch times for the log: a short pass with events around each launch
+            time_steps(step, 5, 0, record)
+        else:
+            t = time_steps(step, args.steps, args.warmup, record)
+            # the vocabulary-head GEMV, every launch of the timed steps timed live with HIP
+            # events on its launch stream
+            durs = [(M, e0.elapsed_time(e1) * 1e-3) for M in ms for (e0, e1) in head_ev[M]]
         value = total / t / 1e9
-        # dominant kernel, every launch of the timed steps timed live with HIP events on
-        # its launch stream: the chain kernel (one launch per M: the whole step's
-        # linears), or with per-GEMV launches the vocabulary-head GEMV
-        durs = [(M, e0.elapsed_time(e1) * 1e-3) for M in ms for (e0, e1) in head_ev[M]]
         dur = sum(d for _, d in durs) / len(durs)
         hb = sum(head_bytes[M] for M, _ in durs) / len(durs)
         achieved = hb / dur / 1e9
@@ -979,6 +1003,12 @@ def main() -> int:
         if args.detail and args.launch != "chain":
             detail_table(ctx, kind, shapes, head, ms)
         per_m = {M: sum(e0.elapsed_time(e1) for e0, e1 in head_ev[M]) / len(head_ev[M]) for M in ms}
+        if args.launch == "chain":
+            roof["timing"] = ("average launch period: one HIP event pair bracketing the timed steps, "
+                              "divided by the launches in them (gaps between launches included)")
+            roof["event_us_by_M"] = {str(M): round(v * 1e3, 1) for M, v in per_m.items()}
+        else:
+            roof["timing"] = "HIP events around every launch of the kernel in the timed steps"
         log(("chain" if args.launch == "chain" else "vocab head") + " per-launch us by M: " +
             ", ".join(f"M={M}: {v * 1e3:.1f} ({head_bytes[M] / v / 1e6:.0f} GB/s)" for M, v in per_m.items()))
         other = None
@@ -1001,7 +1031,7 @@ def main() -> int:
             main_levels = args.levels
             args.levels = "flat" if main_levels == "layer" else "layer"
             tot2, step2, ev2, sb2, rec2, ctx2 = decode_sweep(args, kind, shapes, head, ms, layers, reuse=ctx)
-            t2 = time_steps(step2, max(3, args.steps // 2), 2, rec2)
+            t2 = time_steps(step2, max(3, args.steps // 2), 2)
             other = {"levels": args.levels, "GB_per_s": round(tot2 / t2 / 1e9, 1),
                      "ms_per_step": round(t2 * 1e3, 4)}
             log(f"same step with {args.levels} levels: {tot2 / t2 / 1e9:.0f} GB/s")
