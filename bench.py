@@ -966,12 +966,14 @@ def main() -> int:
         if wl == "single":
             args.launch = "graph"
         total, step, head_ev, head_bytes, record, ctx = decode_sweep(args, kind, shapes, head, ms, layers)
-        if args.launch == "chain":
+        period_timing = args.launch == "chain" and args.head == "chain"
+        if period_timing:
             # the step is nothing but the chain launches (one per M): the timed steps hold
             # no event but one pair bracketing them (an event recorded between launches
             # costs the step 8-11 us per launch, measured), and the chain's average launch
             # period -- the bracket over the launches, gaps between launches included, so
-            # at least the kernel's duration -- prices the roofline
+            # at least the kernel's duration -- prices the roofline.  (With the vocab head
+            # as its own launch after each chain, events around each chain launch do.)
             span = {}
             t = time_steps(step, args.steps, args.warmup, None, span)
             period = span["ms"] * 1e-3 / (args.steps * len(ms))
@@ -980,8 +982,9 @@ def main() -> int:
             time_steps(step, 5, 0, record)
         else:
             t = time_steps(step, args.steps, args.warmup, record)
-            # the vocabulary-head GEMV, every launch of the timed steps timed live with HIP
-            # events on its launch stream
+            # the dominant kernel (with per-GEMV launches the vocabulary-head GEMV; with a
+            # chain followed by the head's own launch the chain), every launch of the
+            # timed steps timed live with HIP events on its launch stream
             durs = [(M, e0.elapsed_time(e1) * 1e-3) for M in ms for (e0, e1) in head_ev[M]]
         value = total / t / 1e9
         dur = sum(d for _, d in durs) / len(durs)
@@ -1003,7 +1006,7 @@ def main() -> int:
         if args.detail and args.launch != "chain":
             detail_table(ctx, kind, shapes, head, ms)
         per_m = {M: sum(e0.elapsed_time(e1) for e0, e1 in head_ev[M]) / len(head_ev[M]) for M in ms}
-        if args.launch == "chain":
+        if period_timing:
             roof["timing"] = ("average launch period: one HIP event pair bracketing the timed steps, "
                               "divided by the launches in them (gaps between launches included)")
             roof["event_us_by_M"] = {str(M): round(v * 1e3, 1) for M, v in per_m.items()}
