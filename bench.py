@@ -656,8 +656,8 @@ def torch_dequant(kind, w, s):
 
 
 def cpu_baseline(kind, shapes, head, budget_s=30.0):
-    """The reference's CPU path on the decode workload at M = 1 (BASELINE's CPU
-    plan): for every layer shape and the whole vocabulary head, dequantize the
+    """The reference's CPU path on the decode workload at M = 1 (dequantize, then an
+    fp32 matmul): for every layer shape and the whole vocabulary head, dequantize the
     weight to fp32 with torch, then torch.matmul in fp32, on the host's cores
     (torch.set_num_threads).  Dequantization and matmul are timed separately, each
     the median of 10 runs after 2 warm-ups; GB/s over the same algorithmic bytes as
