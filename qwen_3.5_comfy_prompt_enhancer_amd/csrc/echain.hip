@@ -80,7 +80,8 @@ constexpr int kSpinLimit = 1 << 22;  // polls of a dependency before giving up
 constexpr int kWaitVm0 = 0x0F70;     // s_waitcnt vmcnt(0)
 constexpr int kQueues = 64;             // unit queues, one counter per 128-byte line
 constexpr int kLevel0 = 32 * (kQueues + 1);
-constexpr int kPlanSlots = 768;      // resident workgroups the unit plan assumes (3 per CU x 256 CUs)
+constexpr int kPlanSlots = 768;      // workgroups the unit plan is sized for (3 per CU x 256 CUs; a fixed
+                                     // constant, so a job's K order never depends on the launch)
 constexpr int kLongFactor = 2;
 constexpr int kEPre = 4;             // producer: row chunks a lane loads ahead (all of a 2048-wide row)
 
@@ -1030,6 +1031,10 @@ namespace {
 std::mutex g_emu;
 int g_egrid[64][2];
 
+// Workgroups of an engine-chain launch: 2 per CU, though 3 fit.  A chain's levels wait
+// on one another, and with fewer workgroups per CU each unit's K loop, sum and exchange
+// run sooner: W8 47.1-47.4 vs 49.0-49.1 us per layer at M = 4 (44.7 vs 44.8 at M = 1),
+// W4 43.9-44.0 vs 45.4-45.6 at M = 1 and 47.9 vs 51.3-51.6 at M = 4 (alternated twice).
 int egrid(bool w4, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -1042,7 +1047,7 @@ int egrid(bool w4, int* grid) {
       e = w4 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, echain_kernel<true>, ET, 0)
              : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, echain_kernel<false>, ET, 0);
     if (e != hipSuccess || cus <= 0 || per <= 0) return set_error(QLIN_ERR_HIP, "qlin_echain_run: occupancy query failed");
-    g_egrid[dev][w4] = cus * per;
+    g_egrid[dev][w4] = cus * std::min(per, 2);
   }
   *grid = g_egrid[dev][w4];
   return QLIN_OK;
