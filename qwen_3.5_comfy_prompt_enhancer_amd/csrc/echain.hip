@@ -1035,6 +1035,7 @@ int g_egrid[64][2];
 // on one another, and with fewer workgroups per CU each unit's K loop, sum and exchange
 // run sooner: W8 47.1-47.4 vs 49.0-49.1 us per layer at M = 4 (44.7 vs 44.8 at M = 1),
 // W4 43.9-44.0 vs 45.4-45.6 at M = 1 and 47.9 vs 51.3-51.6 at M = 4 (alternated twice).
+// One per CU leaves too few units in flight on the wide levels: W8 64.6 / 69.4 us.
 int egrid(bool w4, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
