@@ -935,7 +935,8 @@ std::vector<PlanInfo> g_plans;  // plans initialized in this process
 // with 2 per CU each workgroup streams faster and the last units end sooner (W8 sweep
 // 178.1-178.2 vs 180.4-182.0 us per launch).  W4 units carry half the bytes and run
 // best with 3 per CU (106-108 vs 113-115 us), as do W8 chains with dependency levels
-// (2168 vs 2088 GB/s).
+// (2168 vs 2088 GB/s) and W4 ones (a 9B-class 32-layer chain 1553 vs 1909 us per launch;
+// the 2B-class W4 step with layer levels 338-340 vs 366-367 us).
 int chain_grid(int variant, bool two_per_cu, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
